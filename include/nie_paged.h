@@ -1,0 +1,208 @@
+/*
+ * nie_paged.h — C ABI of the MI355X (gfx950) paged-attention library
+ * (libnie_hip.so).
+ *
+ * The reference engine (ito-integral/nano-infer-engine) does this work with
+ * PyTorch ATen ops called from Python loops.  Each entry point below replaces
+ * one of those loops; the comment on each names the reference code it
+ * replaces.  Paths are relative to the reference repository root.
+ *
+ * Conventions shared by every entry point
+ *  - All data pointers are device pointers unless a comment says "host".
+ *  - KV cache layout is the reference's storage layout, row-major
+ *        keys/values : (num_layers, num_blocks, block_size, kv_heads, head_dim)
+ *    (src/nano_infer_engine/paged_cache.py:71-79).  Offsets are computed in
+ *    64-bit arithmetic, so pools larger than 2^31 elements are fine.
+ *  - A "slot" is phys_block * block_size + offset_in_block
+ *    (src/nano_infer_engine/paged_cache.py:240-262).
+ *  - dtype is NIE_DTYPE_F32 or NIE_DTYPE_BF16; everything in one call shares it.
+ *  - head_dim must be 64 or 128; q_heads must be a multiple of kv_heads with
+ *    q_heads / kv_heads in {1, 2, 4, 8, 16}.  block_size may be any positive
+ *    value.
+ *  - Block IDs read from block tables are clamped into [0, num_blocks) on the
+ *    device, so a bad table cannot address memory outside the pool; callers
+ *    validate tables on the host (the Python layer does).
+ *  - Every call is asynchronous on `stream` (a hipStream_t; NULL = default
+ *    stream).  The library never allocates or frees device memory: scratch
+ *    space is the caller's `workspace`, sized by the *_workspace_bytes query.
+ *  - Return value: NIE_OK, or a negative NIE_E* code; nie_last_error() then
+ *    holds a message for the calling thread.
+ */
+#ifndef NIE_PAGED_H
+#define NIE_PAGED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NIE_OK 0
+#define NIE_EINVAL (-1)       /* bad argument (null pointer, bad size, bad workspace) */
+#define NIE_EUNSUPPORTED (-2) /* dtype / head_dim / GQA group size not built */
+#define NIE_ELAUNCH (-3)      /* HIP reported an error at launch */
+
+#define NIE_DTYPE_F32 0
+#define NIE_DTYPE_BF16 1
+
+/* Library version string, e.g. "nie_paged 0.1 gfx950". */
+const char* nie_version(void);
+
+/* Message describing the last failed call made by this thread. */
+const char* nie_last_error(void);
+
+/*
+ * KV append: scatter-writes the K and V rows of num_tokens new tokens into
+ * one layer of the cache.  Token t goes to slot_mapping[t]; a negative slot
+ * is skipped (padding), as is any slot >= num_blocks * block_size.
+ *   k_new/v_new : (num_tokens, kv_heads, head_dim); token t starts at element
+ *                 t * k_row_stride (resp. v_row_stride); heads and dims are
+ *                 contiguous.
+ * Bit-exact copy.
+ * Replaces: the per-token copy loop of PagedKVCache.write
+ *           (src/nano_infer_engine/paged_cache.py:264-322), called once per
+ *           sequence by GroupedQueryAttention.forward
+ *           (src/nano_infer_engine/layers/attention.py:246-253) and
+ *           forward_ragged (attention.py:384-390).
+ */
+int nie_kv_append(int dtype,
+                  const void* k_new, int64_t k_row_stride,
+                  const void* v_new, int64_t v_row_stride,
+                  const int64_t* slot_mapping, int64_t num_tokens,
+                  void* k_cache, void* v_cache,
+                  int64_t num_layers, int64_t layer_index,
+                  int64_t num_blocks, int64_t block_size,
+                  int64_t kv_heads, int64_t head_dim,
+                  void* stream);
+
+/*
+ * KV gather: copies logical positions 0..token_count-1 of one sequence
+ * (physical block table `block_table`, num_table_entries entries) into
+ * contiguous (token_count, kv_heads, head_dim) tensors.  Bit-exact.
+ * Replaces: the per-token gather loop + torch.stack of PagedKVCache.gather
+ *           (src/nano_infer_engine/paged_cache.py:324-362).
+ */
+int nie_kv_gather(int dtype,
+                  const void* k_cache, const void* v_cache,
+                  int64_t num_layers, int64_t layer_index,
+                  int64_t num_blocks, int64_t block_size,
+                  int64_t kv_heads, int64_t head_dim,
+                  const int32_t* block_table, int64_t num_table_entries,
+                  int64_t token_count,
+                  void* k_out, void* v_out,
+                  void* stream);
+
+/*
+ * Block copy between two caches of identical (num_layers, block_size,
+ * kv_heads, head_dim) geometry: for i < count, every layer of block
+ * src_blocks[i] of the source pool is copied to block dst_blocks[i] of the
+ * destination pool (both K and V).  Either side may instead be a packed
+ * staging buffer of shape (num_layers, count, block_size, kv_heads, head_dim)
+ * by passing a NULL block list for that side.  Bit-exact.
+ * Replaces: the per-block torch.stack of PagedKVCache.export_sequence and the
+ *           per-block copy_ of import_sequence
+ *           (src/nano_infer_engine/paged_cache.py:145-238).
+ */
+int nie_kv_copy_blocks(int dtype,
+                       const void* src_k, const void* src_v,
+                       int64_t src_num_blocks, const int32_t* src_blocks,
+                       void* dst_k, void* dst_v,
+                       int64_t dst_num_blocks, const int32_t* dst_blocks,
+                       int64_t count,
+                       int64_t num_layers, int64_t block_size,
+                       int64_t kv_heads, int64_t head_dim,
+                       void* stream);
+
+/*
+ * Workspace bytes needed by nie_paged_decode for a batch whose sequence
+ * lengths have maximum max_seq_len and sum total_seq_len (host values).
+ */
+int64_t nie_paged_decode_workspace_bytes(int64_t batch, int64_t q_heads,
+                                         int64_t head_dim, int64_t block_size,
+                                         int64_t max_seq_len,
+                                         int64_t total_seq_len);
+
+/*
+ * Paged decode attention: one query token per sequence attends to the first
+ * seq_lens[b] cached tokens of its sequence (no causal mask needed: the
+ * current token is already cached).  GQA: query head h reads KV head
+ * h / (q_heads / kv_heads).
+ *   q     : (batch, q_heads, head_dim), element (b, h, d) at
+ *           b * q_stride_b + h * q_stride_h + d.
+ *   out   : same indexing with out_stride_b / out_stride_h.
+ *   block_tables : (batch, table_stride) int32, row b = physical blocks of
+ *           sequence b in logical order.
+ *   seq_lens     : (batch,) int32 device copy of the lengths, each >= 1.
+ *   max_seq_len / total_seq_len : host copies of max and sum of seq_lens;
+ *           they size the launch and must be exact.
+ * Numerics follow the reference: the q.k score is rounded to the storage
+ * dtype and scaled in that dtype, softmax runs in fp32, P.V accumulates in
+ * fp32 and the result is rounded to the storage dtype.
+ * Replaces: paged_attention_reference / batched_paged_attention_reference
+ *           (src/nano_infer_engine/layers/paged_attention.py:4-176), called
+ *           from GroupedQueryAttention.forward
+ *           (src/nano_infer_engine/layers/attention.py:255-269), and the
+ *           length-1 rows of forward_ragged (attention.py:380-412).
+ */
+int nie_paged_decode(int dtype,
+                     const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache,
+                     int64_t num_layers, int64_t layer_index,
+                     int64_t num_blocks, int64_t block_size,
+                     int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                     const int32_t* block_tables, int64_t table_stride,
+                     const int32_t* seq_lens, int64_t batch,
+                     int64_t max_seq_len, int64_t total_seq_len,
+                     float scale,
+                     void* out, int64_t out_stride_b, int64_t out_stride_h,
+                     void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Workspace bytes needed by nie_varlen_prefill (host values: number of
+ * sequences, total and maximum query length, maximum context+query length).
+ */
+int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query_tokens,
+                                           int64_t max_query_len, int64_t max_seq_len,
+                                           int64_t q_heads, int64_t kv_heads,
+                                           int64_t head_dim);
+
+/*
+ * Varlen (chunked-prefill) attention over the paged cache.  Sequence r owns
+ * packed query rows cu_seqlens_q[r] .. cu_seqlens_q[r+1]-1; row i of it sits
+ * at absolute position context_lens[r] + i and attends to cached positions
+ * 0 .. that position (causal inside the chunk, full attention to the prior
+ * context).  The chunk's own K/V must already be in the cache.
+ *   q   : (total_query_tokens, q_heads, head_dim), element (t, h, d) at
+ *         t * q_stride_t + h * q_stride_h + d;  out likewise.
+ *   cu_seqlens_q : (num_seqs + 1,) int64, cu_seqlens_q[0] == 0.
+ *   context_lens : (num_seqs,) int32.
+ *   total_query_tokens, max_query_len, max_seq_len: host values sizing the
+ *         launch; they must be exact (max_seq_len = max of context + query).
+ * Numerics as nie_paged_decode.
+ * Replaces: the per-request write/gather/repeat_interleave/matmul/mask/
+ *           softmax/matmul loop of GroupedQueryAttention.forward_ragged
+ *           (src/nano_infer_engine/layers/attention.py:378-414) and the dense
+ *           attention of the non-chunked paged prefill
+ *           (src/nano_infer_engine/models/llama.py:274-325).
+ */
+int nie_varlen_prefill(int dtype,
+                       const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                       const int64_t* cu_seqlens_q, const int32_t* context_lens,
+                       int64_t num_seqs, int64_t total_query_tokens,
+                       int64_t max_query_len, int64_t max_seq_len,
+                       const void* k_cache, const void* v_cache,
+                       int64_t num_layers, int64_t layer_index,
+                       int64_t num_blocks, int64_t block_size,
+                       int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                       const int32_t* block_tables, int64_t table_stride,
+                       float scale,
+                       void* out, int64_t out_stride_t, int64_t out_stride_h,
+                       void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NIE_PAGED_H */

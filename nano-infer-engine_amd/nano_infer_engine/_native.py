@@ -1,0 +1,414 @@
+"""ctypes binding of ``libnie_hip.so``, the gfx950 paged-attention library.
+
+Every function here takes torch tensors that live on a ROCm device, checks
+them, and calls one C entry point declared in ``include/nie_paged.h`` on the
+current HIP stream of that device.  There is no CPU path: a tensor on
+another device, or a missing library, raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIBRARY_NAME = "libnie_hip.so"
+
+NIE_DTYPE_F32 = 0
+NIE_DTYPE_BF16 = 1
+
+_DTYPE_CODES = {torch.float32: NIE_DTYPE_F32, torch.bfloat16: NIE_DTYPE_BF16}
+
+#: Head dims and GQA group sizes the attention kernels are built for.
+SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_GROUP_SIZES = (1, 2, 4, 8, 16)
+
+#: Every symbol the library exports (checked by the CPU test suite).
+EXPORTED_SYMBOLS = (
+    "nie_version",
+    "nie_last_error",
+    "nie_kv_append",
+    "nie_kv_gather",
+    "nie_kv_copy_blocks",
+    "nie_paged_decode_workspace_bytes",
+    "nie_paged_decode",
+    "nie_varlen_prefill_workspace_bytes",
+    "nie_varlen_prefill",
+)
+
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_ptr = ctypes.c_void_p
+_f32 = ctypes.c_float
+
+_SIGNATURES = {
+    "nie_version": (ctypes.c_char_p, []),
+    "nie_last_error": (ctypes.c_char_p, []),
+    "nie_kv_append": (
+        _i32,
+        [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr],
+    ),
+    "nie_kv_gather": (
+        _i32,
+        [_i32, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr],
+    ),
+    "nie_kv_copy_blocks": (
+        _i32,
+        [_i32, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr],
+    ),
+    "nie_paged_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "nie_paged_decode": (
+        _i32,
+        [
+            _i32, _ptr, _i64, _i64,          # dtype, q, q strides
+            _ptr, _ptr,                      # caches
+            _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
+            _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
+            _ptr, _i64,                      # block tables, stride
+            _ptr, _i64, _i64, _i64,          # seq_lens, batch, max, total
+            _f32,                            # scale
+            _ptr, _i64, _i64,                # out, strides
+            _ptr, _i64, _ptr,                # workspace, bytes, stream
+        ],
+    ),
+    "nie_varlen_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "nie_varlen_prefill": (
+        _i32,
+        [
+            _i32, _ptr, _i64, _i64,          # dtype, q, q strides
+            _ptr, _ptr, _i64, _i64,          # cu_seqlens, context_lens, num_seqs, total_q
+            _i64, _i64,                      # max_q, max_seq
+            _ptr, _ptr,                      # caches
+            _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
+            _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
+            _ptr, _i64,                      # block tables, stride
+            _f32,                            # scale
+            _ptr, _i64, _i64,                # out, strides
+            _ptr, _i64, _ptr,                # workspace, bytes, stream
+        ],
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+_lib_lock = threading.Lock()
+
+
+def library_path() -> str:
+    """Path of the in-tree built library."""
+    override = os.environ.get("NIE_HIP_LIBRARY")
+    if override:
+        return override
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
+
+
+def load_library() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is None:
+            path = library_path()
+            if not os.path.exists(path):
+                raise RuntimeError(
+                    f"HIP paged-attention library not found at {path}; "
+                    "build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+                )
+            lib = ctypes.CDLL(path)
+            for name, (restype, argtypes) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _lib = lib
+    return _lib
+
+
+def version() -> str:
+    return load_library().nie_version().decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        message = load_library().nie_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {message}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise RuntimeError(f"HIP kernels support float32 and bfloat16, not {dtype}") from None
+
+
+def _require_gpu(*tensors: torch.Tensor) -> None:
+    for tensor in tensors:
+        if tensor.device.type != "cuda":
+            raise RuntimeError(
+                "paged KV operations run on a ROCm GPU through the HIP library; "
+                f"got a tensor on {tensor.device}"
+            )
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _cache_dims(k_cache: torch.Tensor) -> tuple[int, int, int, int, int]:
+    if k_cache.ndim != 5:
+        raise ValueError("key_cache and value_cache must be 5D tensors")
+    if not k_cache.is_contiguous():
+        raise ValueError("KV cache storage must be contiguous")
+    return tuple(k_cache.shape)  # type: ignore[return-value]
+
+
+def _check_cache_pair(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, int, int, int]:
+    _require_gpu(k_cache, v_cache)
+    dims = _cache_dims(k_cache)
+    if v_cache.shape != k_cache.shape or not v_cache.is_contiguous():
+        raise ValueError("key_cache and value_cache must have identical contiguous shapes")
+    if v_cache.dtype != k_cache.dtype or v_cache.device != k_cache.device:
+        raise ValueError("key_cache and value_cache must share dtype and device")
+    return dims
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself if its storage pointer is 16-byte aligned, else an aligned copy."""
+    if t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
+def _rows_view_ok(t: torch.Tensor, kv_heads: int, head_dim: int) -> bool:
+    return t.ndim == 3 and t.shape[1:] == (kv_heads, head_dim) and t.stride(2) == 1 and t.stride(1) == head_dim
+
+
+def kv_append(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    layer_index: int,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Write token t of ``keys``/``values`` (T, Hkv, D) to slot ``slot_mapping[t]``."""
+    num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+    _require_gpu(keys, values, slot_mapping)
+    if keys.dtype != k_cache.dtype or values.dtype != k_cache.dtype:
+        raise ValueError("keys and values must match the cache dtype")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.ndim != 1 or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be a contiguous 1D int64 tensor")
+    if keys.shape != values.shape or keys.shape[0] != slot_mapping.shape[0]:
+        raise ValueError("keys, values and slot_mapping must describe the same tokens")
+    if not _rows_view_ok(keys, kv_heads, head_dim):
+        keys = keys.contiguous()
+    if not _rows_view_ok(values, kv_heads, head_dim):
+        values = values.contiguous()
+    lib = load_library()
+    rc = lib.nie_kv_append(
+        dtype_code(k_cache.dtype),
+        keys.data_ptr(), keys.stride(0),
+        values.data_ptr(), values.stride(0),
+        slot_mapping.data_ptr(), slot_mapping.shape[0],
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim,
+        _stream(k_cache.device),
+    )
+    _check(rc, "nie_kv_append")
+
+
+def kv_gather(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    layer_index: int,
+    block_table: torch.Tensor,
+    token_count: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Contiguous (token_count, Hkv, D) copies of logical positions 0..token_count-1."""
+    num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+    _require_gpu(block_table)
+    if block_table.dtype != torch.int32 or block_table.ndim != 1 or not block_table.is_contiguous():
+        raise ValueError("block_table must be a contiguous 1D int32 tensor")
+    k_out = torch.empty((token_count, kv_heads, head_dim), dtype=k_cache.dtype, device=k_cache.device)
+    v_out = torch.empty_like(k_out)
+    rc = load_library().nie_kv_gather(
+        dtype_code(k_cache.dtype),
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim,
+        block_table.data_ptr(), block_table.shape[0], token_count,
+        k_out.data_ptr(), v_out.data_ptr(),
+        _stream(k_cache.device),
+    )
+    _check(rc, "nie_kv_gather")
+    return k_out, v_out
+
+
+def kv_copy_blocks(
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    src_blocks: torch.Tensor | None,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    dst_blocks: torch.Tensor | None,
+    count: int,
+) -> None:
+    """Copy ``count`` whole blocks (all layers, K and V).
+
+    A side whose block list is ``None`` is a packed staging tensor of shape
+    (L, count, BS, Hkv, D); otherwise it is a pool indexed by the list.
+    """
+    _require_gpu(src_k, src_v, dst_k, dst_v)
+    for t in (src_k, src_v, dst_k, dst_v):
+        if t.ndim != 5 or not t.is_contiguous():
+            raise ValueError("block copies need contiguous 5D K/V tensors")
+    if src_k.shape[0] != dst_k.shape[0] or src_k.shape[2:] != dst_k.shape[2:]:
+        raise ValueError("source and destination layouts differ")
+    if src_k.dtype != dst_k.dtype:
+        raise ValueError("source and destination dtypes differ")
+    for blocks in (src_blocks, dst_blocks):
+        if blocks is not None:
+            _require_gpu(blocks)
+            if blocks.dtype != torch.int32 or blocks.ndim != 1 or blocks.shape[0] < count:
+                raise ValueError("block lists must be 1D int32 tensors with `count` entries")
+    num_layers, _, block_size, kv_heads, head_dim = src_k.shape
+    rc = load_library().nie_kv_copy_blocks(
+        dtype_code(src_k.dtype),
+        src_k.data_ptr(), src_v.data_ptr(), src_k.shape[1],
+        None if src_blocks is None else src_blocks.data_ptr(),
+        dst_k.data_ptr(), dst_v.data_ptr(), dst_k.shape[1],
+        None if dst_blocks is None else dst_blocks.data_ptr(),
+        count, num_layers, block_size, kv_heads, head_dim,
+        _stream(src_k.device),
+    )
+    _check(rc, "nie_kv_copy_blocks")
+
+
+def _check_attention_shapes(q_heads: int, kv_heads: int, head_dim: int) -> None:
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise RuntimeError(f"HIP attention supports head_dim in {SUPPORTED_HEAD_DIMS}, not {head_dim}")
+    if q_heads % kv_heads != 0 or q_heads // kv_heads not in SUPPORTED_GROUP_SIZES:
+        raise RuntimeError(
+            f"HIP attention supports GQA group sizes {SUPPORTED_GROUP_SIZES}; got {q_heads}/{kv_heads}"
+        )
+
+
+def paged_decode(
+    query: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    layer_index: int,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    max_seq_len: int,
+    total_seq_len: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Decode attention of query (B, Hq, D) over each sequence's first seq_lens[b] tokens.
+
+    ``block_tables`` (B, W) int32 and ``seq_lens`` (B,) int32 are device
+    tensors; ``max_seq_len`` and ``total_seq_len`` are their host-side max
+    and sum (they size the launch and must be exact).
+    """
+    num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+    _require_gpu(query, block_tables, seq_lens)
+    if query.ndim != 3 or query.shape[2] != head_dim or query.stride(2) != 1:
+        raise ValueError("query must be (batch, q_heads, head_dim) with unit stride on head_dim")
+    if query.dtype != k_cache.dtype:
+        raise ValueError("query and K/V caches must have the same dtype")
+    query = _aligned(query)
+    batch, q_heads, _ = query.shape
+    _check_attention_shapes(q_heads, kv_heads, head_dim)
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != batch:
+        raise ValueError("block_tables must be an int32 (batch, max_blocks) tensor")
+    if not block_tables.is_contiguous():
+        block_tables = block_tables.contiguous()
+    if seq_lens.dtype != torch.int32 or seq_lens.shape != (batch,) or not seq_lens.is_contiguous():
+        raise ValueError("seq_lens must be a contiguous int32 (batch,) tensor")
+    if out is None:
+        out = torch.empty((batch, q_heads, head_dim), dtype=query.dtype, device=query.device)
+    if batch == 0:
+        return out
+    lib = load_library()
+    ws_bytes = lib.nie_paged_decode_workspace_bytes(batch, q_heads, head_dim, block_size, max_seq_len, total_seq_len)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    rc = lib.nie_paged_decode(
+        dtype_code(query.dtype),
+        query.data_ptr(), query.stride(0), query.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        num_layers, layer_index, num_blocks, block_size,
+        q_heads, kv_heads, head_dim,
+        block_tables.data_ptr(), block_tables.shape[1],
+        seq_lens.data_ptr(), batch, max_seq_len, total_seq_len,
+        float(scale),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        workspace.data_ptr(), workspace.numel(),
+        _stream(query.device),
+    )
+    _check(rc, "nie_paged_decode")
+    return out
+
+
+def varlen_prefill(
+    query: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    context_lens: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    layer_index: int,
+    block_tables: torch.Tensor,
+    max_query_len: int,
+    max_seq_len: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal varlen attention of packed query rows (ΣT, Hq, D) over the paged cache.
+
+    Sequence r owns rows cu_seqlens[r]..cu_seqlens[r+1]-1 at absolute
+    positions context_lens[r] + i.  ``max_query_len`` and ``max_seq_len``
+    (max of context + query) are exact host-side values.
+    """
+    num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+    _require_gpu(query, cu_seqlens, context_lens, block_tables)
+    if query.ndim != 3 or query.shape[2] != head_dim or query.stride(2) != 1:
+        raise ValueError("query must be (tokens, q_heads, head_dim) with unit stride on head_dim")
+    if query.dtype != k_cache.dtype:
+        raise ValueError("query and K/V caches must have the same dtype")
+    query = _aligned(query)
+    total_tokens, q_heads, _ = query.shape
+    _check_attention_shapes(q_heads, kv_heads, head_dim)
+    num_seqs = context_lens.shape[0]
+    if cu_seqlens.dtype != torch.int64 or cu_seqlens.shape != (num_seqs + 1,) or not cu_seqlens.is_contiguous():
+        raise ValueError("cu_seqlens must be a contiguous int64 (num_seqs + 1,) tensor")
+    if context_lens.dtype != torch.int32 or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be a contiguous int32 tensor")
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != num_seqs:
+        raise ValueError("block_tables must be an int32 (num_seqs, max_blocks) tensor")
+    if not block_tables.is_contiguous():
+        block_tables = block_tables.contiguous()
+    if out is None:
+        out = torch.empty((total_tokens, q_heads, head_dim), dtype=query.dtype, device=query.device)
+    if total_tokens == 0 or num_seqs == 0:
+        return out
+    lib = load_library()
+    ws_bytes = lib.nie_varlen_prefill_workspace_bytes(
+        num_seqs, total_tokens, max_query_len, max_seq_len, q_heads, kv_heads, head_dim
+    )
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    rc = lib.nie_varlen_prefill(
+        dtype_code(query.dtype),
+        query.data_ptr(), query.stride(0), query.stride(1),
+        cu_seqlens.data_ptr(), context_lens.data_ptr(), num_seqs, total_tokens,
+        max_query_len, max_seq_len,
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        num_layers, layer_index, num_blocks, block_size,
+        q_heads, kv_heads, head_dim,
+        block_tables.data_ptr(), block_tables.shape[1],
+        float(scale),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        workspace.data_ptr(), workspace.numel(),
+        _stream(query.device),
+    )
+    _check(rc, "nie_varlen_prefill")
+    return out

@@ -1,0 +1,163 @@
+"""Per-forward device metadata of a ragged paged batch, and the attention core.
+
+The reference engine re-derives block tables, positions and slots inside
+every layer from Python tuples (``layers/attention.py:210-261``,
+``:363-394``) and moves K/V one token at a time.  Here a forward builds one
+:class:`RaggedBatch` (two host-to-device copies) that all layers share:
+
+* ``slot_mapping`` — flat cache slot of every new token (for ``kv_append``),
+* ``block_tables`` / ``context_lens`` / ``seq_lens`` / ``cu_seqlens`` — what
+  the decode and varlen-prefill kernels read,
+* ``positions`` — absolute RoPE position of every new token.
+
+:func:`paged_attention` is the per-layer attention core: one ``kv_append``
+launch, then ``paged_decode`` for requests with a single new token and
+``varlen_prefill`` for the rest.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from nano_infer_engine import _native
+from nano_infer_engine.paged_cache import PagedKVCache
+
+
+@dataclass
+class RaggedBatch:
+    sequence_ids: tuple[str, ...]
+    query_lens: tuple[int, ...]
+    context_lens: tuple[int, ...]
+    num_tokens: int
+    # device tensors
+    block_tables: torch.Tensor  # (R, W) int32
+    context_lens_t: torch.Tensor  # (R,) int32
+    seq_lens_t: torch.Tensor  # (R,) int32, context + query
+    cu_seqlens: torch.Tensor  # (R + 1,) int64
+    slot_mapping: torch.Tensor  # (num_tokens,) int64
+    positions: torch.Tensor  # (num_tokens,) int64
+    # host-side launch geometry
+    decode_from: int  # requests [decode_from, R) have one new token each (a contiguous tail)
+
+    @property
+    def num_requests(self) -> int:
+        return len(self.sequence_ids)
+
+
+def build_ragged_batch(
+    cache: PagedKVCache,
+    sequence_ids: tuple[str, ...],
+    query_lens: tuple[int, ...],
+    context_lens: tuple[int, ...] | None = None,
+) -> RaggedBatch:
+    """Metadata for appending ``query_lens[r]`` tokens to each sequence.
+
+    Capacity must already be allocated (``ensure_capacity``).  Context lengths
+    default to the cached lengths.
+    """
+    if context_lens is None:
+        context_lens = tuple(cache.get_sequence_length(s) for s in sequence_ids)
+    bs = cache.block_size
+    for sequence_id, ctx, q in zip(sequence_ids, context_lens, query_lens):
+        # every new token must already be backed by a block (same error as a write)
+        cache._resolve_position(sequence_id, ctx + q - 1)
+    tables = [cache._table(s) for s in sequence_ids]
+    width = max(1, max(len(t) for t in tables))
+    num_requests = len(sequence_ids)
+    num_tokens = int(sum(query_lens))
+
+    ints = np.zeros(num_requests * width + 2 * num_requests, dtype=np.int32)
+    table_view = ints[: num_requests * width].reshape(num_requests, width)
+    longs = np.empty(2 * num_tokens + num_requests + 1, dtype=np.int64)
+    slots = longs[:num_tokens]
+    positions = longs[num_tokens : 2 * num_tokens]
+    cu = longs[2 * num_tokens :]
+    cu[0] = 0
+    cursor = 0
+    for r, (table, ctx, q) in enumerate(zip(tables, context_lens, query_lens)):
+        table_view[r, : len(table)] = table
+        pos = np.arange(ctx, ctx + q, dtype=np.int64)
+        positions[cursor : cursor + q] = pos
+        slots[cursor : cursor + q] = table_view[r, pos // bs].astype(np.int64) * bs + pos % bs
+        cursor += q
+        cu[r + 1] = cursor
+    ints[num_requests * width : num_requests * width + num_requests] = context_lens
+    ints[num_requests * width + num_requests :] = np.asarray(context_lens) + np.asarray(query_lens)
+
+    device = cache.keys.device
+    ints_t = torch.from_numpy(ints).to(device, non_blocking=True)
+    longs_t = torch.from_numpy(longs).to(device, non_blocking=True)
+
+    decode_from = num_requests
+    while decode_from > 0 and query_lens[decode_from - 1] == 1:
+        decode_from -= 1
+
+    return RaggedBatch(
+        sequence_ids=tuple(sequence_ids),
+        query_lens=tuple(query_lens),
+        context_lens=tuple(context_lens),
+        num_tokens=num_tokens,
+        block_tables=ints_t[: num_requests * width].view(num_requests, width),
+        context_lens_t=ints_t[num_requests * width : num_requests * width + num_requests],
+        seq_lens_t=ints_t[num_requests * width + num_requests :],
+        cu_seqlens=longs_t[2 * num_tokens :],
+        slot_mapping=longs_t[:num_tokens],
+        positions=longs_t[num_tokens : 2 * num_tokens],
+        decode_from=decode_from,
+    )
+
+
+def paged_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cache: PagedKVCache,
+    layer_index: int,
+    batch: RaggedBatch,
+    scale: float,
+) -> torch.Tensor:
+    """Append the batch's new K/V to ``layer_index`` and attend.
+
+    q: (num_tokens, Hq, D); k, v: (num_tokens, Hkv, D).  Returns the
+    attention context (num_tokens, Hq, D).  Every new token attends to its
+    sequence's cached prefix and, causally, to the new tokens before it
+    (``layers/attention.py:378-411`` of the reference).
+    """
+    cache.write_slots(layer_index, k, v, batch.slot_mapping)
+    out = torch.empty_like(q)
+    split = batch.decode_from
+    first_decode_token = int(batch.num_tokens - (batch.num_requests - split))
+    if split > 0:
+        # requests [0, split): at least one has several new tokens -> varlen kernel
+        seq_lens = [c + n for c, n in zip(batch.context_lens[:split], batch.query_lens[:split])]
+        _native.varlen_prefill(
+            q[:first_decode_token],
+            batch.cu_seqlens[: split + 1],
+            batch.context_lens_t[:split],
+            cache.keys,
+            cache.values,
+            layer_index,
+            batch.block_tables[:split],
+            max(batch.query_lens[:split]),
+            max(seq_lens),
+            scale,
+            out=out[:first_decode_token],
+        )
+    if split < batch.num_requests:
+        seq_lens = [c + 1 for c in batch.context_lens[split:]]
+        _native.paged_decode(
+            q[first_decode_token:],
+            cache.keys,
+            cache.values,
+            layer_index,
+            batch.block_tables[split:],
+            batch.seq_lens_t[split:],
+            max(seq_lens),
+            sum(seq_lens),
+            scale,
+            out=out[first_decode_token:],
+        )
+    return out

@@ -1,0 +1,129 @@
+"""Loop-for-loop torch restatement of the reference hot path.  Test infrastructure only.
+
+Each function follows the cited lines of ito-integral/nano-infer-engine
+(``src/nano_infer_engine/...``), using the same torch ops in the same order
+so the rounding points match: bf16 q.k via einsum/matmul, ``* scale`` in the
+storage dtype, fp32 softmax, probabilities cast back to the storage dtype,
+P.V via einsum/matmul.  Works on any device (CPU for the baseline and the
+CPU tests, the GPU for the reference-PyTorch-path comparison).
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def paged_attention_reference(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: tuple[int, ...],
+    sequence_length: int,
+    layer_index: int,
+) -> torch.Tensor:
+    """Decode attention by a loop over logical blocks.
+
+    Follows ``layers/paged_attention.py:68-114``: slice the valid rows of
+    each physical block, expand KV heads with repeat_interleave, score with
+    einsum("hd,thd->ht") times head_dim**-0.5, concatenate in logical order,
+    fp32 softmax cast back to the input dtype, einsum("ht,thd->hd").
+    """
+    _, _, block_size, kv_heads, head_dim = key_cache.shape
+    q_heads = query.shape[0]
+    group = q_heads // kv_heads
+    blocks = -(-sequence_length // block_size)
+    scores, values = [], []
+    for logical, physical in enumerate(block_table[:blocks]):
+        valid = min(block_size, sequence_length - logical * block_size)
+        k_rows = key_cache[layer_index, physical, :valid].repeat_interleave(group, dim=1)
+        v_rows = value_cache[layer_index, physical, :valid].repeat_interleave(group, dim=1)
+        scores.append(torch.einsum("hd,thd->ht", query, k_rows) * (head_dim**-0.5))
+        values.append(v_rows)
+    weights = torch.softmax(torch.cat(scores, dim=-1), dim=-1, dtype=torch.float32).to(query.dtype)
+    return torch.einsum("ht,thd->hd", weights, torch.cat(values, dim=0))
+
+
+def batched_paged_attention_reference(query, key_cache, value_cache, block_tables, sequence_lengths, layer_index):
+    """Per-sequence loop + stack (``layers/paged_attention.py:164-176``)."""
+    return torch.stack(
+        [
+            paged_attention_reference(query[b], key_cache, value_cache, block_tables[b], sequence_lengths[b], layer_index)
+            for b in range(query.shape[0])
+        ],
+        dim=0,
+    )
+
+
+def write_tokens(keys, values, layer_index, table, block_size, start_position, new_keys, new_values) -> None:
+    """Per-token scatter into the pool (``paged_cache.py:306-322``)."""
+    for t in range(new_keys.shape[0]):
+        logical, offset = divmod(start_position + t, block_size)
+        physical = table[logical]
+        keys[layer_index, physical, offset].copy_(new_keys[t])
+        values[layer_index, physical, offset].copy_(new_values[t])
+
+
+def gather_tokens(keys, values, layer_index, table, block_size, token_count):
+    """Per-token gather + stack in logical order (``paged_cache.py:349-362``)."""
+    k_rows, v_rows = [], []
+    for p in range(token_count):
+        logical, offset = divmod(p, block_size)
+        physical = table[logical]
+        k_rows.append(keys[layer_index, physical, offset])
+        v_rows.append(values[layer_index, physical, offset])
+    return torch.stack(k_rows), torch.stack(v_rows)
+
+
+def ragged_attention_reference(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    layer_index: int,
+    tables,
+    context_lens,
+    query_lens,
+    scale: float,
+) -> torch.Tensor:
+    """Flattened varlen attention, one request at a time.
+
+    Follows ``layers/attention.py:378-412``: write the request's new K/V,
+    gather its whole context, repeat_interleave KV heads, ``q @ k^T * scale``,
+    mask key_pos > query_pos with -inf, fp32 softmax cast to the value
+    dtype, ``@ v``; contexts concatenated in request order.
+    q (T, Hq, D); k, v (T, Hkv, D) -> (T, Hq, D).
+    """
+    block_size = keys.shape[2]
+    group = q.shape[1] // k.shape[1]
+    outputs = []
+    start = 0
+    for table, ctx, n in zip(tables, context_lens, query_lens):
+        end = start + n
+        write_tokens(keys, values, layer_index, table, block_size, ctx, k[start:end], v[start:end])
+        total = ctx + n
+        ks, vs = gather_tokens(keys, values, layer_index, table, block_size, total)
+        ks = ks.repeat_interleave(group, dim=1).transpose(0, 1)
+        vs = vs.repeat_interleave(group, dim=1).transpose(0, 1)
+        query = q[start:end].transpose(0, 1)
+        scores = query @ ks.transpose(-1, -2) * scale
+        q_pos = torch.arange(ctx, total, device=q.device)[:, None]
+        k_pos = torch.arange(total, device=q.device)[None, :]
+        scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
+        probs = torch.softmax(scores, dim=-1, dtype=torch.float32)
+        outputs.append((probs.to(vs.dtype) @ vs).transpose(0, 1))
+        start = end
+    return torch.cat(outputs, dim=0)
+
+
+def attention_core_like_product(q, k, v, cache, layer_index, batch, scale):
+    """Same signature as the product's per-layer attention core, computed by
+    :func:`ragged_attention_reference` on the cache's storage tensors.
+
+    Used to run the product model with the reference algorithm swapped in
+    (the "reference PyTorch path" of the end-to-end comparison).
+    """
+    tables = [cache.get_block_table(s) for s in batch.sequence_ids]
+    return ragged_attention_reference(
+        q, k, v, cache.keys, cache.values, layer_index, tables, batch.context_lens, batch.query_lens, scale
+    )

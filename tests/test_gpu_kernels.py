@@ -1,0 +1,237 @@
+"""HIP kernels vs the oracle, called through the C ABI (via nano_infer_engine._native).
+
+Bars: KV append / gather / block copies bit-exact; attention fp32 max-abs
+<= 1e-4 and bf16 max-abs <= 2e-2 against the reference-algorithm oracle on
+the same seeded inputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nano_infer_engine import _native, workloads
+from oracle import reference_ops
+from oracle import closed_form
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+def _log(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def _decode_hip(wl: workloads.PagedWorkload, kc, vc, q, dtype):
+    tables = torch.from_numpy(wl.table_array()).to(DEV)
+    lens = torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)
+    out = _native.paged_decode(
+        q.to(DEV), kc, vc, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens), wl.head_dim**-0.5
+    )
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _decode_oracle(wl, kc_cpu, vc_cpu, q_cpu):
+    return reference_ops.batched_paged_attention_reference(
+        q_cpu, kc_cpu, vc_cpu, tuple(tuple(t) for t in wl.tables), tuple(wl.seq_lens), 0
+    )
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kv_append_bit_exact(dtype):
+    _log(f"kv_append dtype={dtype}")
+    wl = workloads.ragged([0, 5, 31, 100], [7, 1, 16, 33], seed=11, num_blocks=64)
+    kc, vc = wl.pool(dtype)
+    _, k_new, v_new = wl.new_tokens(dtype)
+    # source rows as a strided view of a wider buffer (like a fused projection output)
+    wide_k = torch.zeros((k_new.shape[0], 3, wl.kv_heads, wl.head_dim), dtype=dtype)
+    wide_k[:, 1] = k_new
+    slots = wl.slots()
+    slots_with_skip = np.concatenate([slots, [-1]])
+    k_src = torch.cat([k_new, torch.full_like(k_new[:1], 7.0)])
+    v_src = torch.cat([v_new, torch.full_like(v_new[:1], 7.0)])
+
+    ref_k, ref_v = kc.clone(), vc.clone()
+    start = 0
+    for table, ctx, n in zip(wl.tables, wl.context_lens, wl.query_lens):
+        reference_ops.write_tokens(ref_k, ref_v, 0, table, wl.block_size, ctx, k_new[start : start + n], v_new[start : start + n])
+        start += n
+
+    dk, dv = kc.to(DEV), vc.to(DEV)
+    _native.kv_append(dk, dv, 0, k_src.to(DEV), v_src.to(DEV), torch.from_numpy(slots_with_skip).to(DEV))
+    assert torch.equal(dk.cpu(), ref_k) and torch.equal(dv.cpu(), ref_v)
+
+    # strided source view
+    dk, dv = kc.to(DEV), vc.to(DEV)
+    wide_k_dev = wide_k.to(DEV)
+    _native.kv_append(dk, dv, 0, wide_k_dev[:, 1], v_new.to(DEV), torch.from_numpy(slots).to(DEV))
+    assert torch.equal(dk.cpu(), ref_k) and torch.equal(dv.cpu(), ref_v)
+
+
+def test_kv_append_large_pool_offsets():
+    """Slots whose element offsets exceed 2**31 land exactly where the slot math says."""
+    _log("kv_append large pool")
+    num_blocks, bs, hkv, d = 270_000, 16, 8, 64  # 2.2e9 elements per pool (4.4 GB bf16)
+    kc = torch.zeros((1, num_blocks, bs, hkv, d), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    # the last two slots sit past element offset 2**31; the final one is past
+    # the pool and must be skipped
+    slots = torch.tensor([0, 2**21 + 3, 2**31 // (hkv * d) + 5, num_blocks * bs - 1, num_blocks * bs], dtype=torch.int64)
+    rows = (torch.arange(5 * hkv * d, dtype=torch.float32).reshape(5, hkv, d) + 1).to(torch.bfloat16)
+    _native.kv_append(kc, vc, 0, rows.to(DEV), (rows + 1).to(DEV), slots.to(DEV))
+    flat_k = kc.view(-1, hkv, d)
+    flat_v = vc.view(-1, hkv, d)
+    for i, s in enumerate(slots.tolist()[:4]):
+        assert torch.equal(flat_k[s].cpu(), rows[i])
+        assert torch.equal(flat_v[s].cpu(), rows[i] + 1)
+    assert int((kc != 0).sum().item()) == 4 * hkv * d
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("block_size", [1, 4, 16, 32])
+def test_kv_gather_bit_exact(dtype, block_size):
+    _log(f"kv_gather dtype={dtype} bs={block_size}")
+    wl = workloads.ragged([0], [45], seed=3, num_blocks=200 // block_size + 8, block_size=block_size)
+    kc, vc = wl.pool(dtype)
+    table = wl.tables[0]
+    want_k, want_v = reference_ops.gather_tokens(kc, vc, 0, table, block_size, 45)
+    got_k, got_v = _native.kv_gather(
+        kc.to(DEV), vc.to(DEV), 0, torch.tensor(table, dtype=torch.int32, device=DEV), 45
+    )
+    assert torch.equal(got_k.cpu(), want_k) and torch.equal(got_v.cpu(), want_v)
+
+
+def test_kv_copy_blocks_round_trip():
+    _log("kv_copy_blocks")
+    shape = (3, 20, 16, 8, 64)
+    g = torch.Generator().manual_seed(5)
+    src_k = torch.randn(shape, generator=g).to(torch.bfloat16)
+    src_v = torch.randn(shape, generator=g).to(torch.bfloat16)
+    blocks = [7, 2, 19, 0]
+    staged_k = torch.empty((3, 4, 16, 8, 64), dtype=torch.bfloat16, device=DEV)
+    staged_v = torch.empty_like(staged_k)
+    _native.kv_copy_blocks(src_k.to(DEV), src_v.to(DEV), torch.tensor(blocks, dtype=torch.int32, device=DEV),
+                           staged_k, staged_v, None, 4)
+    assert torch.equal(staged_k.cpu(), src_k[:, blocks]) and torch.equal(staged_v.cpu(), src_v[:, blocks])
+    dst_k = torch.zeros((3, 10, 16, 8, 64), dtype=torch.bfloat16, device=DEV)
+    dst_v = torch.zeros_like(dst_k)
+    dst_blocks = [9, 1, 4, 3]
+    _native.kv_copy_blocks(staged_k, staged_v, None, dst_k, dst_v, torch.tensor(dst_blocks, dtype=torch.int32, device=DEV), 4)
+    assert torch.equal(dst_k[:, dst_blocks].cpu(), src_k[:, blocks])
+    assert torch.equal(dst_v[:, dst_blocks].cpu(), src_v[:, blocks])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_small_matches_oracle(dtype):
+    _log(f"decode_small dtype={dtype}")
+    wl = workloads.decode_small()
+    kc, vc = wl.pool(dtype)
+    q, _, _ = wl.new_tokens(dtype)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, dtype)
+    want = _decode_oracle(wl, kc, vc, q)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
+    if dtype == torch.float32:
+        # and the oracle itself against float64 closed form
+        for b in range(4):
+            ks, vs = reference_ops.gather_tokens(kc, vc, 0, wl.tables[b], wl.block_size, wl.seq_lens[b])
+            exact = closed_form.decode(q[b].numpy(), ks.numpy(), vs.numpy(), wl.head_dim**-0.5)
+            assert np.abs(got[b].numpy() - exact).max() <= 1e-4
+
+
+def test_decode_ragged_lognormal_bf16():
+    """16 sequences, lognormal lengths up to 29600 (split-K with merge)."""
+    _log("decode_ragged bf16")
+    wl = workloads.decode_ragged()
+    kc, vc = wl.pool(torch.bfloat16)
+    q, _, _ = wl.new_tokens(torch.bfloat16)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, torch.bfloat16)
+    want = _decode_oracle(wl, kc, vc, q)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  lengths={wl.seq_lens} max_abs_err={err:.3e}")
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize(
+    "q_heads,kv_heads,head_dim,block_size",
+    [(4, 4, 64, 16), (4, 2, 64, 2), (8, 2, 64, 1), (16, 2, 64, 4), (16, 1, 64, 32), (32, 8, 128, 16), (8, 8, 128, 3)],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
+    _log(f"decode shapes hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype}")
+    wl = workloads.ragged([0, 4, 70, 300, 1000], [1] * 5, seed=7, pool_factor=1.5, q_heads=q_heads,
+                          kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
+    kc, vc = wl.pool(dtype)
+    q, _, _ = wl.new_tokens(dtype)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, dtype)
+    want = _decode_oracle(wl, kc, vc, q)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+def test_decode_ignores_garbage_past_length():
+    """NaN in unused slots of the last block must not reach the output."""
+    _log("decode garbage")
+    wl = workloads.ragged([20, 37], [1, 1], seed=9, num_blocks=16)
+    kc, vc = wl.pool(torch.bfloat16)
+    for table, n in zip(wl.tables, wl.seq_lens):
+        last = table[(n - 1) // 16]
+        kc[0, last, (n - 1) % 16 + 1 :] = float("nan")
+        vc[0, last, (n - 1) % 16 + 1 :] = float("nan")
+    q, _, _ = wl.new_tokens(torch.bfloat16)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, torch.bfloat16)
+    assert torch.isfinite(got).all()
+    want = _decode_oracle(wl, kc, vc, q)
+    assert (got.float() - want.float()).abs().max().item() <= 2e-2
+
+
+def _prefill_case(wl, dtype):
+    kc, vc = wl.pool(dtype)
+    q, k_new, v_new = wl.new_tokens(dtype)
+    ref_k, ref_v = kc.clone(), vc.clone()
+    want = reference_ops.ragged_attention_reference(
+        q, k_new, v_new, ref_k, ref_v, 0, wl.tables, wl.context_lens, wl.query_lens, wl.head_dim**-0.5
+    )
+    dk, dv = kc.to(DEV), vc.to(DEV)
+    _native.kv_append(dk, dv, 0, k_new.to(DEV), v_new.to(DEV), torch.from_numpy(wl.slots()).to(DEV))
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(wl.query_lens)]), dtype=torch.int64, device=DEV)
+    ctx = torch.tensor(wl.context_lens, dtype=torch.int32, device=DEV)
+    tables = torch.from_numpy(wl.table_array()).to(DEV)
+    got = _native.varlen_prefill(q.to(DEV), cu, ctx, dk, dv, 0, tables, max(wl.query_lens), max(wl.seq_lens),
+                                 wl.head_dim**-0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), ref_k) and torch.equal(dv.cpu(), ref_v)
+    return got.cpu(), want
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_varlen_prefill_mixed_batch(dtype):
+    _log(f"varlen mixed {dtype}")
+    wl = workloads.mixed_prefill()
+    got, want = _prefill_case(wl, dtype)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize(
+    "q_heads,kv_heads,head_dim,block_size",
+    [(4, 4, 64, 16), (4, 2, 64, 2), (8, 1, 64, 4), (16, 1, 64, 16), (32, 2, 128, 32), (8, 4, 128, 5)],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_varlen_prefill_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
+    _log(f"varlen shapes hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype}")
+    wl = workloads.ragged([0, 3, 50, 0, 17], [19, 5, 1, 40, 2], seed=13, pool_factor=1.5, q_heads=q_heads,
+                          kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
+    got, want = _prefill_case(wl, dtype)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
