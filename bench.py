@@ -1,0 +1,283 @@
+"""Benchmark of the paged-attention decode path on one MI355X.
+
+Workload (one "step"): a continuous-batching decode step of the Llama-3.2-1B
+attention geometry — 16 ragged sequences with lognormal context lengths
+(median 2048, sigma 1, clipped to [32, 29600], seed 1), 32 query / 8 KV
+heads, head_dim 64, block_size 16, bf16, block tables drawn from a seeded
+permutation of a pool twice the size needed.  For each of the 16 layers the
+step appends one new K/V token per sequence through ``slot_mapping`` and runs
+paged decode attention over the grown sequences.  16 layers give a 1.4 GB
+working set, far beyond the 256 MB last-level cache, so every step reads
+its KV from HBM.
+
+Prints one JSON line.  ``value`` = algorithmic bytes (decode K/V/Q/O/table
+reads + append traffic) per second over the timed steps.  ``roofline`` is
+for the decode-attention op, timed per launch with HIP events on its
+stream.  ``cpu_baseline`` times the oracle's restatement of the reference
+PyTorch algorithm on the host cores over a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "nano-infer-engine_amd"))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=40)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--layers", type=int, default=16)
+    p.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
+    p.add_argument("--skip-stress", action="store_true", help="do not run the 16x29600 decode figure")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
+    return p.parse_args()
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class DecodeBench:
+    """Device state for repeated append+decode steps over one workload."""
+
+    def __init__(self, wl, steps_total: int, device, seed: int):
+        import numpy as np
+        import torch
+
+        self.wl = wl
+        self.device = device
+        bs = wl.block_size
+        # extend every table so it holds the tokens appended by all steps
+        rng = np.random.default_rng(seed + 500)
+        need = [-(-(c + steps_total + 1) // bs) for c in wl.context_lens]
+        self.num_blocks = max(int(sum(need) * 2), wl.num_blocks)
+        perm = rng.permutation(self.num_blocks)
+        tables, cursor = [], 0
+        for n in need:
+            tables.append(perm[cursor : cursor + n])
+            cursor += n
+        width = max(len(t) for t in tables)
+        table_arr = np.zeros((len(tables), width), dtype=np.int32)
+        for r, t in enumerate(tables):
+            table_arr[r, : len(t)] = t
+        shape = (wl.num_layers, self.num_blocks, bs, wl.kv_heads, wl.head_dim)
+        gen = torch.Generator(device=device).manual_seed(seed)
+        self.k_cache = torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16)
+        self.v_cache = torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16)
+        self.tables = torch.from_numpy(table_arr).to(device)
+        b = len(tables)
+        # per-step metadata, built before any timing
+        slots = np.zeros((steps_total, b), dtype=np.int64)
+        lens = np.zeros((steps_total, b), dtype=np.int32)
+        self.max_len, self.total_len, self.seq_lens_host = [], [], []
+        for s in range(steps_total):
+            pos = np.asarray(wl.context_lens) + s
+            slots[s] = table_arr[np.arange(b), pos // bs].astype(np.int64) * bs + pos % bs
+            lens[s] = pos + 1
+            self.max_len.append(int(lens[s].max()))
+            self.total_len.append(int(lens[s].sum()))
+            self.seq_lens_host.append(lens[s].tolist())
+        self.slots = torch.from_numpy(slots).to(device)
+        self.lens = torch.from_numpy(lens).to(device)
+        self.q = torch.randn((b, wl.q_heads, wl.head_dim), generator=gen, device=device, dtype=torch.bfloat16)
+        self.k_new = torch.randn((b, wl.kv_heads, wl.head_dim), generator=gen, device=device, dtype=torch.bfloat16)
+        self.v_new = torch.randn_like(self.k_new)
+        self.out = torch.empty_like(self.q)
+        self.scale = wl.head_dim**-0.5
+
+    def step(self, s: int, events: list | None = None) -> None:
+        """One decode step over every layer; optionally brackets each decode launch with HIP events."""
+        import torch
+
+        from nano_infer_engine import _native
+
+        for layer in range(self.wl.num_layers):
+            _native.kv_append(self.k_cache, self.v_cache, layer, self.k_new, self.v_new, self.slots[s])
+            if events is not None:
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+            _native.paged_decode(
+                self.q, self.k_cache, self.v_cache, layer, self.tables, self.lens[s],
+                self.max_len[s], self.total_len[s], self.scale, out=self.out,
+            )
+            if events is not None:
+                end.record()
+                events.append((start, end))
+
+
+def run_gpu(args):
+    import torch
+
+    from nano_infer_engine import _native, workloads
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    _native.load_library()
+    wl = workloads.decode_ragged(num_layers=args.layers)
+    total_steps = args.warmup + args.steps
+    bench = DecodeBench(wl, total_steps, device, seed=1)
+    log(f"workload: {len(wl.context_lens)} seqs, contexts {wl.context_lens}, layers {args.layers}, "
+        f"pool {bench.num_blocks} blocks ({2 * bench.k_cache.numel() * 2 / 1e9:.2f} GB)")
+
+    for s in range(args.warmup):
+        bench.step(s)
+    torch.cuda.synchronize()
+
+    ev: list = []
+    t0 = time.perf_counter()
+    for s in range(args.warmup, total_steps):
+        bench.step(s, ev)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    decode_bytes = 0
+    append_bytes = 0
+    for s in range(args.warmup, total_steps):
+        decode_bytes += workloads.decode_bytes(bench.seq_lens_host[s]) * args.layers
+        append_bytes += workloads.append_bytes(len(wl.context_lens)) * args.layers
+    launch_ms = [a.elapsed_time(b) for a, b in ev]
+    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
+    bytes_per_launch = decode_bytes / len(launch_ms)
+    achieved = bytes_per_launch / avg_launch_s / 1e9
+    value = (decode_bytes + append_bytes) / elapsed / 1e9
+    log(f"timed {args.steps} steps in {elapsed * 1e3:.2f} ms; decode launch avg {avg_launch_s * 1e6:.2f} us "
+        f"for {bytes_per_launch / 1e6:.2f} MB -> {achieved:.0f} GB/s")
+
+    result = {
+        "metric": "paged-attn HBM GB/s (% of peak); e2e output tok/s, Llama-1B-shape batch 16",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q, seeded lognormal context lengths",
+        "config": {
+            "workload": "continuous-batching decode step: 16 ragged sequences (lognormal median 2048, "
+                        "sigma 1, clip [32, 29600], seed 1), 32 q / 8 kv heads, head_dim 64, block_size 16, "
+                        f"append 1 token/seq then paged decode attention, x{args.layers} layers",
+            "sequences": len(wl.context_lens),
+            "context_tokens_first_step": int(sum(wl.context_lens)),
+            "layers": args.layers,
+            "global_batch": len(wl.context_lens),
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_kernel (+ decode_merge_kernel inside the timed launch)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": _measured_traffic(),
+            "algorithmic_bytes_per_launch": int(bytes_per_launch),
+            "avg_launch_us": round(avg_launch_s * 1e6, 3),
+        },
+    }
+    del bench
+    torch.cuda.empty_cache()
+    if not args.skip_stress:
+        result["stress_16x29600"] = run_stress(args)
+    return result
+
+
+def run_stress(args):
+    """Decode over 16 x 29600-token contexts (970 MB per layer-step), one layer."""
+    import torch
+
+    from nano_infer_engine import workloads
+
+    device = torch.device("cuda:0")
+    steps, warmup = 20, 3
+    wl = workloads.decode_long(num_layers=1)
+    bench = DecodeBench(wl, steps + warmup, device, seed=4)
+    for s in range(warmup):
+        bench.step(s)
+    torch.cuda.synchronize()
+    ev: list = []
+    for s in range(warmup, warmup + steps):
+        bench.step(s, ev)
+    torch.cuda.synchronize()
+    launch_ms = [a.elapsed_time(b) for a, b in ev]
+    avg = sum(launch_ms) / len(launch_ms) / 1e3
+    per_launch = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(warmup, warmup + steps)) / steps
+    gbs = per_launch / avg / 1e9
+    log(f"stress 16x29600: {avg * 1e6:.1f} us per layer-step, {gbs:.0f} GB/s")
+    del bench
+    torch.cuda.empty_cache()
+    return {"avg_launch_us": round(avg * 1e6, 2), "bytes_per_launch": int(per_launch),
+            "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def _measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(REPO, "profiles", "paged_decode_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def run_cpu_baseline(args):
+    """The oracle (reference algorithm, torch on CPU) on a bounded sample of the workload."""
+    import torch
+
+    from nano_infer_engine import workloads
+    from oracle import reference_ops
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    wl = workloads.decode_ragged(num_layers=1)
+    kc, vc = wl.pool(torch.bfloat16)
+    q, _, _ = wl.new_tokens(torch.bfloat16)
+    tables = tuple(tuple(t) for t in wl.tables)
+    lens = tuple(wl.seq_lens)
+    reference_ops.batched_paged_attention_reference(q, kc, vc, tables, lens, 0)  # warm-up
+    done, t0 = 0, time.perf_counter()
+    while True:
+        reference_ops.batched_paged_attention_reference(q, kc, vc, tables, lens, 0)
+        done += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    elapsed = time.perf_counter() - t0
+    gbs = workloads.decode_bytes(lens) * done / elapsed / 1e9
+    log(f"cpu baseline: {done} layer-steps in {elapsed:.1f} s on {threads} threads -> {gbs:.3f} GB/s")
+    return {
+        "value": round(gbs, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{done} single-layer decode attention calls over the same 16 sequences "
+                  f"({sum(lens)} tokens), reference per-block loop in torch bf16 on CPU, {elapsed:.1f} s",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the path runs on a single MI355X).", file=sys.stderr)
+        sys.exit(2)
+    result = run_gpu(args)
+    result["cpu_baseline"] = None if args.skip_cpu else run_cpu_baseline(args)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -24,7 +24,9 @@
  *    validate tables on the host (the Python layer does).
  *  - Every call is asynchronous on `stream` (a hipStream_t; NULL = default
  *    stream).  The library never allocates or frees device memory: scratch
- *    space is the caller's `workspace`, sized by the *_workspace_bytes query.
+ *    space is the caller's `workspace`, sized by the *_workspace_bytes query;
+ *    it needs no initialisation.  Calls that overlap in time (different
+ *    streams) need different workspaces.
  *  - Return value: NIE_OK, or a negative NIE_E* code; nie_last_error() then
  *    holds a message for the calling thread.
  */
@@ -116,6 +118,8 @@ int nie_kv_copy_blocks(int dtype,
 /*
  * Workspace bytes needed by nie_paged_decode for a batch whose sequence
  * lengths have maximum max_seq_len and sum total_seq_len (host values).
+ * Layout: fp32 split partials (unnormalised O rows, then (max, sum) pairs).
+ * The pointer must be 16-byte aligned.  May be 0 when no sequence splits.
  */
 int64_t nie_paged_decode_workspace_bytes(int64_t batch, int64_t q_heads,
                                          int64_t head_dim, int64_t block_size,
@@ -135,6 +139,8 @@ int64_t nie_paged_decode_workspace_bytes(int64_t batch, int64_t q_heads,
  *   seq_lens     : (batch,) int32 device copy of the lengths, each >= 1.
  *   max_seq_len / total_seq_len : host copies of max and sum of seq_lens;
  *           they size the launch and must be exact.
+ * Long sequences are split over several workgroups whose fp32 partials a
+ * second kernel, on the same stream, merges exactly (log-sum-exp weights).
  * Numerics follow the reference: the q.k score is rounded to the storage
  * dtype and scaled in that dtype, softmax runs in fp32, P.V accumulates in
  * fp32 and the result is rounded to the storage dtype.

@@ -5,8 +5,9 @@
 //   kv_gather_kernel        logical -> contiguous copy of one sequence
 //   kv_copy_blocks_kernel   whole-block copies (export / import of sequences)
 //   paged_decode_kernel     split-K decode attention, one workgroup per
-//                           (sequence, key-split), one wave per KV head
-//   decode_merge_kernel     exact fp32 merge of the split-K partials
+//                           (sequence, key split, KV-head group), one wave
+//                           per KV head; the last split of a sequence to
+//                           finish merges the partials (exact fp32)
 //   varlen_prefill_kernel   chunked-prefill attention over packed varlen rows
 //
 // Attention math (both attention kernels) runs on the matrix cores with the
@@ -31,6 +32,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "nie_paged.h"
@@ -95,16 +97,17 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// float -> bf16, round to nearest even (torch's conversion).  NaN stays NaN.
+// float -> bf16, round to nearest even (torch's conversion).  NaN stays a
+// quiet NaN.  Branch-free: both candidates are computed and selected.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet_nan = (u >> 16) | 0x40u;
+  return ((u & 0x7fffffffu) > 0x7f800000u) ? quiet_nan : rounded;
 }
 
 __device__ __forceinline__ float round_to_bf16(float x) {
-  return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  return __uint_as_float(f32_to_bf16_bits(x) << 16);
 }
 
 // Rounds a value to the storage dtype (identity for fp32).
@@ -133,6 +136,12 @@ __device__ __forceinline__ float max_over_groups(float x) {
   return x;
 }
 
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Locates work item `item` in a flattened list where sequence b owns
 // per_seq(b) consecutive items.  Every lane of the wave returns the same
 // (b, k, first_item_of_b, count_of_b); b == -1 if item is past the end.
@@ -157,10 +166,14 @@ __device__ __forceinline__ void locate_item(int64_t item, int64_t num_seqs, Coun
       const bool mine = (b < num_seqs) && (item >= base + excl) && (item < base + incl);
       const uint64_t mask = __ballot(mine);
       const int src = __builtin_ctzll(mask);
-      *seq = b0 + src;
-      *first = base + __shfl(excl, src);
-      *count = __shfl(n, src);
-      *local = item - *first;
+      // The values are wave-uniform; readfirstlane lets the compiler keep
+      // everything derived from them (table lookups, addresses) in SGPRs.
+      const int64_t f = base + __shfl(excl, src);
+      const int64_t c = __shfl(n, src);
+      *seq = (int64_t)__builtin_amdgcn_readfirstlane((int)(b0 + src));
+      *first = uniform64(f);
+      *count = uniform64(c);
+      *local = uniform64(item - f);
       return;
     }
     base += total;
@@ -202,15 +215,54 @@ __device__ __forceinline__ int64_t token_offset(const CacheGeom& g, const int32_
   return g.layer_offset + ((int64_t)phys * g.block_size + off) * g.row_elems;
 }
 
+// Caches 64 consecutive block-table entries of one sequence in a VGPR
+// (entry base+i in lane i), so the per-tile physical-block lookup is a
+// v_readlane instead of a memory load whose wait would also drain the
+// prefetched K/V loads.
+struct TableCache {
+  int base;     // first cached logical block (wave-uniform)
+  int entries;  // lane i: table[base + i], 0 past the end of the table row
+
+  __device__ __forceinline__ void load(const int32_t* table, int table_len, int first) {
+    base = __builtin_amdgcn_readfirstlane(first);
+    const int i = base + lane_id();
+    entries = i < table_len ? table[i] : 0;
+  }
+  // Physical block of logical block `lb` (wave-uniform).  With kRefill the
+  // window moves when `lb` leaves it; without, the caller guarantees
+  // base <= lb < base + 64 (no load inside the caller's loop, so the
+  // compiler can keep counting that loop's outstanding K/V loads exactly).
+  template <bool kRefill>
+  __device__ __forceinline__ int lookup(const int32_t* table, int table_len, int lb) {
+    lb = __builtin_amdgcn_readfirstlane(lb);
+    if constexpr (kRefill) {
+      if (lb < base || lb - base >= kWave) load(table, table_len, lb);
+    }
+    const int idx = lb - base;
+    return __builtin_amdgcn_readlane(entries, idx < 0 ? 0 : (idx >= kWave ? kWave - 1 : idx));
+  }
+};
+
 // Addressing of the 16 keys of one tile (tiles start at multiples of 16).
-// kUniform: block_size is a multiple of 16, so the whole tile lies in one
-// physical block and a single (scalar) table lookup serves all lanes.
-template <bool kUniform>
+// kUniform: block_size is a power of two >= 16, so the whole tile lies in one
+// physical block: one wave-uniform lookup (through a TableCache) serves all
+// lanes and per-lane offsets are 32-bit.  Otherwise every lane resolves its
+// own key through the table.
+template <bool kUniform, bool kRefill>
 struct TileAddr {
   int64_t base;
   __device__ __forceinline__ void init(const CacheGeom& g, const int32_t* table, int table_len,
-                                       int key0) {
-    if constexpr (kUniform) base = token_offset(g, table, table_len, key0);
+                                       TableCache& tc, int key0) {
+    if constexpr (kUniform) {
+      // uniform mode implies a power-of-two block size (see the launchers)
+      key0 = __builtin_amdgcn_readfirstlane(key0);
+      int lb = key0 >> g.bs_shift;
+      const int off = key0 & (g.block_size - 1);
+      lb = lb < table_len ? lb : table_len - 1;
+      int phys = tc.template lookup<kRefill>(table, table_len, lb);
+      phys = phys < 0 ? 0 : (phys >= g.num_blocks ? g.num_blocks - 1 : phys);
+      base = g.layer_offset + ((int64_t)phys * g.block_size + off) * g.row_elems;
+    }
   }
   // offset of key key0 + r
   __device__ __forceinline__ int64_t at(const CacheGeom& g, const int32_t* table, int table_len,
@@ -223,20 +275,14 @@ struct TileAddr {
   }
 };
 
-template <int N>
-__device__ __forceinline__ void load_vecs(uint4 (&dst)[N], const void* src) {
-  const uint4* s = reinterpret_cast<const uint4*>(src);
-#pragma unroll
-  for (int i = 0; i < N; ++i) dst[i] = s[i];
-}
-
 // ---------------------------------------------------------------------------
 // MFMA tile math shared by decode and prefill
 // ---------------------------------------------------------------------------
 // Each lane holds, for its row (l%16: the key for K, the query row for Q),
-// the D/4 consecutive dims starting at (D/4)*(l/16).  The MFMA K index is
-// mapped onto those dims identically for both operands, so the sum over all
-// MFMAs is the full q.k dot product.
+// kVec 16-byte vectors; vector j covers bytes [64j + 16*(l/16), +16) of the
+// row, so one load instruction reads 64 contiguous bytes of 16 rows.  The
+// MFMA K index is mapped onto those dims identically for both operands, so
+// the sum over all MFMAs is the full q.k dot product.
 template <typename T, int D>
 struct Frag {
   static constexpr int kBytes = D * Elt<T>::kBytes / 4;  // bytes of one lane's slice
@@ -244,10 +290,19 @@ struct Frag {
   uint4 v[kVec];
 };
 
+// Loads this lane's slice of a row (`row` = element 0 of the row).
+template <typename T, int D>
+__device__ __forceinline__ void load_slice(Frag<T, D>& f, const void* row) {
+  const unsigned char* p = reinterpret_cast<const unsigned char*>(row) + 16 * (lane_id() >> 4);
+#pragma unroll
+  for (int j = 0; j < Frag<T, D>::kVec; ++j) f.v[j] = *reinterpret_cast<const uint4*>(p + 64 * j);
+}
+
 template <typename T, int D>
 __device__ __forceinline__ v4f qk_mfma(const Frag<T, D>& k, const Frag<T, D>& q) {
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   if constexpr (Elt<T>::kIsBf16) {
+    // MFMA c takes 4 bf16 (two dwords) of the slice; c -> (vector c/2, half c%2)
     const uint32_t* kw = reinterpret_cast<const uint32_t*>(k.v);
     const uint32_t* qw = reinterpret_cast<const uint32_t*>(q.v);
 #pragma unroll
@@ -488,16 +543,194 @@ __device__ __forceinline__ int64_t decode_splits_of(const DecodeArgs& a, int64_t
   return len > 0 ? cdiv(cdiv(len, kTileKeys), a.tiles_per_split) : (int64_t)0;
 }
 
-template <typename T, int D, bool kUniform>
-__global__ __launch_bounds__(kDecodeWaves* kWave) void paged_decode_kernel(DecodeArgs a) {
-  constexpr int kRowBytes = D * Elt<T>::kBytes;
-  constexpr int kPitch = kRowBytes + kLdsPadBytes;
-  constexpr int kChunksPerRow = kRowBytes / 16;        // 16-byte chunks per V row
-  constexpr int kRowsPerPass = kWave / kChunksPerRow;  // V rows one load instruction covers
-  constexpr int kPasses = kTileKeys / kRowsPerPass;    // load instructions per V tile
-  constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
+// s_waitcnt immediate that waits until at most `n` vector-memory operations
+// are outstanding and leaves the export / LGKM counters alone (gfx9 encoding).
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16-byte-per-lane global -> LDS DMA (global_load_lds_dwordx4): lane l's 16
+// bytes land at dst + 16*l.  The builtin exists only in the device pass; in
+// the host pass (which only emits launch stubs) it would make clang drop the
+// enclosing kernel's stub, so the host pass sees an empty body.
+__device__ __forceinline__ void lds_dma16(const void* src, unsigned char* dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+#else
+  (void)src;
+  (void)dst;
+#endif
+}
+
+// ---------------------------------------------------------------------------
+// Decode staging.  A workgroup owns a group of kHeads KV heads (one wave per
+// head) and, for every 16-key tile, stages in LDS the K and V rows of all its
+// heads: row r of a tile is key key0+r's contiguous slice of kHeads*D
+// elements (1 KiB for 8 bf16 heads of 64 dims).  The rows are fetched with
+// LDS DMA (global_load_lds_dwordx4), 64 lanes x 16 bytes = 1 KiB of
+// consecutive bytes per op, spread round-robin over the waves, so every op
+// is a fully contiguous read — the access pattern of a streaming copy.
+// Chunk c of row r is stored at chunk position c ^ (r & 15): both the MFMA
+// K reads (16 lanes read one chunk of 16 different rows) and the V^T reads
+// (four lane groups read rows 4g+e) then hit distinct LDS banks.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int kHeads>
+struct GroupTile {
+  static constexpr int kSliceBytes = kHeads * D * Elt<T>::kBytes;  // one key's row
+  static constexpr int kChunks = kSliceBytes / 16;                  // 16-byte chunks per row
+  static constexpr int kSwzMask = (kChunks < 16 ? kChunks : 16) - 1;
+  static constexpr int kBytes = kTileKeys * kSliceBytes;           // one K (or V) tile
+  static constexpr int kOps = kBytes / (kWave * 16);               // DMA ops per K (or V) tile
+  static constexpr int kRowsPerOp = kWave * 16 / kSliceBytes;
+  static constexpr int kOpsPerWave = kOps / kHeads;
+  static_assert(kSliceBytes <= kWave * 16 && (kWave * 16) % kSliceBytes == 0, "slice must divide 1 KiB");
+  static_assert(kOps % kHeads == 0, "ops must spread evenly over the waves");
+  __device__ static __forceinline__ int swz(int r) { return r & kSwzMask; }
+  // LDS byte offset of 16-byte chunk c of row r
+  __device__ static __forceinline__ int chunk_offset(int r, int c) { return r * kSliceBytes + ((c ^ swz(r)) << 4); }
+  // LDS byte offset of element d of head hl in row r
+  __device__ static __forceinline__ int elt_offset(int r, int hl, int d) {
+    const int byte = (hl * D + d) * Elt<T>::kBytes;
+    return chunk_offset(r, byte >> 4) + (byte & 15);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Ring reads.  The tiles arrive by LDS DMA, whose destination the compiler
+// cannot tell apart per ring slot, so compiler-visible LDS reads of the ring
+// would each be preceded by a wait for *all* DMA in flight.  The bf16 path
+// therefore reads the ring with inline-asm ds_reads, after the explicit
+// vmcnt wait + barrier that cover exactly the tile being read; a closing
+// lgkmcnt(0) asm takes every result as a read-write operand, so no use of a
+// result can be scheduled before the data has arrived.
+// ---------------------------------------------------------------------------
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// K slice (MFMA A layout, kVec 16-byte chunks) at precomputed LDS addresses.
+template <int kVec>
+__device__ __forceinline__ void ring_read_k(uint4 (&out)[kVec], const uint32_t (&addr)[kVec]) {
+  v4u r[kVec];
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) asm volatile("ds_read_b128 %0, %1" : "=v"(r[j]) : "v"(addr[j]));
+  if constexpr (kVec == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]));
+  } else {
+    static_assert(kVec == 4, "bf16 slices are 2 or 4 chunks");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+  }
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) out[j] = uint4{r[j][0], r[j][1], r[j][2], r[j][3]};
+}
+
+// Sixteen bf16 V^T values (four MFMA A operands) at precomputed addresses.
+__device__ __forceinline__ void ring_read_vt16(v4s (&a)[4], const uint32_t (&addr)[16]) {
+  uint32_t r[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) asm volatile("ds_read_u16 %0, %1" : "=v"(r[i]) : "v"(addr[i]));
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
+                 "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]),
+                 "+v"(r[13]), "+v"(r[14]), "+v"(r[15]));
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[c][e] = (short)r[4 * c + e];
+  }
+}
+
+// Merges the split partials of `rows` consecutive query heads (starting at
+// qh0) of sequence b, one wave: weights exp(m_s - max) one split per lane,
+// O rows read as float4 by D/4 lanes per split, several splits per load
+// instruction, all rows' loads issued before any is consumed.
+template <typename T, int D>
+__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int64_t b, int64_t first, int nsplit,
+                                             int qh0, int rows) {
+  constexpr int kLanesPerSplit = D / 4;
+  constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
+  const int lane = lane_id();
+  const int sub = lane / kLanesPerSplit;
+  const int chunk = lane % kLanesPerSplit;
+  const int64_t ml_stride = (int64_t)a.q_heads * 2;
+  const int64_t po_stride = (int64_t)a.q_heads * D;
+  for (int r = 0; r < rows; ++r) {
+    const int qh = qh0 + r;
+    const float* ml = a.ws_ml + (first * a.q_heads + qh) * 2;
+    const float* po = a.ws_o + (first * a.q_heads + qh) * D;
+    float mmax = kNegInf;
+    for (int s = lane; s < nsplit; s += kWave) mmax = fmaxf(mmax, ml[s * ml_stride]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+    float denom = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nsplit; s0 += kWave) {
+      const int s_lane = s0 + lane;
+      float w = 0.f;
+      if (s_lane < nsplit) {
+        const float m = ml[s_lane * ml_stride];
+        w = (m == kNegInf) ? 0.f : exp2f((m - mmax) * kLog2e);
+        denom += w * ml[s_lane * ml_stride + 1];
+      }
+      const int count = min(kWave, nsplit - s0);
+#pragma unroll 8
+      for (int k = 0; k < count; k += kSplitsPerPass) {
+        const int s = k + sub;
+        const float ws = __shfl(w, s < kWave ? s : 0);
+        if (s < count) {
+          const float4 v = *reinterpret_cast<const float4*>(po + (s0 + s) * po_stride + 4 * chunk);
+          acc.x += ws * v.x;
+          acc.y += ws * v.y;
+          acc.z += ws * v.z;
+          acc.w += ws * v.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) denom += __shfl_xor(denom, off);
+#pragma unroll
+    for (int off = kLanesPerSplit; off < kWave; off <<= 1) {
+      acc.x += __shfl_xor(acc.x, off);
+      acc.y += __shfl_xor(acc.y, off);
+      acc.z += __shfl_xor(acc.z, off);
+      acc.w += __shfl_xor(acc.w, off);
+    }
+    if (sub == 0) {
+      const float inv = 1.f / denom;
+      T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * chunk;
+      store4<T>(dst, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
+  }
+}
+
+// Heads per decode workgroup: as many as fill a 1 KiB row slice, capped by
+// the largest power of two dividing kv_heads (so every wave has a head).
+template <typename T, int D>
+constexpr int decode_max_heads() {
+  return (kWave * 16) / (D * Elt<T>::kBytes) > kDecodeWaves ? kDecodeWaves : (kWave * 16) / (D * Elt<T>::kBytes);
+}
+
+constexpr int kDecodeLdsBudget = 160 * 1024;
+
+template <typename T, int D, int kHeads>
+constexpr int decode_stages() {
+  constexpr int per_stage = 2 * GroupTile<T, D, kHeads>::kBytes;
+  return kDecodeLdsBudget / per_stage >= 4 ? 4 : (kDecodeLdsBudget / per_stage >= 3 ? 3 : 2);
+}
+
+// One workgroup = one (sequence, key split, head group); wave w handles KV
+// head group*kHeads + w and its GQA query heads.
+template <typename T, int D, bool kUniform, int kHeads>
+__global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs a) {
   using F = Frag<T, D>;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kDecodeWaves][kTileKeys * kPitch];
+  using GT = GroupTile<T, D, kHeads>;
+  constexpr int kStages = decode_stages<T, D, kHeads>();
+  constexpr int kStageBytes = 2 * GT::kBytes;  // K tile then V tile
+  constexpr int kOwnOps = 2 * GT::kOpsPerWave;  // DMA ops one wave issues per tile
+  constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char ring[kStages][kStageBytes];
 
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
@@ -507,9 +740,9 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void paged_decode_kernel(Decod
   int64_t b, split, first_item, nsplit;
   locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s); },
               &b, &split, &first_item, &nsplit);
-  if (b < 0) return;
-  const int h = (int)blockIdx.y * kDecodeWaves + wave;
-  if (h >= a.geom.kv_heads) return;
+  if (b < 0) return;  // uniform over the workgroup
+  const int h0 = (int)blockIdx.y * kHeads;  // first KV head of the group
+  const int h = h0 + wave;
 
   const int seq_len = a.seq_lens[b];
   const int32_t* table = a.tables + b * a.table_stride;
@@ -518,16 +751,15 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void paged_decode_kernel(Decod
   const int key_end = min(key_begin + a.tiles_per_split * kTileKeys, seq_len);
   const int last = key_end - 1;
 
-  // Lane-specific base pointers: this lane's K slice and V chunk of head h.
-  const T* kc = reinterpret_cast<const T*>(a.k_cache) + h * D + g * (D / 4);
-  const T* vc = reinterpret_cast<const T*>(a.v_cache) + h * D + (lane % kChunksPerRow) * kEltPerChunk;
+  const T* kc = reinterpret_cast<const T*>(a.k_cache) + h0 * D;
+  const T* vc = reinterpret_cast<const T*>(a.v_cache) + h0 * D;
 
   // Q^T operand: row -> query head h*group + row (rows >= group are zero).
   F qf;
   const bool row_valid = row < a.group;
   const int qh = h * a.group + row;
   if (row_valid) {
-    load_vecs(qf.v, reinterpret_cast<const T*>(a.q) + b * a.q_sb + qh * a.q_sh + g * (D / 4));
+    load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + b * a.q_sb + qh * a.q_sh);
   } else {
 #pragma unroll
     for (int i = 0; i < F::kVec; ++i) qf.v[i] = uint4{0u, 0u, 0u, 0u};
@@ -535,62 +767,124 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void paged_decode_kernel(Decod
 
   SoftmaxState<D> st;
   st.init();
-  unsigned char* vt = lds[wave];
 
-  // Register double buffer of whole tiles (K slice = A operand, V chunks).
-  // Tiles are passed by value and every prefetch is unconditional (past the
-  // end it re-reads the split's last tile, an L2 hit), which keeps both
-  // buffers in VGPRs.  Keys past the end of the sequence are clamped to the
-  // last valid key, so no lane reads a slot the sequence does not own; those
-  // keys are masked to p = 0.
-  struct Tile {
-    F k;
-    uint4 v[kPasses];
-  };
-  auto fetch = [&](int key0) {
-    Tile tl;
-    TileAddr<kUniform> ta;
-    ta.init(a.geom, table, tlen, key0);
+  TableCache tc;
+  if constexpr (kUniform) tc.load(table, tlen, key_begin >> a.geom.bs_shift);
+
+  // This wave's share of the DMA ops of a tile: op = wave + i*kHeads; in op
+  // `op`, lane l fills LDS position op*64 + l, i.e. row r = op*kRowsPerOp +
+  // l/kChunks, chunk position l%kChunks, which holds global chunk
+  // position ^ swz(r).  Keys past the end of the split are clamped to its
+  // last key (so no lane reads a slot the sequence does not own; those keys
+  // are masked to p = 0).
+  auto issue = [&](int slot, int key0) {
+    TileAddr<kUniform, false> ta;  // a split covers <= 64 tiles, so <= 64 blocks
+    ta.init(a.geom, table, tlen, tc, key0);
     const int lim = last - key0;
-    load_vecs(tl.k.v, kc + ta.at(a.geom, table, tlen, key0, min(row, lim)));
+    unsigned char* kdst = &ring[slot][0];
+    unsigned char* vdst = kdst + GT::kBytes;
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int r = min(p * kRowsPerPass + lane / kChunksPerRow, lim);
-      tl.v[p] = *reinterpret_cast<const uint4*>(vc + ta.at(a.geom, table, tlen, key0, r));
+    for (int i = 0; i < GT::kOpsPerWave; ++i) {
+      const int op = wave + i * kHeads;
+      const int r = op * GT::kRowsPerOp + lane / GT::kChunks;
+      const int chunk = (lane % GT::kChunks) ^ GT::swz(r);
+      const int64_t src = ta.at(a.geom, table, tlen, key0, min(r, lim)) + chunk * kEltPerChunk;
+      lds_dma16(kc + src, kdst + op * kWave * 16);
+      lds_dma16(vc + src, vdst + op * kWave * 16);
     }
-    return tl;
   };
-  auto consume = [&](const Tile& tl, int key0) {
-    // Stage V into this wave's LDS rows ([key][dim]) for the transposed read.
+
+  // Per-lane LDS offsets inside a stage (tile independent): the K slice
+  // chunks and the sixteen V^T elements of the bf16 path.
+  uint32_t koff[F::kVec];
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int r = p * kRowsPerPass + lane / kChunksPerRow;
-      *reinterpret_cast<uint4*>(vt + r * kPitch + (lane % kChunksPerRow) * 16) = tl.v[p];
+  for (int j = 0; j < F::kVec; ++j) {
+    koff[j] = GT::chunk_offset(row, (wave * D * Elt<T>::kBytes + 64 * j + 16 * g) >> 4);
+  }
+  uint32_t voff[(D / 16) * 4];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, wave, 16 * c + row);
+  }
+
+  auto consume = [&](int slot, int key0) {
+    const unsigned char* stage = &ring[slot][0];
+    F kf;
+    if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t base = lds_off(stage);
+      uint32_t ka[F::kVec];
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) ka[j] = base + koff[j];
+      ring_read_k<F::kVec>(kf.v, ka);
+    } else {
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
     }
-    v4f s = qk_mfma<T, D>(tl.k, qf);
+    v4f s = qk_mfma<T, D>(kf, qf);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      s[i] = (key0 + 4 * g + i <= last) ? scaled_score<T>(s[i], a.scale) : kNegInf;
+      const float v = scaled_score<T>(s[i], a.scale);
+      s[i] = (key0 + 4 * g + i <= last) ? v : kNegInf;
     }
     softmax_tile<D>(st, s);
-    pv_mfma<T, D>(st, vt, kPitch, s);
+    if constexpr (Elt<T>::kIsBf16) {
+      v4s pb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pb[i] = (short)f32_to_bf16_bits(s[i]);
+      const uint32_t base = lds_off(stage);
+#pragma unroll
+      for (int c0 = 0; c0 < D / 16; c0 += 4) {
+        uint32_t va[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) va[i] = base + voff[4 * c0 + i];
+        v4s vt[4];
+        ring_read_vt16(vt, va);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          st.o[c0 + c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[c], pb, st.o[c0 + c], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = *reinterpret_cast<const float*>(stage + voff[4 * c + j]);
+          st.o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(v, s[j], st.o[c], 0, 0, 0);
+        }
+      }
+    }
   };
 
   const int ntiles = (key_end - key_begin + kTileKeys - 1) / kTileKeys;
   const int last_key0 = key_begin + (ntiles - 1) * kTileKeys;
-  Tile t0 = fetch(key_begin);
-  for (int t = 0; t < ntiles; t += 2) {
-    const int key0 = key_begin + t * kTileKeys;
-    const Tile t1 = fetch(min(key0 + kTileKeys, last_key0));
-    consume(t0, key0);
-    if (t + 1 >= ntiles) break;
-    t0 = fetch(min(key0 + 2 * kTileKeys, last_key0));
-    consume(t1, key0 + kTileKeys);
+  constexpr int kAhead = kStages - 1;
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) issue(j, min(key_begin + j * kTileKeys, last_key0));
+  for (int t = 0; t < ntiles; t += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) {
+      const int tt = t + j;
+      if (tt >= ntiles) break;  // uniform over the workgroup
+      // this wave's ops for tile tt are done once at most the kAhead-1 later
+      // tiles' ops are outstanding; the barrier extends that to every wave
+      // and guarantees that every wave has finished reading tile tt-1
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((kAhead - 1) * kOwnOps));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue((j + kAhead) % kStages, min(key_begin + (tt + kAhead) * kTileKeys, last_key0));
+      __builtin_amdgcn_sched_barrier(0);
+      consume(j, key_begin + tt * kTileKeys);
+    }
   }
 
+  // Drain the redundant prefetches issued past the last tile before this
+  // workgroup's LDS can be handed to another one.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   const float lsum = sum_over_groups(st.lsum);
-  if (!row_valid) return;
   if (nsplit == 1) {
+    if (!row_valid) return;
     const float inv = 1.f / lsum;
     T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * g;
 #pragma unroll
@@ -598,64 +892,39 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void paged_decode_kernel(Decod
       store4<T>(dst + 16 * c, st.o[c][0] * inv, st.o[c][1] * inv, st.o[c][2] * inv,
                 st.o[c][3] * inv);
     }
-  } else {
-    const int64_t item = first_item + split;
-    // Only reachable with a workspace; the bound keeps inconsistent length
-    // hints from writing outside it.
-    if (a.ws_o == nullptr || item >= a.ws_items) return;
-    float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      *reinterpret_cast<float4*>(dst + 16 * c) = make_float4(st.o[c][0], st.o[c][1], st.o[c][2], st.o[c][3]);
-    }
-    if (g == 0) {
-      float* ml = a.ws_ml + (item * a.q_heads + qh) * 2;
-      ml[0] = st.m;
-      ml[1] = lsum;
-    }
+    return;
   }
+  // Split-K: store this split's partial (unnormalised O, running max, sum)
+  // for the merge kernel.  The bound keeps inconsistent length hints from
+  // writing outside the workspace.
+  const int64_t item = first_item + split;
+  if (!row_valid || a.ws_o == nullptr || item >= a.ws_items) return;
+  float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+    *reinterpret_cast<float4*>(dst + 16 * c) = make_float4(st.o[c][0], st.o[c][1], st.o[c][2], st.o[c][3]);
+  }
+  if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
 }
 
-// grid (batch, ceil(q_heads/4)), 4 waves: one wave per (sequence, query
-// head) merges that row's split partials in fp32.
+// Split merge: one wave per (sequence, query head); sequences with a single
+// split were finished by the decode kernel.  The sequence's first item is
+// the sum of the split counts of the sequences before it.
+constexpr int kMergeWaves = 4;
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  const int lane = lane_id();
+__global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(DecodeArgs a) {
   const int64_t b = blockIdx.x;
-  const int qh = (int)blockIdx.y * 4 + (int)(threadIdx.x / kWave);
-  if (b >= a.batch) return;
-  // first item of sequence b = number of items of the sequences before it
-  int64_t first = 0;
-  for (int64_t b0 = 0; b0 < b; b0 += kWave) {
-    const int64_t s = b0 + lane;
-    int64_t n = (s < b) ? decode_splits_of(a, s) : 0;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) n += __shfl_xor(n, off);
-    first += n;
-  }
+  const int qh = (int)blockIdx.y * kMergeWaves + (int)(threadIdx.x / kWave);
+  if (qh >= a.q_heads) return;
   const int64_t nsplit = decode_splits_of(a, b);
-  if (qh >= a.q_heads || nsplit <= 1 || a.ws_o == nullptr || first + nsplit > a.ws_items) return;
-  float mmax = kNegInf;
-  for (int64_t s = 0; s < nsplit; ++s) {
-    mmax = fmaxf(mmax, a.ws_ml[((first + s) * a.q_heads + qh) * 2]);
-  }
-  constexpr int kPerLane = D / kWave;
-  float denom = 0.f;
-  float acc[kPerLane];
+  if (nsplit <= 1) return;
+  int64_t first = 0;
+  for (int64_t s = lane_id(); s < b; s += kWave) first += decode_splits_of(a, s);
 #pragma unroll
-  for (int j = 0; j < kPerLane; ++j) acc[j] = 0.f;
-  for (int64_t s = 0; s < nsplit; ++s) {
-    const int64_t idx = (first + s) * a.q_heads + qh;
-    const float m = a.ws_ml[idx * 2];
-    const float w = (m == kNegInf) ? 0.f : exp2f((m - mmax) * kLog2e);
-    denom += w * a.ws_ml[idx * 2 + 1];
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) acc[j] += w * a.ws_o[idx * D + j * kWave + lane];
-  }
-  const float inv = 1.f / denom;
-  T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh;
-#pragma unroll
-  for (int j = 0; j < kPerLane; ++j) store_elt<T>(dst + j * kWave + lane, acc[j] * inv);
+  for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
+  if (first + nsplit > a.ws_items) return;
+  merge_splits<T, D>(a, b, first, (int)nsplit, qh, 1);
 }
 
 // Work decomposition of a decode call: 16-key tiles per split chosen so the
@@ -663,13 +932,27 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 // (two resident workgroups on each of the 256 CUs).
 constexpr int64_t kDecodeTargetItems = 512;
 constexpr int64_t kDecodeMinTilesPerSplit = 4;
+constexpr int64_t kDecodeMaxTilesPerSplit = 64;  // the per-split block-table window (one VGPR)
+
+// NIE_DECODE_TARGET_ITEMS overrides the work-item target for tuning.
+int64_t decode_target_items() {
+  static const int64_t target = [] {
+    const char* env = getenv("NIE_DECODE_TARGET_ITEMS");
+    const long long v = env ? atoll(env) : 0;
+    return v > 0 ? (int64_t)v : kDecodeTargetItems;
+  }();
+  return target;
+}
 
 int64_t decode_tiles_per_split(int64_t batch, int64_t total_seq_len) {
   const int64_t total_tiles = cdiv(total_seq_len, kTileKeys) + batch;
-  const int64_t tps = cdiv(total_tiles, kDecodeTargetItems);
-  return tps < kDecodeMinTilesPerSplit ? kDecodeMinTilesPerSplit : tps;
+  int64_t tps = cdiv(total_tiles, decode_target_items());
+  tps = tps < kDecodeMinTilesPerSplit ? kDecodeMinTilesPerSplit : tps;
+  return tps > kDecodeMaxTilesPerSplit ? kDecodeMaxTilesPerSplit : tps;
 }
 
+// Workspace layout of a decode call: the partial O rows (items x q_heads x
+// head_dim floats), then (max, sum) pairs (items x q_heads x 2 floats).
 int64_t decode_max_items(int64_t batch, int64_t total_seq_len, int64_t tps) {
   // sum_b ceil(ceil(len_b/16)/tps) <= (sum_b len_b/16 + batch)/tps + batch
   return (cdiv(total_seq_len, kTileKeys) + batch) / tps + batch + 1;
@@ -744,7 +1027,7 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
 
   F qf;
   if (row_valid) {
-    load_vecs(qf.v, reinterpret_cast<const T*>(a.q) + (q_begin + tq) * a.q_st + qh * a.q_sh + g * (D / 4));
+    load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + (q_begin + tq) * a.q_st + qh * a.q_sh);
   } else {
 #pragma unroll
     for (int i = 0; i < F::kVec; ++i) qf.v[i] = uint4{0u, 0u, 0u, 0u};
@@ -754,9 +1037,11 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
   const T* vc = reinterpret_cast<const T*>(a.v_cache) + h * D;
 
   uint4 stage[kLoadsPerThread];
+  TableCache tc;
+  if constexpr (kUniform) tc.load(table, tlen, 0);
   auto fetch = [&](int key0) {
-    TileAddr<kUniform> ta;
-    ta.init(a.geom, table, tlen, key0);
+    TileAddr<kUniform, true> ta;
+    ta.init(a.geom, table, tlen, tc, key0);
     const int lim = key_end - 1 - key0;
 #pragma unroll
     for (int j = 0; j < kLoadsPerThread; ++j) {
@@ -790,13 +1075,14 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
     __syncthreads();
     fetch(min(key0 + kTileKeys, (ntiles - 1) * kTileKeys));  // past the end: re-read (L2 hit)
     F kf;
-    load_vecs(kf.v, k_lds + row * kPitch + g * F::kBytes);
+    load_slice<T, D>(kf, k_lds + row * kPitch);
     v4f s = qk_mfma<T, D>(kf, qf);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // S^T C-layout: this value is key key0 + 4g + i of this lane's row.
       const int key = key0 + 4 * g + i;
-      s[i] = (key <= q_pos && key < key_end) ? scaled_score<T>(s[i], a.scale) : kNegInf;
+      const float v = scaled_score<T>(s[i], a.scale);
+      s[i] = (key <= q_pos && key < key_end) ? v : kNegInf;
     }
     softmax_tile<D>(st, s);
     pv_mfma<T, D>(st, v_lds, kPitch, s);
@@ -874,27 +1160,46 @@ CacheGeom make_geom(int64_t layer_index, int64_t num_blocks, int64_t block_size,
   return g;
 }
 
-template <typename T, int D, bool U>
-void launch_decode_t(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
-  const dim3 grid((unsigned)items, (unsigned)cdiv(a.geom.kv_heads, kDecodeWaves));
-  const int waves = a.geom.kv_heads < kDecodeWaves ? a.geom.kv_heads : kDecodeWaves;
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, U>), grid, dim3(waves * kWave), 0, stream, a);
+// One wave-uniform block lookup per tile needs the tile inside one block:
+// block_size a power of two of at least 16.
+bool uniform_tiles(const CacheGeom& g) { return g.bs_shift >= 4; }
+
+template <typename T, int D, bool U, int H>
+void launch_decode_h(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
+  const dim3 grid((unsigned)items, (unsigned)(a.geom.kv_heads / H));
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a);
   if (merge) {
-    const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv(a.q_heads, 4));
-    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(256), 0, stream, a);
+    const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv((int64_t)a.q_heads, (int64_t)kMergeWaves));
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a);
+  }
+}
+
+// Heads per workgroup: the largest power of two that divides kv_heads, up to
+// the number that fills a 1 KiB row slice.
+template <typename T, int D, bool U>
+void launch_decode_u(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
+  constexpr int kMax = decode_max_heads<T, D>();
+  const int hkv = a.geom.kv_heads;
+  int heads = 1;
+  while (heads * 2 <= kMax && hkv % (heads * 2) == 0) heads *= 2;
+  switch (heads) {
+    case 1: launch_decode_h<T, D, U, 1>(a, items, stream, merge); break;
+    case 2: launch_decode_h<T, D, U, (kMax >= 2 ? 2 : 1)>(a, items, stream, merge); break;
+    case 4: launch_decode_h<T, D, U, (kMax >= 4 ? 4 : 1)>(a, items, stream, merge); break;
+    default: launch_decode_h<T, D, U, (kMax >= 8 ? 8 : 1)>(a, items, stream, merge); break;
   }
 }
 
 template <typename T, int D>
 void launch_decode(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
-  if (a.geom.block_size % kTileKeys == 0) launch_decode_t<T, D, true>(a, items, stream, merge);
-  else launch_decode_t<T, D, false>(a, items, stream, merge);
+  if (uniform_tiles(a.geom)) launch_decode_u<T, D, true>(a, items, stream, merge);
+  else launch_decode_u<T, D, false>(a, items, stream, merge);
 }
 
 template <typename T, int D>
 void launch_prefill(const PrefillArgs& a, int64_t tiles, hipStream_t stream) {
   const dim3 grid((unsigned)tiles, (unsigned)a.geom.kv_heads);
-  if (a.geom.block_size % kTileKeys == 0) {
+  if (uniform_tiles(a.geom)) {
     hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
   } else {
     hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
@@ -1057,7 +1362,7 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
   const int64_t items = decode_max_items(batch, total_seq_len, tps);
   const bool may_split = cdiv(max_seq_len, kTileKeys) > tps;
   const int64_t need = items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
-  if (may_split && (workspace == nullptr || workspace_bytes < need)) {
+  if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,
                 (long long)workspace_bytes);
   }

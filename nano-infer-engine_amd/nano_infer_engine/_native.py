@@ -94,6 +94,23 @@ _SIGNATURES = {
 _lib: ctypes.CDLL | None = None
 _lib_lock = threading.Lock()
 
+# Decode workspaces (split partials), one per (device, stream), grown as
+# needed and reused: calls on one stream are ordered, so they can share a
+# buffer; calls on different streams cannot.
+_decode_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_workspace_lock = threading.Lock()
+
+
+def _decode_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    with _workspace_lock:
+        ws = _decode_workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            size = max(nbytes, 1 << 20, 0 if ws is None else 2 * ws.numel())
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            _decode_workspaces[key] = ws
+    return ws
+
 
 def library_path() -> str:
     """Path of the in-tree built library."""
@@ -332,7 +349,8 @@ def paged_decode(
         return out
     lib = load_library()
     ws_bytes = lib.nie_paged_decode_workspace_bytes(batch, q_heads, head_dim, block_size, max_seq_len, total_seq_len)
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    stream = _stream(query.device)
+    workspace = _decode_workspace(query.device, stream, ws_bytes)
     rc = lib.nie_paged_decode(
         dtype_code(query.dtype),
         query.data_ptr(), query.stride(0), query.stride(1),
@@ -344,7 +362,7 @@ def paged_decode(
         float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
         workspace.data_ptr(), workspace.numel(),
-        _stream(query.device),
+        stream,
     )
     _check(rc, "nie_paged_decode")
     return out

@@ -193,6 +193,35 @@ def test_decode_ignores_garbage_past_length():
     assert (got.float() - want.float()).abs().max().item() <= 2e-2
 
 
+def test_decode_workspace_reuse_across_calls():
+    """Back-to-back launches share one workspace: split counters must be left at zero.
+
+    Calls alternate between a long-context batch (many splits per sequence)
+    and a short one, with no host synchronisation between them; every output
+    is checked against the oracle afterwards.
+    """
+    _log("decode workspace reuse")
+    cases = [workloads.decode_ragged(seed=s) for s in (1, 3)] + [workloads.decode_small()]
+    prepared = []
+    for wl in cases:
+        kc, vc = wl.pool(torch.bfloat16)
+        q, _, _ = wl.new_tokens(torch.bfloat16)
+        prepared.append((wl, kc, vc, q, kc.to(DEV), vc.to(DEV), q.to(DEV),
+                         torch.from_numpy(wl.table_array()).to(DEV),
+                         torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)))
+    outs = []
+    for rep in range(3):
+        for wl, _, _, _, dk, dv, dq, tables, lens in prepared:
+            outs.append(_native.paged_decode(dq, dk, dv, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens),
+                                             wl.head_dim**-0.5))
+    torch.cuda.synchronize()
+    for i, got in enumerate(outs):
+        wl, kc, vc, q = prepared[i % len(prepared)][:4]
+        err = (got.cpu().float() - _decode_oracle(wl, kc, vc, q).float()).abs().max().item()
+        _log(f"  call {i} max_abs_err={err:.3e}")
+        assert err <= 2e-2
+
+
 def _prefill_case(wl, dtype):
     kc, vc = wl.pool(dtype)
     q, k_new, v_new = wl.new_tokens(dtype)
