@@ -1,0 +1,283 @@
+"""Host-side logic of the paged path (CPU only, no kernel launches).
+
+Restates the checks of the reference's own tests for the block allocator
+and the cache bookkeeping (``tests/test_block_allocator.py``,
+``tests/test_paged_cache.py:22-200``), plus the ragged-batch metadata that
+feeds the kernels, and that data movement refuses to run without a GPU.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nano_infer_engine import _native
+from nano_infer_engine.block_allocator import BlockAllocator
+from nano_infer_engine.layers.paged_attention import paged_attention_reference
+from nano_infer_engine.paged_batch import build_ragged_batch
+from nano_infer_engine.paged_cache import PagedKVCache, PagedKVTransfer
+from oracle import slots
+
+
+# ---------------------------------------------------------------------------
+# BlockAllocator (tests/test_block_allocator.py)
+# ---------------------------------------------------------------------------
+def test_allocator_order_and_counts():
+    a = BlockAllocator(4)
+    assert (a.free_block_count, a.allocated_block_count) == (4, 0)
+    assert a.allocate(2) == [0, 1]
+    assert (a.free_block_count, a.allocated_block_count) == (2, 2)
+
+
+def test_allocator_reuses_freed_blocks_in_free_order():
+    a = BlockAllocator(4)
+    got = a.allocate(4)
+    a.free([got[1], got[3]])
+    assert a.allocate(2) == [got[1], got[3]]
+
+
+def test_allocator_failures_leave_state_unchanged():
+    a = BlockAllocator(2)
+    with pytest.raises(ValueError, match="not enough free blocks"):
+        a.allocate(3)
+    assert (a.free_block_count, a.allocated_block_count) == (2, 0)
+    b = a.allocate()[0]
+    with pytest.raises(ValueError, match="same block more than once"):
+        a.free([b, b])
+    assert (a.free_block_count, a.allocated_block_count) == (1, 1)
+    with pytest.raises(ValueError, match="block is not allocated"):
+        a.free([b, 1])
+    assert (a.free_block_count, a.allocated_block_count) == (1, 1)
+    a.free([b])
+    with pytest.raises(ValueError, match="block is not allocated"):
+        a.free([b])
+
+
+@pytest.mark.parametrize("bad,exc,msg", [(0, ValueError, "num_blocks must be positive"),
+                                         (-1, ValueError, "num_blocks must be positive"),
+                                         (True, TypeError, "num_blocks must be an integer"),
+                                         (1.5, TypeError, "num_blocks must be an integer")])
+def test_allocator_constructor_validation(bad, exc, msg):
+    with pytest.raises(exc, match=msg):
+        BlockAllocator(bad)
+
+
+@pytest.mark.parametrize("bad,exc,msg", [(0, ValueError, "block_count must be positive"),
+                                         (True, TypeError, "block_count must be an integer"),
+                                         (1.5, TypeError, "block_count must be an integer")])
+def test_allocator_allocate_validation(bad, exc, msg):
+    with pytest.raises(exc, match=msg):
+        BlockAllocator(2).allocate(bad)
+
+
+@pytest.mark.parametrize("bad,exc,msg", [(-1, ValueError, "block ID out of range"),
+                                         (2, ValueError, "block ID out of range"),
+                                         (True, TypeError, "block IDs must be integers"),
+                                         (1.5, TypeError, "block IDs must be integers")])
+def test_allocator_free_validation(bad, exc, msg):
+    with pytest.raises(exc, match=msg):
+        BlockAllocator(2).free([bad])
+
+
+# ---------------------------------------------------------------------------
+# PagedKVCache bookkeeping (tests/test_paged_cache.py:22-200)
+# ---------------------------------------------------------------------------
+def _cache(**kw):
+    args = dict(num_blocks=4, block_size=4, num_layers=2, kv_head_num=2, head_dim=4, dtype=torch.float32, device="cpu")
+    args.update(kw)
+    return PagedKVCache(**args)
+
+
+@pytest.mark.parametrize("tokens,blocks", [(1, 1), (4, 1), (5, 2), (8, 2), (9, 3)])
+def test_ensure_capacity_allocates_required_blocks(tokens, blocks):
+    c = _cache()
+    c.ensure_capacity("request-a", tokens)
+    assert len(c.get_block_table("request-a")) == blocks
+    assert c.allocator.allocated_block_count == blocks
+
+
+def test_ensure_capacity_is_incremental_and_tables_are_snapshots():
+    c = _cache()
+    c.ensure_capacity("request-a", 2)
+    first = c.get_block_table("request-a")
+    c.ensure_capacity("request-a", 4)
+    assert c.get_block_table("request-a") == first
+    c.ensure_capacity("request-a", 5)
+    assert isinstance(first, tuple) and len(first) == 1
+    assert c.get_block_table("request-a")[:1] == first and len(c.get_block_table("request-a")) == 2
+
+
+def test_lengths_advance_only_within_capacity():
+    c = _cache(num_blocks=2)
+    assert c.get_sequence_length("request-a") == 0
+    c.ensure_capacity("request-a", 4)
+    c.advance("request-a", 3)
+    c.advance("request-a", 1)
+    assert c.get_sequence_length("request-a") == 4
+    with pytest.raises(IndexError, match="exceeds allocated capacity"):
+        c.advance("request-a", 1)
+    assert c.get_sequence_length("request-a") == 4
+
+
+def test_failed_allocation_creates_no_table():
+    c = _cache(num_blocks=2)
+    c.ensure_capacity("request-a", 4)
+    existing = c.get_block_table("request-a")
+    with pytest.raises(ValueError, match="not enough free blocks"):
+        c.ensure_capacity("request-b", 8)
+    with pytest.raises(KeyError):
+        c.get_block_table("request-b")
+    assert c.get_block_table("request-a") == existing and c.allocator.free_block_count == 1
+
+
+def test_tables_of_sequences_are_disjoint_and_release_returns_blocks():
+    c = _cache()
+    c.ensure_capacity("request-a", 5)
+    c.ensure_capacity("request-b", 5)
+    a, b = c.get_block_table("request-a"), c.get_block_table("request-b")
+    assert set(a).isdisjoint(b)
+    c.release("request-a")
+    assert c.get_block_table("request-b") == b and c.allocator.allocated_block_count == 2
+    with pytest.raises(KeyError, match="request-a"):
+        c.release("request-a")
+    assert c.allocator.allocate(2) == list(a)
+
+
+def test_release_keeps_table_when_free_fails(monkeypatch):
+    c = _cache(num_blocks=2)
+    c.ensure_capacity("request-a", 4)
+    table = c.get_block_table("request-a")
+
+    def boom(ids):
+        raise RuntimeError("simulated allocator failure")
+
+    monkeypatch.setattr(c.allocator, "free", boom)
+    with pytest.raises(RuntimeError, match="simulated allocator failure"):
+        c.release("request-a")
+    assert c.get_block_table("request-a") == table
+
+
+@pytest.mark.parametrize("sid,exc,msg", [(None, TypeError, "sequence_id must be a string"),
+                                         (1, TypeError, "sequence_id must be a string"),
+                                         ("", ValueError, "sequence_id must not be empty")])
+def test_sequence_id_validation(sid, exc, msg):
+    c = _cache()
+    for call in (lambda: c.get_block_table(sid), lambda: c.ensure_capacity(sid, 1),
+                 lambda: c.get_sequence_length(sid), lambda: c.release(sid)):
+        with pytest.raises(exc, match=msg):
+            call()
+
+
+@pytest.mark.parametrize("n,exc,msg", [(0, ValueError, "required_tokens must be positive"),
+                                       (-1, ValueError, "required_tokens must be positive"),
+                                       (True, TypeError, "required_tokens must be an integer"),
+                                       (1.5, TypeError, "required_tokens must be an integer")])
+def test_required_tokens_validation(n, exc, msg):
+    with pytest.raises(exc, match=msg):
+        _cache().ensure_capacity("request-a", n)
+
+
+def test_cache_constructor_validation():
+    for name in ("num_blocks", "block_size", "num_layers", "kv_head_num", "head_dim"):
+        with pytest.raises(ValueError, match=f"{name} must be positive"):
+            _cache(**{name: 0})
+        with pytest.raises(TypeError, match=f"{name} must be an integer"):
+            _cache(**{name: 2.0})
+
+
+def test_write_validates_before_touching_the_device():
+    c = _cache()
+    c.ensure_capacity("request-a", 4)
+    k = torch.zeros(2, 2, 4)
+    with pytest.raises(IndexError, match="layer_index out of range"):
+        c.write(2, "request-a", 0, k, k)
+    with pytest.raises(ValueError, match="identical shapes"):
+        c.write(0, "request-a", 0, k, torch.zeros(1, 2, 4))
+    with pytest.raises(ValueError, match="cache dtype"):
+        c.write(0, "request-a", 0, k.double(), k.double())
+    with pytest.raises(IndexError, match="exceeds allocated capacity"):
+        c.write(0, "request-a", 3, k, k)
+
+
+def test_import_rejects_incompatible_layout_without_allocating():
+    c = _cache(num_blocks=2)
+    transfer = PagedKVTransfer("request-a", 1, 8, 2, 2, 4, torch.empty(2, 1, 8, 2, 4), torch.empty(2, 1, 8, 2, 4))
+    with pytest.raises(ValueError, match="layout does not match"):
+        c.import_sequence("request-a", transfer)
+    assert c.allocator.allocated_block_count == 0
+
+
+def test_data_movement_without_gpu_fails_loudly():
+    """No CPU fallback: moving K/V on a non-GPU cache raises RuntimeError."""
+    c = _cache()
+    c.ensure_capacity("request-a", 4)
+    k = torch.zeros(2, 2, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        c.write(0, "request-a", 0, k, k)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        c.gather(0, "request-a", 2)
+    q = torch.zeros(4, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        paged_attention_reference(q, c.keys, c.values, c.get_block_table("request-a"), 2, 0)
+
+
+# ---------------------------------------------------------------------------
+# ragged batch metadata
+# ---------------------------------------------------------------------------
+def test_ragged_batch_metadata_matches_closed_form():
+    c = _cache(num_blocks=16, block_size=4)
+    plan = {"p0": (0, 6), "p1": (5, 3), "d0": (9, 1), "d1": (2, 1)}
+    for sid, (ctx, n) in plan.items():
+        c.ensure_capacity(sid, ctx + n)
+        if ctx:
+            c.advance(sid, ctx)
+    ids = tuple(plan)
+    batch = build_ragged_batch(c, ids, tuple(n for _, n in plan.values()))
+    tables = [c.get_block_table(s) for s in ids]
+    ctx = [plan[s][0] for s in ids]
+    qlen = [plan[s][1] for s in ids]
+    assert batch.slot_mapping.tolist() == slots.slot_mapping(tables, ctx, qlen, 4).tolist()
+    assert batch.cu_seqlens.tolist() == [0, 6, 9, 10, 11]
+    assert batch.positions.tolist() == [0, 1, 2, 3, 4, 5, 5, 6, 7, 9, 2]
+    assert batch.context_lens_t.tolist() == ctx
+    assert batch.seq_lens_t.tolist() == [6, 8, 10, 3]
+    assert batch.decode_from == 2
+    for r, t in enumerate(tables):
+        assert batch.block_tables[r, : len(t)].tolist() == list(t)
+    # a token past the allocated capacity is refused before anything is built
+    with pytest.raises(IndexError, match="exceeds allocated capacity"):
+        build_ragged_batch(c, ("d1",), (3,))
+
+
+# ---------------------------------------------------------------------------
+# the C ABI library (loads and exports; no compute without a GPU)
+# ---------------------------------------------------------------------------
+def _header_symbols():
+    import os
+    import re
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "nie_paged.h")
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nie_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _native.load_library()
+    declared = _header_symbols()
+    assert declared == sorted(_native.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.nie_version().decode().startswith("nie_paged")
+
+
+def test_library_workspace_queries():
+    lib = _native.load_library()
+    # decode partials: items * q_heads * (head_dim + 2) floats, items bounded by the split count
+    small = lib.nie_paged_decode_workspace_bytes(4, 32, 64, 16, 500, 710)
+    assert small > 0 and small % 4 == 0
+    big = lib.nie_paged_decode_workspace_bytes(16, 32, 64, 16, 29600, 16 * 29600)
+    assert big >= small
+    assert lib.nie_paged_decode_workspace_bytes(0, 32, 64, 16, 1, 1) == 0
+    assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 64) >= 0
