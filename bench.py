@@ -41,6 +41,10 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
     p.add_argument("--skip-stress", action="store_true", help="do not run the 16x29600 decode figure")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
+    p.add_argument("--stress-only", action="store_true",
+                   help="run only the 16x29600 decode figure (for per-workload profiles)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run 4 device-to-device copies of MIB MiB (reference for HBM byte counters)")
     return p.parse_args()
 
 
@@ -179,7 +183,7 @@ def run_gpu(args):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_kernel (+ decode_merge_kernel inside the timed launch)",
+            "kernel": "nie_paged_decode call: paged_decode_kernel + decode_merge_kernel (HIP events around the call)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -226,7 +230,7 @@ def run_stress(args):
 
 def _measured_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if present."""
-    path = os.path.join(REPO, "profiles", "paged_decode_traffic.json")
+    path = os.path.join(REPO, "profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json")
     try:
         with open(path) as f:
             return json.load(f).get("hbm_bytes_per_launch")
@@ -268,12 +272,34 @@ def run_cpu_baseline(args):
     }
 
 
+def run_copy_calibration(mib: int):
+    """A plain copy of known size: each launch reads and writes mib MiB."""
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n, "launches": 4}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the path runs on a single MI355X).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        run_copy_calibration(args.copy_calibration)
+        return
+    if args.stress_only:
+        from nano_infer_engine import _native
+
+        _native.load_library()
+        print(json.dumps({"stress_16x29600": run_stress(args)}), flush=True)
+        return
     result = run_gpu(args)
     result["cpu_baseline"] = None if args.skip_cpu else run_cpu_baseline(args)
     print(json.dumps(result), flush=True)
