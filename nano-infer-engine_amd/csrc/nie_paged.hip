@@ -6,8 +6,8 @@
 //   kv_copy_blocks_kernel   whole-block copies (export / import of sequences)
 //   paged_decode_kernel     split-K decode attention, one workgroup per
 //                           (sequence, key split, KV-head group), one wave
-//                           per KV head; the last split of a sequence to
-//                           finish merges the partials (exact fp32)
+//                           per KV head
+//   decode_merge_kernel     exact fp32 merge of the split partials
 //   varlen_prefill_kernel   chunked-prefill attention over packed varlen rows
 //
 // Attention math (both attention kernels) runs on the matrix cores with the
@@ -928,8 +928,8 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
 }
 
 // Work decomposition of a decode call: 16-key tiles per split chosen so the
-// batch yields about kDecodeTargetItems workgroups per group of 8 KV heads
-// (two resident workgroups on each of the 256 CUs).
+// batch yields about kDecodeTargetItems work items (each one workgroup per
+// KV-head group), two rounds of workgroups over the 256 CUs.
 constexpr int64_t kDecodeTargetItems = 512;
 constexpr int64_t kDecodeMinTilesPerSplit = 4;
 constexpr int64_t kDecodeMaxTilesPerSplit = 64;  // the per-split block-table window (one VGPR)
