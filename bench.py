@@ -101,20 +101,24 @@ class DecodeBench:
         self.scale = wl.head_dim**-0.5
 
     def step(self, s: int, events: list | None = None) -> None:
-        """One decode step over every layer; optionally brackets each decode launch with HIP events."""
+        """One decode step over every layer; optionally brackets each decode launch with HIP events.
+
+        The append and decode launches are prepared once per step and reused
+        by every layer, as a model forward does (``RaggedBatch.launchers``).
+        """
         import torch
 
         from nano_infer_engine import _native
 
+        append = _native.PreparedAppend(self.k_cache, self.v_cache, self.slots[s])
+        decode = _native.PreparedDecode(self.k_cache, self.v_cache, self.tables, self.lens[s], self.max_len[s],
+                                        self.total_len[s], self.wl.q_heads, self.scale)
         for layer in range(self.wl.num_layers):
-            _native.kv_append(self.k_cache, self.v_cache, layer, self.k_new, self.v_new, self.slots[s])
+            append(self.k_new, self.v_new, layer)
             if events is not None:
                 start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 start.record()
-            _native.paged_decode(
-                self.q, self.k_cache, self.v_cache, layer, self.tables, self.lens[s],
-                self.max_len[s], self.total_len[s], self.scale, out=self.out,
-            )
+            decode(self.q, layer, self.out)
             if events is not None:
                 end.record()
                 events.append((start, end))

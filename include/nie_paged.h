@@ -116,14 +116,16 @@ int nie_kv_copy_blocks(int dtype,
                        void* stream);
 
 /*
- * Workspace bytes needed by nie_paged_decode for a batch whose sequence
- * lengths have maximum max_seq_len and sum total_seq_len (host values).
+ * Workspace bytes needed by nie_paged_decode for a call with these
+ * arguments (same meaning as there; host values), whose sequence lengths
+ * have maximum max_seq_len and sum total_seq_len.  The split of the work
+ * depends on all of them, so query with the values of the call.
  * Layout: fp32 split partials (unnormalised O rows, then (max, sum) pairs).
- * The pointer must be 16-byte aligned.  May be 0 when no sequence splits.
+ * The pointer must be 16-byte aligned.  Returns 0 for invalid arguments.
  */
-int64_t nie_paged_decode_workspace_bytes(int64_t batch, int64_t q_heads,
-                                         int64_t head_dim, int64_t block_size,
-                                         int64_t max_seq_len,
+int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,
+                                         int64_t kv_heads, int64_t head_dim,
+                                         int64_t block_size, int64_t max_seq_len,
                                          int64_t total_seq_len);
 
 /*

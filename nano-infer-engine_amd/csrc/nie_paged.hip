@@ -642,66 +642,75 @@ __device__ __forceinline__ void ring_read_vt16(v4s (&a)[4], const uint32_t (&add
   }
 }
 
-// Merges the split partials of `rows` consecutive query heads (starting at
-// qh0) of sequence b, one wave: weights exp(m_s - max) one split per lane,
-// O rows read as float4 by D/4 lanes per split, several splits per load
-// instruction, all rows' loads issued before any is consumed.
+// Merges the split partials of query head qh of sequence b, one wave.  The
+// lanes form kSplitsPerPass groups of D/4 lanes; a group reads one split's
+// O row as float4s.  Splits go in batches of kPasses * kSplitsPerPass: every
+// load of a batch (the O rows, and one (max, sum) pair per lane) is issued
+// before any is used, and batches combine through a running maximum, so the
+// usual merge (<= 32 splits at head_dim 64) costs one memory round trip.
 template <typename T, int D>
-__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int64_t b, int64_t first, int nsplit,
-                                             int qh0, int rows) {
+__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int64_t b, int64_t first, int nsplit, int qh) {
   constexpr int kLanesPerSplit = D / 4;
   constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
+  constexpr int kPasses = 8;
+  constexpr int kBatch = kPasses * kSplitsPerPass;
+  static_assert(kBatch <= kWave, "one (max, sum) pair per lane");
   const int lane = lane_id();
   const int sub = lane / kLanesPerSplit;
   const int chunk = lane % kLanesPerSplit;
   const int64_t ml_stride = (int64_t)a.q_heads * 2;
   const int64_t po_stride = (int64_t)a.q_heads * D;
-  for (int r = 0; r < rows; ++r) {
-    const int qh = qh0 + r;
-    const float* ml = a.ws_ml + (first * a.q_heads + qh) * 2;
-    const float* po = a.ws_o + (first * a.q_heads + qh) * D;
-    float mmax = kNegInf;
-    for (int s = lane; s < nsplit; s += kWave) mmax = fmaxf(mmax, ml[s * ml_stride]);
+  const float* ml = a.ws_ml + (first * a.q_heads + qh) * 2;
+  const float* po = a.ws_o + (first * a.q_heads + qh) * D + 4 * chunk;
+  float run_max = kNegInf;
+  float denom = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+    const int count = min(kBatch, nsplit - s0);
+    float4 v[kPasses];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
-    float denom = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < nsplit; s0 += kWave) {
-      const int s_lane = s0 + lane;
-      float w = 0.f;
-      if (s_lane < nsplit) {
-        const float m = ml[s_lane * ml_stride];
-        w = (m == kNegInf) ? 0.f : exp2f((m - mmax) * kLog2e);
-        denom += w * ml[s_lane * ml_stride + 1];
-      }
-      const int count = min(kWave, nsplit - s0);
-#pragma unroll 8
-      for (int k = 0; k < count; k += kSplitsPerPass) {
-        const int s = k + sub;
-        const float ws = __shfl(w, s < kWave ? s : 0);
-        if (s < count) {
-          const float4 v = *reinterpret_cast<const float4*>(po + (s0 + s) * po_stride + 4 * chunk);
-          acc.x += ws * v.x;
-          acc.y += ws * v.y;
-          acc.z += ws * v.z;
-          acc.w += ws * v.w;
-        }
-      }
+    for (int p = 0; p < kPasses; ++p) {
+      const int sp = p * kSplitsPerPass + sub;
+      v[p] = sp < count ? *reinterpret_cast<const float4*>(po + (s0 + sp) * po_stride)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    const float2 mls = lane < count ? *reinterpret_cast<const float2*>(ml + (s0 + lane) * ml_stride)
+                                    : make_float2(kNegInf, 0.f);
+    float bmax = mls.x;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) denom += __shfl_xor(denom, off);
+    for (int off = 32; off > 0; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off));
+    const float new_max = fmaxf(run_max, bmax);
+    const float keep = run_max == kNegInf ? 0.f : exp2f((run_max - new_max) * kLog2e);
+    const float w = mls.x == kNegInf ? 0.f : exp2f((mls.x - new_max) * kLog2e);
+    float dsum = w * mls.y;
 #pragma unroll
-    for (int off = kLanesPerSplit; off < kWave; off <<= 1) {
-      acc.x += __shfl_xor(acc.x, off);
-      acc.y += __shfl_xor(acc.y, off);
-      acc.z += __shfl_xor(acc.z, off);
-      acc.w += __shfl_xor(acc.w, off);
+    for (int off = 32; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
+    denom = denom * keep + dsum;
+    acc.x *= keep;
+    acc.y *= keep;
+    acc.z *= keep;
+    acc.w *= keep;
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const float ws = __shfl(w, p * kSplitsPerPass + sub);
+      acc.x += ws * v[p].x;
+      acc.y += ws * v[p].y;
+      acc.z += ws * v[p].z;
+      acc.w += ws * v[p].w;
     }
-    if (sub == 0) {
-      const float inv = 1.f / denom;
-      T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * chunk;
-      store4<T>(dst, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-    }
+    run_max = new_max;
+  }
+#pragma unroll
+  for (int off = kLanesPerSplit; off < kWave; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off);
+    acc.y += __shfl_xor(acc.y, off);
+    acc.z += __shfl_xor(acc.z, off);
+    acc.w += __shfl_xor(acc.w, off);
+  }
+  if (sub == 0) {
+    const float inv = 1.f / denom;
+    T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * chunk;
+    store4<T>(dst, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
   }
 }
 
@@ -924,32 +933,46 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
   if (first + nsplit > a.ws_items) return;
-  merge_splits<T, D>(a, b, first, (int)nsplit, qh, 1);
+  merge_splits<T, D>(a, b, first, (int)nsplit, qh);
 }
 
-// Work decomposition of a decode call: 16-key tiles per split chosen so the
-// batch yields about kDecodeTargetItems work items (each one workgroup per
-// KV-head group), two rounds of workgroups over the 256 CUs.
-constexpr int64_t kDecodeTargetItems = 512;
+// Work decomposition of a decode call.  A workgroup costs about
+// kDecodeFixedTiles tile-times of fixed latency (lengths -> block table ->
+// first DMA, and the drain at the end) plus one tile-time per 16-key tile,
+// and the workgroups of a call run in rounds of (CUs x resident workgroups
+// per CU).  The planner takes the number of rounds r that minimises
+// r * (kDecodeFixedTiles + tiles per split), where tiles per split is the
+// smallest that fits the call into r rounds, within [4, 64] (64 = the
+// per-split block-table window, one VGPR per lane).
+constexpr int64_t kDecodeCUs = 256;  // MI355X
 constexpr int64_t kDecodeMinTilesPerSplit = 4;
-constexpr int64_t kDecodeMaxTilesPerSplit = 64;  // the per-split block-table window (one VGPR)
+constexpr int64_t kDecodeMaxTilesPerSplit = 64;
+constexpr int64_t kDecodeFixedTiles = 4;
+constexpr int64_t kDecodeMaxRounds = 8;
 
-// NIE_DECODE_TARGET_ITEMS overrides the work-item target for tuning.
-int64_t decode_target_items() {
-  static const int64_t target = [] {
-    const char* env = getenv("NIE_DECODE_TARGET_ITEMS");
-    const long long v = env ? atoll(env) : 0;
-    return v > 0 ? (int64_t)v : kDecodeTargetItems;
-  }();
-  return target;
+// Tuning overrides: NIE_DECODE_MAX_HEADS caps the KV heads per workgroup,
+// NIE_DECODE_TILES_PER_SPLIT fixes the split length.
+int env_int(const char* name) {
+  const char* env = getenv(name);
+  return env ? atoi(env) : 0;
 }
 
-int64_t decode_tiles_per_split(int64_t batch, int64_t total_seq_len) {
-  const int64_t total_tiles = cdiv(total_seq_len, kTileKeys) + batch;
-  int64_t tps = cdiv(total_tiles, decode_target_items());
-  tps = tps < kDecodeMinTilesPerSplit ? kDecodeMinTilesPerSplit : tps;
-  return tps > kDecodeMaxTilesPerSplit ? kDecodeMaxTilesPerSplit : tps;
+int decode_heads_cap() {
+  static const int cap = env_int("NIE_DECODE_MAX_HEADS");
+  return cap > 0 ? cap : 1 << 30;
 }
+
+int64_t decode_tiles_override() {
+  static const int64_t tps = env_int("NIE_DECODE_TILES_PER_SPLIT");
+  return tps;
+}
+
+struct DecodePlan {
+  int heads = 1;     // KV heads per workgroup (one wave each)
+  int resident = 1;  // workgroups resident on one CU
+  int64_t tps = kDecodeMinTilesPerSplit;
+  int64_t items = 0;  // grid.x: an upper bound on the number of work items
+};
 
 // Workspace layout of a decode call: the partial O rows (items x q_heads x
 // head_dim floats), then (max, sum) pairs (items x q_heads x 2 floats).
@@ -1164,36 +1187,116 @@ CacheGeom make_geom(int64_t layer_index, int64_t num_blocks, int64_t block_size,
 // block_size a power of two of at least 16.
 bool uniform_tiles(const CacheGeom& g) { return g.bs_shift >= 4; }
 
+// Resident decode workgroups per CU of one instantiation: the runtime's
+// occupancy figure, or the LDS bound when it cannot be queried.
 template <typename T, int D, bool U, int H>
-void launch_decode_h(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
-  const dim3 grid((unsigned)items, (unsigned)(a.geom.kv_heads / H));
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a);
-  if (merge) {
-    const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv((int64_t)a.q_heads, (int64_t)kMergeWaves));
-    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a);
-  }
+int decode_resident() {
+  static const int n = [] {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_kernel<T, D, U, H>, H * kWave, 0) !=
+            hipSuccess ||
+        blocks < 1) {
+      (void)hipGetLastError();
+      constexpr int lds = decode_stages<T, D, H>() * 2 * GroupTile<T, D, H>::kBytes;
+      blocks = kDecodeLdsBudget / lds > 0 ? kDecodeLdsBudget / lds : 1;
+    }
+    return blocks;
+  }();
+  return n;
 }
 
 // Heads per workgroup: the largest power of two that divides kv_heads, up to
 // the number that fills a 1 KiB row slice.
-template <typename T, int D, bool U>
-void launch_decode_u(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
+template <typename T, int D>
+int decode_heads(int64_t kv_heads) {
   constexpr int kMax = decode_max_heads<T, D>();
-  const int hkv = a.geom.kv_heads;
+  const int cap = decode_heads_cap();
   int heads = 1;
-  while (heads * 2 <= kMax && hkv % (heads * 2) == 0) heads *= 2;
+  while (heads * 2 <= kMax && heads * 2 <= cap && kv_heads % (heads * 2) == 0) heads *= 2;
+  return heads;
+}
+
+// Instantiation of a decode launch for a runtime head count.
+template <int kMax, int H>
+constexpr int heads_clamp() {
+  return kMax >= H ? H : 1;
+}
+
+template <typename T, int D, bool U>
+int decode_resident_u(int heads) {
+  constexpr int kMax = decode_max_heads<T, D>();
   switch (heads) {
-    case 1: launch_decode_h<T, D, U, 1>(a, items, stream, merge); break;
-    case 2: launch_decode_h<T, D, U, (kMax >= 2 ? 2 : 1)>(a, items, stream, merge); break;
-    case 4: launch_decode_h<T, D, U, (kMax >= 4 ? 4 : 1)>(a, items, stream, merge); break;
-    default: launch_decode_h<T, D, U, (kMax >= 8 ? 8 : 1)>(a, items, stream, merge); break;
+    case 1: return decode_resident<T, D, U, 1>();
+    case 2: return decode_resident<T, D, U, heads_clamp<kMax, 2>()>();
+    case 4: return decode_resident<T, D, U, heads_clamp<kMax, 4>()>();
+    default: return decode_resident<T, D, U, heads_clamp<kMax, 8>()>();
+  }
+}
+
+template <typename T, int D, bool U, int H>
+void launch_decode_h(const DecodeArgs& a, int64_t items, hipStream_t stream) {
+  const dim3 grid((unsigned)items, (unsigned)(a.geom.kv_heads / H));
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a);
+}
+
+template <typename T, int D, bool U>
+void launch_decode_u(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+  constexpr int kMax = decode_max_heads<T, D>();
+  switch (p.heads) {
+    case 1: launch_decode_h<T, D, U, 1>(a, p.items, stream); break;
+    case 2: launch_decode_h<T, D, U, heads_clamp<kMax, 2>()>(a, p.items, stream); break;
+    case 4: launch_decode_h<T, D, U, heads_clamp<kMax, 4>()>(a, p.items, stream); break;
+    default: launch_decode_h<T, D, U, heads_clamp<kMax, 8>()>(a, p.items, stream); break;
   }
 }
 
 template <typename T, int D>
-void launch_decode(const DecodeArgs& a, int64_t items, hipStream_t stream, bool merge) {
-  if (uniform_tiles(a.geom)) launch_decode_u<T, D, true>(a, items, stream, merge);
-  else launch_decode_u<T, D, false>(a, items, stream, merge);
+DecodePlan plan_decode_t(int64_t kv_heads, bool uniform, int64_t batch, int64_t total_seq_len) {
+  DecodePlan p;
+  p.heads = decode_heads<T, D>(kv_heads);
+  p.resident = uniform ? decode_resident_u<T, D, true>(p.heads) : decode_resident_u<T, D, false>(p.heads);
+  const int64_t groups = kv_heads / p.heads;
+  const int64_t slots = (kDecodeCUs * p.resident) / groups > 0 ? (kDecodeCUs * p.resident) / groups : 1;
+  const int64_t tiles = cdiv(total_seq_len, kTileKeys) + batch;  // >= sum_b ceil(len_b / 16)
+  p.tps = kDecodeMaxTilesPerSplit;
+  int64_t best = -1;
+  for (int64_t r = 1; r <= kDecodeMaxRounds; ++r) {
+    const int64_t room = r * slots - batch - 1;  // items <= tiles / tps + batch + 1
+    if (room <= 0) continue;
+    int64_t tps = cdiv(tiles, room);
+    tps = tps < kDecodeMinTilesPerSplit ? kDecodeMinTilesPerSplit : tps;
+    if (tps > kDecodeMaxTilesPerSplit) continue;
+    const int64_t cost = r * (kDecodeFixedTiles + tps);
+    if (best < 0 || cost < best) {
+      best = cost;
+      p.tps = tps;
+    }
+  }
+  const int64_t forced = decode_tiles_override();
+  if (forced > 0) p.tps = forced < kDecodeMaxTilesPerSplit ? forced : kDecodeMaxTilesPerSplit;
+  p.items = decode_max_items(batch, total_seq_len, p.tps);
+  return p;
+}
+
+DecodePlan plan_decode(int dtype, int64_t head_dim, int64_t kv_heads, int64_t block_size, int64_t batch,
+                       int64_t total_seq_len) {
+  const bool uniform = block_size >= 16 && (block_size & (block_size - 1)) == 0;
+  if (dtype == NIE_DTYPE_BF16) {
+    return head_dim == 64 ? plan_decode_t<bf16_t, 64>(kv_heads, uniform, batch, total_seq_len)
+                          : plan_decode_t<bf16_t, 128>(kv_heads, uniform, batch, total_seq_len);
+  }
+  return head_dim == 64 ? plan_decode_t<float, 64>(kv_heads, uniform, batch, total_seq_len)
+                        : plan_decode_t<float, 128>(kv_heads, uniform, batch, total_seq_len);
+}
+
+template <typename T, int D>
+void launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream, bool merge) {
+  if (uniform_tiles(a.geom)) launch_decode_u<T, D, true>(a, p, stream);
+  else launch_decode_u<T, D, false>(a, p, stream);
+  if (merge) {
+    const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv((int64_t)a.q_heads, (int64_t)kMergeWaves));
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a);
+  }
 }
 
 template <typename T, int D>
@@ -1314,15 +1417,17 @@ NIE_API int nie_kv_copy_blocks(int dtype, const void* src_k, const void* src_v,
   return launched("kv_copy_blocks");
 }
 
-NIE_API int64_t nie_paged_decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
+NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,
+                                                 int64_t kv_heads, int64_t head_dim,
                                                  int64_t block_size, int64_t max_seq_len,
                                                  int64_t total_seq_len) {
-  (void)block_size;
   (void)max_seq_len;
-  if (batch <= 0 || q_heads <= 0 || head_dim <= 0 || total_seq_len <= 0) return 0;
-  const int64_t tps = decode_tiles_per_split(batch, total_seq_len);
-  const int64_t items = decode_max_items(batch, total_seq_len, tps);
-  return items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
+  if (check_dtype(dtype) != NIE_OK || batch <= 0 || q_heads <= 0 || total_seq_len <= 0 || block_size <= 0 ||
+      check_attention_shape(q_heads, kv_heads, head_dim, 1, block_size) != NIE_OK) {
+    return 0;
+  }
+  const DecodePlan p = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len);
+  return p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
 NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -1358,8 +1463,9 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
       ((uintptr_t)k_cache % 16) || ((uintptr_t)v_cache % 16)) {
     return fail(NIE_EINVAL, "q/out/cache pointers and strides must be 16-byte aligned");
   }
-  const int64_t tps = decode_tiles_per_split(batch, total_seq_len);
-  const int64_t items = decode_max_items(batch, total_seq_len, tps);
+  const DecodePlan plan = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len);
+  const int64_t tps = plan.tps;
+  const int64_t items = plan.items;
   const bool may_split = cdiv(max_seq_len, kTileKeys) > tps;
   const int64_t need = items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
   if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
@@ -1393,11 +1499,11 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
   // workgroups past the last real item return immediately.
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    if (head_dim == 64) launch_decode<bf16_t, 64>(a, items, s, may_split);
-    else launch_decode<bf16_t, 128>(a, items, s, may_split);
+    if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, s, may_split);
+    else launch_decode<bf16_t, 128>(a, plan, s, may_split);
   } else {
-    if (head_dim == 64) launch_decode<float, 64>(a, items, s, may_split);
-    else launch_decode<float, 128>(a, items, s, may_split);
+    if (head_dim == 64) launch_decode<float, 64>(a, plan, s, may_split);
+    else launch_decode<float, 128>(a, plan, s, may_split);
   }
   return launched("paged_decode");
 }

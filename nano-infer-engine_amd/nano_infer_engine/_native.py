@@ -58,7 +58,7 @@ _SIGNATURES = {
         _i32,
         [_i32, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr],
     ),
-    "nie_paged_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "nie_paged_decode": (
         _i32,
         [
@@ -348,7 +348,9 @@ def paged_decode(
     if batch == 0:
         return out
     lib = load_library()
-    ws_bytes = lib.nie_paged_decode_workspace_bytes(batch, q_heads, head_dim, block_size, max_seq_len, total_seq_len)
+    ws_bytes = lib.nie_paged_decode_workspace_bytes(
+        dtype_code(query.dtype), batch, q_heads, kv_heads, head_dim, block_size, max_seq_len, total_seq_len
+    )
     stream = _stream(query.device)
     workspace = _decode_workspace(query.device, stream, ws_bytes)
     rc = lib.nie_paged_decode(
@@ -413,7 +415,7 @@ def varlen_prefill(
     ws_bytes = lib.nie_varlen_prefill_workspace_bytes(
         num_seqs, total_tokens, max_query_len, max_seq_len, q_heads, kv_heads, head_dim
     )
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes > 0 else None
     rc = lib.nie_varlen_prefill(
         dtype_code(query.dtype),
         query.data_ptr(), query.stride(0), query.stride(1),
@@ -425,8 +427,147 @@ def varlen_prefill(
         block_tables.data_ptr(), block_tables.shape[1],
         float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
-        workspace.data_ptr(), workspace.numel(),
+        None if workspace is None else workspace.data_ptr(), 0 if workspace is None else workspace.numel(),
         _stream(query.device),
     )
     _check(rc, "nie_varlen_prefill")
     return out
+
+
+# ---------------------------------------------------------------------------
+# Prepared launches: a forward pass runs the same append / decode / prefill
+# launch once per layer with only the layer index and the per-layer q, k, v
+# and output tensors changing.  These objects check and resolve everything
+# else (cache and metadata pointers, launch plan, workspace, stream) once, so
+# a layer's launch costs one C call.  They launch on the stream that was
+# current when they were built.
+# ---------------------------------------------------------------------------
+class PreparedAppend:
+    """``kv_append`` for one slot mapping, any layer."""
+
+    __slots__ = ("_fn", "_args_cache", "_tokens", "_dtype", "_row_shape", "_device", "_stream", "_slots")
+
+    def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor):
+        num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+        _require_gpu(slot_mapping)
+        if slot_mapping.dtype != torch.int64 or slot_mapping.ndim != 1 or not slot_mapping.is_contiguous():
+            raise ValueError("slot_mapping must be a contiguous 1D int64 tensor")
+        self._fn = load_library().nie_kv_append
+        self._dtype = k_cache.dtype
+        self._device = k_cache.device
+        self._row_shape = (kv_heads, head_dim)
+        self._tokens = slot_mapping.shape[0]
+        self._slots = slot_mapping  # keeps the mapping alive
+        self._stream = _stream(k_cache.device)
+        self._args_cache = (slot_mapping.data_ptr(), self._tokens, k_cache.data_ptr(), v_cache.data_ptr(),
+                            num_layers, num_blocks, block_size, kv_heads, head_dim)
+
+    def __call__(self, keys: torch.Tensor, values: torch.Tensor, layer_index: int) -> None:
+        kv_heads, head_dim = self._row_shape
+        for t in (keys, values):
+            if (t.dtype != self._dtype or t.device != self._device or t.ndim != 3 or t.shape[0] != self._tokens
+                    or t.shape[1:] != self._row_shape or t.stride(2) != 1 or t.stride(1) != head_dim):
+                raise ValueError("keys/values must be (tokens, kv_heads, head_dim) rows matching the cache")
+        slots, tokens, kptr, vptr, num_layers, num_blocks, block_size, _, _ = self._args_cache
+        rc = self._fn(_DTYPE_CODES[self._dtype], keys.data_ptr(), keys.stride(0), values.data_ptr(), values.stride(0),
+                      slots, tokens, kptr, vptr, num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim,
+                      self._stream)
+        if rc:
+            _check(rc, "nie_kv_append")
+
+
+class PreparedDecode:
+    """``paged_decode`` for one batch of sequences (tables, lengths), any layer."""
+
+    __slots__ = ("_fn", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep")
+
+    def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                 seq_lens: torch.Tensor, max_seq_len: int, total_seq_len: int, q_heads: int, scale: float):
+        num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+        _require_gpu(block_tables, seq_lens)
+        _check_attention_shapes(q_heads, kv_heads, head_dim)
+        batch = seq_lens.shape[0] if seq_lens.ndim == 1 else -1
+        if seq_lens.dtype != torch.int32 or batch <= 0 or not seq_lens.is_contiguous():
+            raise ValueError("seq_lens must be a contiguous int32 (batch,) tensor")
+        if (block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != batch
+                or not block_tables.is_contiguous()):
+            raise ValueError("block_tables must be a contiguous int32 (batch, max_blocks) tensor")
+        lib = load_library()
+        code = dtype_code(k_cache.dtype)
+        ws_bytes = lib.nie_paged_decode_workspace_bytes(code, batch, q_heads, kv_heads, head_dim, block_size,
+                                                        max_seq_len, total_seq_len)
+        stream = _stream(k_cache.device)
+        workspace = _decode_workspace(k_cache.device, stream, ws_bytes)
+        self._fn = lib.nie_paged_decode
+        self._dtype = k_cache.dtype
+        self._device = k_cache.device
+        self._shape = (batch, q_heads, head_dim)
+        self._keep = (block_tables, seq_lens, workspace)
+        self._pre = (code,)
+        self._mid = (k_cache.data_ptr(), v_cache.data_ptr(), num_layers)
+        self._post = (num_blocks, block_size, q_heads, kv_heads, head_dim, block_tables.data_ptr(),
+                      block_tables.shape[1], seq_lens.data_ptr(), batch, max_seq_len, total_seq_len, float(scale),
+                      (workspace.data_ptr(), workspace.numel(), stream))
+
+    def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
+        for t in (query, out):
+            if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
+                    or t.data_ptr() % 16):
+                raise ValueError("query/out must be aligned (batch, q_heads, head_dim) tensors matching the batch")
+        kptr, vptr, num_layers = self._mid
+        (num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch, max_len, total_len,
+         scale, (ws, ws_bytes, stream)) = self._post
+        rc = self._fn(self._pre[0], query.data_ptr(), query.stride(0), query.stride(1), kptr, vptr, num_layers,
+                      layer_index, num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch,
+                      max_len, total_len, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes, stream)
+        if rc:
+            _check(rc, "nie_paged_decode")
+        return out
+
+
+class PreparedPrefill:
+    """``varlen_prefill`` for one packed ragged batch, any layer."""
+
+    __slots__ = ("_fn", "_args", "_shape", "_dtype", "_device", "_keep")
+
+    def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, cu_seqlens: torch.Tensor,
+                 context_lens: torch.Tensor, block_tables: torch.Tensor, total_tokens: int, max_query_len: int,
+                 max_seq_len: int, q_heads: int, scale: float):
+        num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+        _require_gpu(cu_seqlens, context_lens, block_tables)
+        _check_attention_shapes(q_heads, kv_heads, head_dim)
+        num_seqs = context_lens.shape[0]
+        if cu_seqlens.dtype != torch.int64 or cu_seqlens.shape != (num_seqs + 1,) or not cu_seqlens.is_contiguous():
+            raise ValueError("cu_seqlens must be a contiguous int64 (num_seqs + 1,) tensor")
+        if context_lens.dtype != torch.int32 or not context_lens.is_contiguous():
+            raise ValueError("context_lens must be a contiguous int32 tensor")
+        if (block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != num_seqs
+                or not block_tables.is_contiguous()):
+            raise ValueError("block_tables must be a contiguous int32 (num_seqs, max_blocks) tensor")
+        lib = load_library()
+        if lib.nie_varlen_prefill_workspace_bytes(num_seqs, total_tokens, max_query_len, max_seq_len, q_heads,
+                                                  kv_heads, head_dim) != 0:
+            raise RuntimeError("varlen prefill unexpectedly needs a workspace")
+        self._fn = lib.nie_varlen_prefill
+        self._dtype = k_cache.dtype
+        self._device = k_cache.device
+        self._shape = (total_tokens, q_heads, head_dim)
+        self._keep = (cu_seqlens, context_lens, block_tables)
+        self._args = (dtype_code(k_cache.dtype), cu_seqlens.data_ptr(), context_lens.data_ptr(), num_seqs,
+                      total_tokens, max_query_len, max_seq_len, k_cache.data_ptr(), v_cache.data_ptr(), num_layers,
+                      num_blocks, block_size, q_heads, kv_heads, head_dim, block_tables.data_ptr(),
+                      block_tables.shape[1], float(scale), _stream(k_cache.device))
+
+    def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
+        for t in (query, out):
+            if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
+                    or t.data_ptr() % 16):
+                raise ValueError("query/out must be aligned (tokens, q_heads, head_dim) tensors matching the batch")
+        (code, cu, ctx, num_seqs, total, max_q, max_s, kptr, vptr, num_layers, num_blocks, block_size, q_heads,
+         kv_heads, head_dim, tables, tstride, scale, stream) = self._args
+        rc = self._fn(code, query.data_ptr(), query.stride(0), query.stride(1), cu, ctx, num_seqs, total, max_q,
+                      max_s, kptr, vptr, num_layers, layer_index, num_blocks, block_size, q_heads, kv_heads, head_dim,
+                      tables, tstride, scale, out.data_ptr(), out.stride(0), out.stride(1), None, 0, stream)
+        if rc:
+            _check(rc, "nie_varlen_prefill")
+        return out

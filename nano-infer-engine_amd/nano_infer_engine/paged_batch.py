@@ -17,7 +17,7 @@ launch, then ``paged_decode`` for requests with a single new token and
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -41,10 +41,48 @@ class RaggedBatch:
     positions: torch.Tensor  # (num_tokens,) int64
     # host-side launch geometry
     decode_from: int  # requests [decode_from, R) have one new token each (a contiguous tail)
+    # prepared per-layer launches, built on first use (see ``launchers``)
+    _launch: dict = field(default_factory=dict, repr=False, compare=False)
 
     @property
     def num_requests(self) -> int:
         return len(self.sequence_ids)
+
+    @property
+    def first_decode_token(self) -> int:
+        """Packed row of the first single-token (decode) request."""
+        return self.num_tokens - (self.num_requests - self.decode_from)
+
+    def launchers(self, cache: PagedKVCache, q_heads: int, scale: float):
+        """(append, prefill or None, decode or None) launches of this batch on ``cache``.
+
+        Built once and reused by every layer: the cache pointers, metadata,
+        launch plan, workspace and stream are resolved here, so a layer's
+        attention costs one C call per kernel family.
+        """
+        key = (cache.keys.data_ptr(), q_heads, float(scale))
+        found = self._launch.get(key)
+        if found is not None:
+            return found
+        append = _native.PreparedAppend(cache.keys, cache.values, self.slot_mapping)
+        split = self.decode_from
+        prefill = decode = None
+        if split > 0:
+            seq_lens = [c + n for c, n in zip(self.context_lens[:split], self.query_lens[:split])]
+            prefill = _native.PreparedPrefill(
+                cache.keys, cache.values, self.cu_seqlens[: split + 1], self.context_lens_t[:split],
+                self.block_tables[:split], self.first_decode_token, max(self.query_lens[:split]), max(seq_lens),
+                q_heads, scale,
+            )
+        if split < self.num_requests:
+            seq_lens = [c + 1 for c in self.context_lens[split:]]
+            decode = _native.PreparedDecode(
+                cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], max(seq_lens),
+                sum(seq_lens), q_heads, scale,
+            )
+        found = (append, prefill, decode)
+        self._launch[key] = found
+        return found
 
 
 def build_ragged_batch(
@@ -126,38 +164,20 @@ def paged_attention(
     sequence's cached prefix and, causally, to the new tokens before it
     (``layers/attention.py:378-411`` of the reference).
     """
-    cache.write_slots(layer_index, k, v, batch.slot_mapping)
+    append, prefill, decode = batch.launchers(cache, q.shape[1], scale)
+    append(_rows(k), _rows(v), layer_index)
+    q = _rows(q)
     out = torch.empty_like(q)
-    split = batch.decode_from
-    first_decode_token = int(batch.num_tokens - (batch.num_requests - split))
-    if split > 0:
-        # requests [0, split): at least one has several new tokens -> varlen kernel
-        seq_lens = [c + n for c, n in zip(batch.context_lens[:split], batch.query_lens[:split])]
-        _native.varlen_prefill(
-            q[:first_decode_token],
-            batch.cu_seqlens[: split + 1],
-            batch.context_lens_t[:split],
-            cache.keys,
-            cache.values,
-            layer_index,
-            batch.block_tables[:split],
-            max(batch.query_lens[:split]),
-            max(seq_lens),
-            scale,
-            out=out[:first_decode_token],
-        )
-    if split < batch.num_requests:
-        seq_lens = [c + 1 for c in batch.context_lens[split:]]
-        _native.paged_decode(
-            q[first_decode_token:],
-            cache.keys,
-            cache.values,
-            layer_index,
-            batch.block_tables[split:],
-            batch.seq_lens_t[split:],
-            max(seq_lens),
-            sum(seq_lens),
-            scale,
-            out=out[first_decode_token:],
-        )
+    split = batch.first_decode_token
+    if prefill is not None:
+        prefill(q[:split], layer_index, out[:split])
+    if decode is not None:
+        decode(q[split:], layer_index, out[split:])
     return out
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """``t`` if it is contiguous with a 16-byte aligned start, else an aligned copy."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)

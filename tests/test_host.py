@@ -275,9 +275,13 @@ def test_library_exports_every_header_symbol():
 def test_library_workspace_queries():
     lib = _native.load_library()
     # decode partials: items * q_heads * (head_dim + 2) floats, items bounded by the split count
-    small = lib.nie_paged_decode_workspace_bytes(4, 32, 64, 16, 500, 710)
-    assert small > 0 and small % 4 == 0
-    big = lib.nie_paged_decode_workspace_bytes(16, 32, 64, 16, 29600, 16 * 29600)
+    small = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710)
+    assert small > 0 and small % (32 * 66 * 4) == 0
+    big = lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600)
     assert big >= small
-    assert lib.nie_paged_decode_workspace_bytes(0, 32, 64, 16, 1, 1) == 0
+    # at most 64 tiles of 16 keys per split: at least 16 * ceil(1850 / 64) items
+    assert big >= 16 * 29 * 32 * 66 * 4
+    assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1) == 0
+    assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710) == 0  # bad dtype
+    assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710) == 0  # head_dim 96
     assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 64) >= 0
