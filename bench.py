@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(REPO, "nano-infer-engine_amd"))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse_args():
@@ -41,6 +42,8 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
     p.add_argument("--skip-stress", action="store_true", help="do not run the 16x29600 decode figure")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
+    p.add_argument("--skip-mixed", action="store_true", help="do not run the mixed chunked-prefill figure")
+    p.add_argument("--mixed-only", action="store_true", help="run only the mixed chunked-prefill figure")
     p.add_argument("--stress-only", action="store_true",
                    help="run only the 16x29600 decode figure (for per-workload profiles)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -201,6 +204,8 @@ def run_gpu(args):
     torch.cuda.empty_cache()
     if not args.skip_stress:
         result["stress_16x29600"] = run_stress(args)
+    if not args.skip_mixed:
+        result["mixed_prefill_step"] = run_mixed(args)
     return result
 
 
@@ -230,6 +235,74 @@ def run_stress(args):
     torch.cuda.empty_cache()
     return {"avg_launch_us": round(avg * 1e6, 2), "bytes_per_launch": int(per_launch),
             "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def run_mixed(args):
+    """Mixed chunked-prefill step: 4 x 128-token chunks on contexts {0, 384, 1024, 4000}
+    + 12 decode rows (contexts U[256, 8192]), packed varlen layout, one layer.
+
+    Times the varlen prefill launch (algorithmic FLOPs over unmasked pairs vs
+    the bf16 MFMA peak) and the decode launch of the same step separately.
+    """
+    import numpy as np
+    import torch
+
+    from nano_infer_engine import _native, workloads
+
+    device = torch.device("cuda:0")
+    wl = workloads.mixed_prefill()
+    kc, vc = wl.pool(torch.bfloat16, device)
+    q, k_new, v_new = wl.new_tokens(torch.bfloat16, device)
+    slots = torch.from_numpy(wl.slots()).to(device)
+    _native.kv_append(kc, vc, 0, k_new, v_new, slots)
+    n_pref = 4
+    pref_tokens = int(sum(wl.query_lens[:n_pref]))
+    tables = torch.from_numpy(wl.table_array()).to(device)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(wl.query_lens[:n_pref])]), dtype=torch.int64, device=device)
+    ctx = torch.tensor(wl.context_lens[:n_pref], dtype=torch.int32, device=device)
+    seq_lens = wl.seq_lens
+    dec_lens = torch.tensor(seq_lens[n_pref:], dtype=torch.int32, device=device)
+    scale = wl.head_dim ** -0.5
+    prefill = _native.PreparedPrefill(kc, vc, cu, ctx, tables[:n_pref].contiguous(), pref_tokens,
+                                      max(wl.query_lens[:n_pref]), max(seq_lens[:n_pref]), wl.q_heads, scale)
+    decode = _native.PreparedDecode(kc, vc, tables[n_pref:].contiguous(), dec_lens, max(seq_lens[n_pref:]),
+                                    sum(seq_lens[n_pref:]), wl.q_heads, scale)
+    out = torch.empty_like(q)
+    qp, op = q[:pref_tokens], out[:pref_tokens]
+    qd, od = q[pref_tokens:], out[pref_tokens:]
+    reps, warm = 50, 5
+    for _ in range(warm):
+        prefill(qp, 0, op)
+        decode(qd, 0, od)
+    torch.cuda.synchronize()
+    pev, dev_ = [], []
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        prefill(qp, 0, op)
+        e[1].record()
+        decode(qd, 0, od)
+        e[2].record()
+        pev.append((e[0], e[1]))
+        dev_.append((e[1], e[2]))
+    torch.cuda.synchronize()
+    p_us = sum(a.elapsed_time(b) for a, b in pev) / reps * 1e3
+    d_us = sum(a.elapsed_time(b) for a, b in dev_) / reps * 1e3
+    flops = workloads.prefill_flops(wl.context_lens[:n_pref], wl.query_lens[:n_pref])
+    tflops = flops / (p_us * 1e-6) / 1e12
+    dbytes = workloads.decode_bytes(seq_lens[n_pref:])
+    gbs = dbytes / (d_us * 1e-6) / 1e9
+    log(f"mixed step: prefill {p_us:.1f} us = {tflops:.1f} TFLOP/s ({flops / 1e9:.2f} GFLOP); "
+        f"decode rows {d_us:.1f} us = {gbs:.0f} GB/s")
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {
+        "prefill": {"kernel": "varlen_prefill_kernel", "avg_launch_us": round(p_us, 2), "flops_per_launch": flops,
+                    "achieved_TFLOPs": round(tflops, 2), "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS,
+                    "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "decode_rows": {"avg_launch_us": round(d_us, 2), "bytes_per_launch": dbytes, "achieved_GBs": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)},
+    }
 
 
 def _measured_traffic():
@@ -297,6 +370,12 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         run_copy_calibration(args.copy_calibration)
+        return
+    if args.mixed_only:
+        from nano_infer_engine import _native
+
+        _native.load_library()
+        print(json.dumps({"mixed_prefill_step": run_mixed(args)}), flush=True)
         return
     if args.stress_only:
         from nano_infer_engine import _native

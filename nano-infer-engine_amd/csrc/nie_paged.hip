@@ -97,18 +97,34 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// float -> bf16, round to nearest even (torch's conversion).  NaN stays a
-// quiet NaN.  Branch-free: both candidates are computed and selected.
+// float -> bf16, round to nearest even (torch's conversion), on gfx950's
+// v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t quiet_nan = (u >> 16) | 0x40u;
-  return ((u & 0x7fffffffu) > 0x7f800000u) ? quiet_nan : rounded;
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+// Two floats -> two bf16 in one dword (a in the low half).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 __device__ __forceinline__ float round_to_bf16(float x) {
-  return __uint_as_float(f32_to_bf16_bits(x) << 16);
+  return (float)(__bf16)x;
 }
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Four floats -> the bf16 MFMA operand (element i = x[i]).
+__device__ __forceinline__ v4s pack_bf16x4(float x0, float x1, float x2, float x3) {
+  return __builtin_bit_cast(v4s, u32x2_t{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)});
+}
+
+// 2^x on v_exp_f32 (results below 2^-126 flush to zero, which the softmax
+// sums cannot resolve anyway).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Rounds a value to the storage dtype (identity for fp32).
 template <typename T>
@@ -307,15 +323,8 @@ __device__ __forceinline__ v4f qk_mfma(const Frag<T, D>& k, const Frag<T, D>& q)
     const uint32_t* qw = reinterpret_cast<const uint32_t*>(q.v);
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      v4s a, b;
-      a[0] = (short)(kw[2 * c] & 0xffff);
-      a[1] = (short)(kw[2 * c] >> 16);
-      a[2] = (short)(kw[2 * c + 1] & 0xffff);
-      a[3] = (short)(kw[2 * c + 1] >> 16);
-      b[0] = (short)(qw[2 * c] & 0xffff);
-      b[1] = (short)(qw[2 * c] >> 16);
-      b[2] = (short)(qw[2 * c + 1] & 0xffff);
-      b[3] = (short)(qw[2 * c + 1] >> 16);
+      const v4s a = __builtin_bit_cast(v4s, u32x2_t{kw[2 * c], kw[2 * c + 1]});
+      const v4s b = __builtin_bit_cast(v4s, u32x2_t{qw[2 * c], qw[2 * c + 1]});
       acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
     }
   } else {
@@ -356,18 +365,24 @@ __device__ __forceinline__ void softmax_tile(SoftmaxState<D>& st, v4f& s) {
   const float m_new = fmaxf(st.m, tmax);
   // A row with nothing unmasked so far keeps m = -inf; use 0 as the
   // reference point so the exponentials below are exact zeros, not NaN.
-  const float ref = (m_new == kNegInf) ? 0.f : m_new;
-  const float alpha = exp2f((st.m - ref) * kLog2e);
+  const float nref = (m_new == kNegInf) ? 0.f : -m_new * kLog2e;
   float tsum = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    s[i] = exp2f((s[i] - ref) * kLog2e);
+    s[i] = fast_exp2(fmaf(s[i], kLog2e, nref));
     tsum += s[i];
   }
-  st.lsum = st.lsum * alpha + tsum;
-  st.m = m_new;
+  // Rescale only when some row's maximum moved (alpha would be exactly 1
+  // otherwise); the test is wave-uniform.
+  if (__ballot(m_new != st.m)) {
+    const float alpha = fast_exp2(fmaf(st.m, kLog2e, nref));
+    st.lsum = st.lsum * alpha + tsum;
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) st.o[c] *= alpha;
+    for (int c = 0; c < D / 16; ++c) st.o[c] *= alpha;
+  } else {
+    st.lsum += tsum;
+  }
+  st.m = m_new;
 }
 
 // O^T += V^T . P^T for one 16-key tile.  `vt` is the LDS copy of the tile's
@@ -380,9 +395,7 @@ __device__ __forceinline__ void pv_mfma(SoftmaxState<D>& st, const unsigned char
   const int g = lane >> 4;
   const int col = lane & 15;
   if constexpr (Elt<T>::kIsBf16) {
-    v4s b;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) b[i] = (short)f32_to_bf16_bits(p[i]);
+    const v4s b = pack_bf16x4(p[0], p[1], p[2], p[3]);
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       v4s a;
@@ -417,8 +430,8 @@ template <typename T>
 __device__ __forceinline__ void store4(T* dst, float a, float b, float c, float d) {
   if constexpr (Elt<T>::kIsBf16) {
     uint2 w;
-    w.x = f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
-    w.y = f32_to_bf16_bits(c) | (f32_to_bf16_bits(d) << 16);
+    w.x = pack_bf16x2(a, b);
+    w.y = pack_bf16x2(c, d);
     *reinterpret_cast<uint2*>(dst) = w;
   } else {
     *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, d);
@@ -642,14 +655,17 @@ __device__ __forceinline__ void ring_read_vt16(v4s (&a)[4], const uint32_t (&add
   }
 }
 
-// Merges the split partials of query head qh of sequence b, one wave.  The
-// lanes form kSplitsPerPass groups of D/4 lanes; a group reads one split's
-// O row as float4s.  Splits go in batches of kPasses * kSplitsPerPass: every
-// load of a batch (the O rows, and one (max, sum) pair per lane) is issued
-// before any is used, and batches combine through a running maximum, so the
-// usual merge (<= 32 splits at head_dim 64) costs one memory round trip.
+// Merges nsplit split partials of one output row, one wave.  Split s of the
+// row has its unnormalised O row at po + s*po_stride and its (max, sum) pair
+// at ml + s*ml_stride.  The lanes form kSplitsPerPass groups of D/4 lanes; a
+// group reads one split's O row as float4s.  Splits go in batches of
+// kPasses * kSplitsPerPass: every load of a batch (the O rows, and one
+// (max, sum) pair per lane) is issued before any is used, and batches
+// combine through a running maximum, so the usual merge (<= 32 splits at
+// head_dim 64) costs one memory round trip.
 template <typename T, int D>
-__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int64_t b, int64_t first, int nsplit, int qh) {
+__device__ __forceinline__ void merge_row(const float* po, int64_t po_stride, const float* ml, int64_t ml_stride,
+                                          int nsplit, T* out) {
   constexpr int kLanesPerSplit = D / 4;
   constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
   constexpr int kPasses = 8;
@@ -658,10 +674,7 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, int64_t b, int
   const int lane = lane_id();
   const int sub = lane / kLanesPerSplit;
   const int chunk = lane % kLanesPerSplit;
-  const int64_t ml_stride = (int64_t)a.q_heads * 2;
-  const int64_t po_stride = (int64_t)a.q_heads * D;
-  const float* ml = a.ws_ml + (first * a.q_heads + qh) * 2;
-  const float* po = a.ws_o + (first * a.q_heads + qh) * D + 4 * chunk;
+  po += 4 * chunk;
   float run_max = kNegInf;
   float denom = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -709,8 +722,7 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, int64_t b, int
   }
   if (sub == 0) {
     const float inv = 1.f / denom;
-    T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * chunk;
-    store4<T>(dst, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    store4<T>(out + 4 * chunk, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
   }
 }
 
@@ -832,15 +844,14 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     }
     v4f s = qk_mfma<T, D>(kf, qf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = scaled_score<T>(s[i], a.scale);
-      s[i] = (key0 + 4 * g + i <= last) ? v : kNegInf;
+    for (int i = 0; i < 4; ++i) s[i] = scaled_score<T>(s[i], a.scale);
+    if (key0 + kTileKeys - 1 > last) {  // only the split's last tile can pass its end
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = (key0 + 4 * g + i <= last) ? s[i] : kNegInf;
     }
     softmax_tile<D>(st, s);
     if constexpr (Elt<T>::kIsBf16) {
-      v4s pb;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pb[i] = (short)f32_to_bf16_bits(s[i]);
+      const v4s pb = pack_bf16x4(s[0], s[1], s[2], s[3]);
       const uint32_t base = lds_off(stage);
 #pragma unroll
       for (int c0 = 0; c0 < D / 16; c0 += 4) {
@@ -933,7 +944,9 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
   if (first + nsplit > a.ws_items) return;
-  merge_splits<T, D>(a, b, first, (int)nsplit, qh);
+  merge_row<T, D>(a.ws_o + (first * a.q_heads + qh) * D, (int64_t)a.q_heads * D,
+                  a.ws_ml + (first * a.q_heads + qh) * 2, (int64_t)a.q_heads * 2, (int)nsplit,
+                  reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh);
 }
 
 // Work decomposition of a decode call.  A workgroup costs about
@@ -985,6 +998,14 @@ int64_t decode_max_items(int64_t batch, int64_t total_seq_len, int64_t tps) {
 // Varlen prefill
 // ---------------------------------------------------------------------------
 constexpr int kPrefillWaves = 4;
+constexpr int kPrefillLdsBudget = 64 * 1024;
+
+// Query rows per wave: kRowBlocks MFMA row blocks of 16 rows, each block
+// = 16/G consecutive tokens x the G query heads of the workgroup's KV head.
+template <int kRowBlocks>
+constexpr int prefill_rows_per_item() {
+  return kPrefillWaves * kRowBlocks * 16;
+}
 
 struct PrefillArgs {
   const void* q;
@@ -996,130 +1017,357 @@ struct PrefillArgs {
   const void* v_cache;
   CacheGeom geom;
   int32_t group;
-  int32_t tokens_per_tile;  // query tokens per workgroup
+  int32_t tokens_per_tile;  // query tokens per work item
+  int32_t tiles_per_split;  // 16-key tiles per work item
   const int32_t* tables;
   int64_t table_stride;
   float scale;
   void* out;
   int64_t o_st, o_sh;
+  float* ws_o;       // (ws_items, kv_heads, rows_per_item, head_dim)
+  float* ws_ml;      // (ws_items, kv_heads, rows_per_item, 2)
+  int64_t ws_items;  // item slots in the workspace
 };
 
-template <typename T, int D, bool kUniform>
+// Key tiles visible to query tile qt of request r (its last row's position + 1).
+__device__ __forceinline__ int prefill_key_tiles(int ctx, int q_len, int tpt, int qt) {
+  const int t_end = min((qt + 1) * tpt, q_len);
+  return (ctx + t_end + kTileKeys - 1) / kTileKeys;
+}
+
+__device__ __forceinline__ int64_t prefill_items_of(const PrefillArgs& a, int64_t r) {
+  const int q_len = (int)(a.cu_seqlens[r + 1] - a.cu_seqlens[r]);
+  const int ctx = a.context_lens[r];
+  const int tpt = a.tokens_per_tile;
+  const int nqt = (q_len + tpt - 1) / tpt;
+  int64_t n = 0;
+  for (int qt = 0; qt < nqt; ++qt) n += cdiv((int64_t)prefill_key_tiles(ctx, q_len, tpt, qt), (int64_t)a.tiles_per_split);
+  return n;
+}
+
+template <typename T, int D>
+constexpr int prefill_stages() {
+  constexpr int stage = 2 * GroupTile<T, D, 1>::kBytes;
+  return kPrefillLdsBudget / stage >= 8 ? 8 : (kPrefillLdsBudget / stage >= 2 ? kPrefillLdsBudget / stage : 2);
+}
+
+// One workgroup = one (request, query tile, key split) for one KV head.  The
+// head's K and V rows of each 16-key tile stream through an LDS ring by LDS
+// DMA (as in decode; the K and V DMA ops of a tile are spread evenly over
+// the waves); every wave reads the whole tile and applies it to its
+// kRowBlocks row blocks.  A row block whose tokens all precede the tile skips
+// it (causal mask).  With one split the rows are written out; with several,
+// the split's unnormalised partial goes to the workspace for
+// prefill_merge_kernel.
+template <typename T, int D, bool kUniform, int kRowBlocks>
 __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(PrefillArgs a) {
-  constexpr int kRowBytes = D * Elt<T>::kBytes;
-  constexpr int kPitch = kRowBytes + kLdsPadBytes;
-  constexpr int kChunksPerRow = kRowBytes / 16;
-  constexpr int kChunksPerTile = kTileKeys * kChunksPerRow;  // per K (or V) tile
-  constexpr int kThreads = kPrefillWaves * kWave;
-  constexpr int kLoadsPerThread = (2 * kChunksPerTile) / kThreads;  // K and V together
-  constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
-  static_assert((2 * kChunksPerTile) % kThreads == 0, "tile chunks must divide evenly");
   using F = Frag<T, D>;
-  __shared__ __attribute__((aligned(16))) unsigned char k_lds[kTileKeys * kPitch];
-  __shared__ __attribute__((aligned(16))) unsigned char v_lds[kTileKeys * kPitch];
+  using GT = GroupTile<T, D, 1>;
+  constexpr int kStages = prefill_stages<T, D>();
+  constexpr int kStageBytes = 2 * GT::kBytes;
+  constexpr int kTileOps = 2 * GT::kOps;  // K then V DMA ops of one tile
+  static_assert(kTileOps % kPrefillWaves == 0, "tile DMA ops must spread evenly over the waves");
+  constexpr int kOwnOps = kTileOps / kPrefillWaves;
+  constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
+  constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
+  __shared__ __attribute__((aligned(16))) unsigned char ring[kStages][kStageBytes];
 
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane >> 4;
   const int row = lane & 15;
   const int tpt = a.tokens_per_tile;
+  const int S = a.tiles_per_split;
 
-  int64_t r, tile, first_tile, ntile_r;
-  locate_item(
-      (int64_t)blockIdx.x, a.num_seqs,
-      [&](int64_t s) { return cdiv(a.cu_seqlens[s + 1] - a.cu_seqlens[s], (int64_t)tpt); },
-      &r, &tile, &first_tile, &ntile_r);
-  if (r < 0) return;  // same for every wave of the workgroup
+  int64_t r, local, first_r, count_r;
+  locate_item((int64_t)blockIdx.x, a.num_seqs, [&](int64_t q) { return prefill_items_of(a, q); }, &r, &local,
+              &first_r, &count_r);
+  if (r < 0) return;  // uniform over the workgroup
   const int h = (int)blockIdx.y;
-
   const int64_t q_begin = a.cu_seqlens[r];
   const int q_len = (int)(a.cu_seqlens[r + 1] - q_begin);
   const int ctx = a.context_lens[r];
+  // (query tile, split) of this item; the loop is wave-uniform
+  int qt = 0, split = (int)local, nsplit = 0;
+  for (;;) {
+    nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
+    if (split < nsplit) break;
+    split -= nsplit;
+    ++qt;
+  }
+  qt = __builtin_amdgcn_readfirstlane(qt);
+  split = __builtin_amdgcn_readfirstlane(split);
+  nsplit = __builtin_amdgcn_readfirstlane(nsplit);
+  const int64_t item = first_r + local;
+  const int t0 = qt * tpt;
+  const int t_end = min(t0 + tpt, q_len);
+  const int key_end = ctx + t_end;
+  const int tile_begin = split * S;
+  const int tile_end = min(tile_begin + S, (key_end + kTileKeys - 1) / kTileKeys);
+  const int last = min(tile_end * kTileKeys, key_end) - 1;  // last key this item reads
   const int32_t* table = a.tables + r * a.table_stride;
   const int tlen = (int)a.table_stride;
-  const int t0 = (int)tile * tpt;                  // first query token of the tile
-  const int t_end = min(t0 + tpt, q_len);
-  const int key_end = ctx + t_end;                 // keys visible to the tile's last row
-
-  // This lane's query row: token t0 + wave*(16/group) + row/group, head row%group.
-  const int tokens_per_wave = 16 / a.group;
-  const int tq = t0 + wave * tokens_per_wave + row / a.group;
-  const int qh = h * a.group + row % a.group;
-  const bool row_valid = tq < t_end;
-  const int q_pos = ctx + tq;
-
-  F qf;
-  if (row_valid) {
-    load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + (q_begin + tq) * a.q_st + qh * a.q_sh);
-  } else {
-#pragma unroll
-    for (int i = 0; i < F::kVec; ++i) qf.v[i] = uint4{0u, 0u, 0u, 0u};
-  }
-
   const T* kc = reinterpret_cast<const T*>(a.k_cache) + h * D;
   const T* vc = reinterpret_cast<const T*>(a.v_cache) + h * D;
 
-  uint4 stage[kLoadsPerThread];
-  TableCache tc;
-  if constexpr (kUniform) tc.load(table, tlen, 0);
-  auto fetch = [&](int key0) {
-    TileAddr<kUniform, true> ta;
-    ta.init(a.geom, table, tlen, tc, key0);
-    const int lim = key_end - 1 - key0;
+  // Rows: block nb of this wave = tokens t0 + (wave*kRowBlocks + nb)*(16/G) + row/G, head row%G.
+  const int tpb = 16 / a.group;  // tokens per row block
+  F qf[kRowBlocks];
+  SoftmaxState<D> st[kRowBlocks];
+  int q_pos[kRowBlocks];
 #pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) {
-      const int chunk = threadIdx.x + j * kThreads;  // 0 .. 2*kChunksPerTile-1
-      const int c = chunk % kChunksPerTile;
-      const int rr = min(c / kChunksPerRow, lim);
-      const T* base = (chunk < kChunksPerTile) ? kc : vc;
-      stage[j] = *reinterpret_cast<const uint4*>(base + ta.at(a.geom, table, tlen, key0, rr) +
-                                                 (c % kChunksPerRow) * kEltPerChunk);
-    }
-  };
-  auto commit = [&]() {
+  for (int nb = 0; nb < kRowBlocks; ++nb) {
+    const int tq = t0 + (wave * kRowBlocks + nb) * tpb + row / a.group;
+    const int qh = h * a.group + row % a.group;
+    q_pos[nb] = tq < t_end ? ctx + tq : -1;  // -1: no keys visible (padding row)
+    if (tq < t_end) {
+      load_slice<T, D>(qf[nb], reinterpret_cast<const T*>(a.q) + (q_begin + tq) * a.q_st + qh * a.q_sh);
+    } else {
 #pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) {
-      const int chunk = threadIdx.x + j * kThreads;
-      const int c = chunk % kChunksPerTile;
-      unsigned char* dst = (chunk < kChunksPerTile ? k_lds : v_lds) + (c / kChunksPerRow) * kPitch +
-                           (c % kChunksPerRow) * 16;
-      *reinterpret_cast<uint4*>(dst) = stage[j];
+      for (int i = 0; i < F::kVec; ++i) qf[nb].v[i] = uint4{0u, 0u, 0u, 0u};
     }
-  };
-
-  SoftmaxState<D> st;
-  st.init();
-  const int ntiles = (key_end + kTileKeys - 1) / kTileKeys;
-  fetch(0);
-  for (int t = 0; t < ntiles; ++t) {
-    const int key0 = t * kTileKeys;
-    __syncthreads();  // every wave is done with the previous tile
-    commit();
-    __syncthreads();
-    fetch(min(key0 + kTileKeys, (ntiles - 1) * kTileKeys));  // past the end: re-read (L2 hit)
-    F kf;
-    load_slice<T, D>(kf, k_lds + row * kPitch);
-    v4f s = qk_mfma<T, D>(kf, qf);
+    st[nb].init();
+  }
+  // first and last position of each row block (wave-uniform): tiles past
+  // the last are fully masked, tiles up to the first fully visible
+  int block_first[kRowBlocks], block_last[kRowBlocks];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // S^T C-layout: this value is key key0 + 4g + i of this lane's row.
-      const int key = key0 + 4 * g + i;
-      const float v = scaled_score<T>(s[i], a.scale);
-      s[i] = (key <= q_pos && key < key_end) ? v : kNegInf;
-    }
-    softmax_tile<D>(st, s);
-    pv_mfma<T, D>(st, v_lds, kPitch, s);
+  for (int nb = 0; nb < kRowBlocks; ++nb) {
+    block_first[nb] = ctx + t0 + (wave * kRowBlocks + nb) * tpb;
+    block_last[nb] = min(ctx + t0 + (wave * kRowBlocks + nb + 1) * tpb, key_end) - 1;
   }
 
-  const float lsum = sum_over_groups(st.lsum);
-  if (!row_valid) return;
-  const float inv = 1.f / lsum;
-  T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh + 4 * g;
+  TableCache tc;
+  if constexpr (kUniform) tc.load(table, tlen, (tile_begin * kTileKeys) >> a.geom.bs_shift);
+
+  auto issue = [&](int slot, int key0) {
+    TileAddr<kUniform, false> ta;  // an item covers <= 64 tiles, so <= 64 blocks
+    ta.init(a.geom, table, tlen, tc, key0);
+    const int lim = last - key0;
+    unsigned char* base = &ring[slot][0];
+#pragma unroll
+    for (int i = 0; i < kOwnOps; ++i) {
+      const int op = wave + i * kPrefillWaves;  // 0 .. kTileOps-1: K ops, then V ops
+      const int kop = op % GT::kOps;
+      const int rr = kop * GT::kRowsPerOp + lane / GT::kChunks;
+      const int chunk = (lane % GT::kChunks) ^ GT::swz(rr);
+      const int64_t src = ta.at(a.geom, table, tlen, key0, min(rr, lim)) + chunk * kEltPerChunk;
+      lds_dma16((op < GT::kOps ? kc : vc) + src, base + op * kWave * 16);
+    }
+  };
+
+  uint32_t koff[F::kVec];
+#pragma unroll
+  for (int j = 0; j < F::kVec; ++j) koff[j] = GT::chunk_offset(row, (64 * j + 16 * g) >> 4);
+  uint32_t voff[(D / 16) * 4];
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
-    store4<T>(dst + 16 * c, st.o[c][0] * inv, st.o[c][1] * inv, st.o[c][2] * inv,
-              st.o[c][3] * inv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, 0, 16 * c + row);
   }
+
+  auto consume = [&](int slot, int key0) {
+    const unsigned char* stage = &ring[slot][0];
+    F kf;
+    if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t sb = lds_off(stage);
+      uint32_t ka[F::kVec];
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) ka[j] = sb + koff[j];
+      ring_read_k<F::kVec>(kf.v, ka);
+    } else {
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
+    }
+    bool live[kRowBlocks];
+    v4f p[kRowBlocks];
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) {
+      live[nb] = key0 <= block_last[nb];
+      if (live[nb]) {
+        v4f sc = qk_mfma<T, D>(kf, qf[nb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i] = scaled_score<T>(sc[i], a.scale);
+        if (key0 + kTileKeys - 1 > min(block_first[nb], last)) {  // causal boundary or split end
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + 4 * g + i;
+            sc[i] = (key <= q_pos[nb] && key <= last) ? sc[i] : kNegInf;
+          }
+        }
+        softmax_tile<D>(st[nb], sc);
+        p[nb] = sc;
+      }
+    }
+    if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t sb = lds_off(stage);
+#pragma unroll
+      for (int c0 = 0; c0 < D / 16; c0 += 4) {
+        uint32_t va[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) va[i] = sb + voff[4 * c0 + i];
+        v4s vt[4];
+        ring_read_vt16(vt, va);
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+          if (!live[nb]) continue;
+          const v4s pb = pack_bf16x4(p[nb][0], p[nb][1], p[nb][2], p[nb][3]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            st[nb].o[c0 + c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[c], pb, st[nb].o[c0 + c], 0, 0, 0);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        float vv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vv[j] = *reinterpret_cast<const float*>(stage + voff[4 * c + j]);
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+          if (!live[nb]) continue;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], p[nb][j], st[nb].o[c], 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+
+  const int ntiles = tile_end - tile_begin;
+  const int last_key0 = (tile_end - 1) * kTileKeys;
+  constexpr int kAhead = kStages - 1;
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) issue(j, min((tile_begin + j) * kTileKeys, last_key0));
+  for (int t = 0; t < ntiles; t += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) {
+      const int tt = t + j;
+      if (tt >= ntiles) break;  // uniform over the workgroup
+      // this wave's ops for tile tt are done once at most the kAhead-1 later
+      // tiles' ops are outstanding; the barrier extends that to every wave
+      // and guarantees that every wave has finished reading tile tt-1
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((kAhead - 1) * kOwnOps));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue((j + kAhead) % kStages, min((tile_begin + tt + kAhead) * kTileKeys, last_key0));
+      __builtin_amdgcn_sched_barrier(0);
+      consume(j, (tile_begin + tt) * kTileKeys);
+    }
+  }
+  // drain the redundant prefetches before the LDS is handed to another workgroup
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+
+#pragma unroll
+  for (int nb = 0; nb < kRowBlocks; ++nb) {
+    const float lsum = sum_over_groups(st[nb].lsum);
+    const int tq = t0 + (wave * kRowBlocks + nb) * tpb + row / a.group;
+    if (tq >= t_end) continue;
+    const int qh = h * a.group + row % a.group;
+    if (nsplit == 1) {
+      const float inv = 1.f / lsum;
+      T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh + 4 * g;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        store4<T>(dst + 16 * c, st[nb].o[c][0] * inv, st[nb].o[c][1] * inv, st[nb].o[c][2] * inv,
+                  st[nb].o[c][3] * inv);
+      }
+    } else if (a.ws_o != nullptr && item < a.ws_items) {
+      const int64_t slot = (item * a.geom.kv_heads + h) * kRows + (wave * kRowBlocks + nb) * 16 + row;
+      float* dst = a.ws_o + slot * D + 4 * g;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        *reinterpret_cast<float4*>(dst + 16 * c) =
+            make_float4(st[nb].o[c][0], st[nb].o[c][1], st[nb].o[c][2], st[nb].o[c][3]);
+      }
+      if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + slot * 2) = make_float2(st[nb].m, lsum);
+    }
+  }
+}
+
+// Merge of split prefill rows: one wave per (query token, query head).  The
+// token's request, query tile and that tile's first item are recomputed
+// from cu_seqlens / context_lens exactly as the prefill kernel enumerates
+// its items; tiles with a single split were finished by the prefill kernel.
+template <typename T, int D, int kRowBlocks>
+__global__ __launch_bounds__(kMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a) {
+  constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
+  const int64_t t = blockIdx.x;  // packed query row
+  const int qh = (int)blockIdx.y * kMergeWaves + (int)(threadIdx.x / kWave);
+  if (qh >= a.geom.kv_heads * a.group) return;
+  const int lane = lane_id();
+  // request r with cu[r] <= t < cu[r+1], and the items of requests before it
+  int64_t r = -1, before = 0;
+  for (int64_t b0 = 0; b0 < a.num_seqs && r < 0; b0 += kWave) {
+    const int64_t b = b0 + lane;
+    const bool in = b < a.num_seqs && a.cu_seqlens[b] <= t && t < a.cu_seqlens[b + 1];
+    const uint64_t mask = __ballot(in);
+    const int64_t upto = mask ? b0 + __builtin_ctzll(mask) : a.num_seqs;  // requests before r (this chunk)
+    int64_t n = (b < upto) ? prefill_items_of(a, b) : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) n += __shfl_xor(n, off);
+    before += n;
+    if (mask) r = upto;
+  }
+  if (r < 0) return;
+  r = uniform64(r);
+  before = uniform64(before);
+  const int64_t q_begin = a.cu_seqlens[r];
+  const int q_len = (int)(a.cu_seqlens[r + 1] - q_begin);
+  const int ctx = a.context_lens[r];
+  const int tpt = a.tokens_per_tile;
+  const int S = a.tiles_per_split;
+  const int tt = (int)(t - q_begin);
+  const int qt = tt / tpt;
+  int64_t first = before;
+  for (int k = 0; k < qt; ++k) first += (prefill_key_tiles(ctx, q_len, tpt, k) + S - 1) / S;
+  const int nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
+  if (nsplit <= 1 || first + nsplit > a.ws_items) return;
+  const int h = qh / a.group;
+  const int tpb = 16 / a.group;
+  const int in_tile = tt - qt * tpt;
+  const int row = (in_tile / tpb) * 16 + (in_tile % tpb) * a.group + qh % a.group;
+  const int64_t slot = (first * a.geom.kv_heads + h) * kRows + row;
+  const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;
+  merge_row<T, D>(a.ws_o + slot * D, split_stride * D, a.ws_ml + slot * 2, split_stride * 2, nsplit,
+                  reinterpret_cast<T*>(a.out) + t * a.o_st + qh * a.o_sh);
+}
+
+// Work decomposition of a prefill call, from host-side bounds only: query
+// tiles of tokens_per_tile tokens, each split into items of at most
+// tiles_per_split key tiles, chosen so an upper bound on the total work
+// gives about kPrefillTargetItems workgroups (several resident per CU).
+constexpr int64_t kPrefillTargetItems = 2048;
+constexpr int64_t kPrefillMinTilesPerSplit = 8;
+constexpr int64_t kPrefillMaxTilesPerSplit = 64;
+
+struct PrefillPlan {
+  int row_blocks = 1;  // MFMA row blocks per wave
+  int tokens_per_tile = 64;
+  int64_t tps = kPrefillMaxTilesPerSplit;
+  int64_t items = 0;  // grid.x: an upper bound on the number of items
+  int64_t rows = 0;   // rows per item
+};
+
+PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int64_t total_tokens,
+                         int64_t max_seq_len) {
+  PrefillPlan p;
+  p.row_blocks = group >= 4 ? 4 : (int)group;
+  p.tokens_per_tile = kPrefillWaves * p.row_blocks * (int)(16 / group);
+  p.rows = kPrefillWaves * p.row_blocks * 16;
+  const int64_t qtiles = total_tokens / p.tokens_per_tile + num_seqs;  // >= sum_r ceil(len_r / tpt)
+  const int64_t ktiles = cdiv(max_seq_len, kTileKeys);
+  const int64_t work = qtiles * ktiles;                                 // >= key tiles over all query tiles
+  int64_t tps = cdiv(work * kv_heads, kPrefillTargetItems);
+  tps = tps < kPrefillMinTilesPerSplit ? kPrefillMinTilesPerSplit : tps;
+  tps = tps > kPrefillMaxTilesPerSplit ? kPrefillMaxTilesPerSplit : tps;
+  static const int64_t forced = env_int("NIE_PREFILL_TILES_PER_SPLIT");
+  if (forced > 0) tps = forced < kPrefillMaxTilesPerSplit ? forced : kPrefillMaxTilesPerSplit;
+  p.tps = tps;
+  p.items = work / tps + qtiles + 1;  // sum ceil(n / tps) <= sum n / tps + count
+  return p;
 }
 
 // ---------------------------------------------------------------------------
@@ -1299,13 +1547,29 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
   }
 }
 
-template <typename T, int D>
-void launch_prefill(const PrefillArgs& a, int64_t tiles, hipStream_t stream) {
-  const dim3 grid((unsigned)tiles, (unsigned)a.geom.kv_heads);
+template <typename T, int D, int NB>
+void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, int64_t total_tokens, hipStream_t stream,
+                       bool merge) {
+  const dim3 grid((unsigned)p.items, (unsigned)a.geom.kv_heads);
   if (uniform_tiles(a.geom)) {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+  }
+  if (merge) {
+    const int64_t q_heads = (int64_t)a.geom.kv_heads * a.group;
+    const dim3 mgrid((unsigned)total_tokens, (unsigned)cdiv(q_heads, (int64_t)kMergeWaves));
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a);
+  }
+}
+
+template <typename T, int D>
+void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, int64_t total_tokens, hipStream_t stream,
+                    bool merge) {
+  switch (p.row_blocks) {
+    case 1: launch_prefill_nb<T, D, 1>(a, p, total_tokens, stream, merge); break;
+    case 2: launch_prefill_nb<T, D, 2>(a, p, total_tokens, stream, merge); break;
+    default: launch_prefill_nb<T, D, 4>(a, p, total_tokens, stream, merge); break;
   }
 }
 
@@ -1512,15 +1776,14 @@ NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t tot
                                                    int64_t max_query_len, int64_t max_seq_len,
                                                    int64_t q_heads, int64_t kv_heads,
                                                    int64_t head_dim) {
-  // The prefill kernel writes its output directly; no scratch is needed.
-  (void)num_seqs;
-  (void)total_query_tokens;
   (void)max_query_len;
-  (void)max_seq_len;
-  (void)q_heads;
-  (void)kv_heads;
-  (void)head_dim;
-  return 0;
+  if (num_seqs <= 0 || total_query_tokens <= 0 || max_seq_len <= 0 ||
+      check_attention_shape(q_heads, kv_heads, head_dim, 1, 1) != NIE_OK) {
+    return 0;
+  }
+  const PrefillPlan p = plan_prefill(q_heads / kv_heads, kv_heads, num_seqs, total_query_tokens, max_seq_len);
+  if (cdiv(max_seq_len, kTileKeys) <= p.tps) return 0;  // no query tile is split
+  return p.items * kv_heads * p.rows * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
 NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int64_t q_stride_h,
@@ -1533,8 +1796,6 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
                                int64_t table_stride, float scale, void* out,
                                int64_t out_stride_t, int64_t out_stride_h, void* workspace,
                                int64_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -1559,10 +1820,14 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
     return fail(NIE_EINVAL, "q/out/cache pointers and strides must be 16-byte aligned");
   }
   const int group = (int)(q_heads / kv_heads);
-  const int tpt = kPrefillWaves * (16 / group);
-  // sum_r ceil(len_r / tpt) <= total / tpt + num_seqs
-  const int64_t tiles = total_query_tokens / tpt + num_seqs;
-  if (tiles > 0x7fffffffLL) return fail(NIE_EINVAL, "grid too large");
+  const PrefillPlan plan = plan_prefill(group, kv_heads, num_seqs, total_query_tokens, max_seq_len);
+  if (plan.items > 0x7fffffffLL || total_query_tokens > 0x7fffffffLL) return fail(NIE_EINVAL, "grid too large");
+  const bool may_split = cdiv(max_seq_len, kTileKeys) > plan.tps;
+  const int64_t need = plan.items * kv_heads * plan.rows * (head_dim + 2) * (int64_t)sizeof(float);
+  if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
+    return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,
+                (long long)workspace_bytes);
+  }
   PrefillArgs a;
   a.q = q;
   a.q_st = q_stride_t;
@@ -1574,20 +1839,25 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   a.v_cache = v_cache;
   a.geom = make_geom(layer_index, num_blocks, block_size, kv_heads, head_dim);
   a.group = group;
-  a.tokens_per_tile = tpt;
+  a.tokens_per_tile = plan.tokens_per_tile;
+  a.tiles_per_split = (int32_t)plan.tps;
   a.tables = block_tables;
   a.table_stride = table_stride;
   a.scale = scale;
   a.out = out;
   a.o_st = out_stride_t;
   a.o_sh = out_stride_h;
+  const bool have_ws = may_split && workspace != nullptr && workspace_bytes >= need;
+  a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
+  a.ws_ml = have_ws ? a.ws_o + plan.items * kv_heads * plan.rows * head_dim : nullptr;
+  a.ws_items = have_ws ? plan.items : 0;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, tiles, s);
-    else launch_prefill<bf16_t, 128>(a, tiles, s);
+    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, total_query_tokens, s, may_split);
+    else launch_prefill<bf16_t, 128>(a, plan, total_query_tokens, s, may_split);
   } else {
-    if (head_dim == 64) launch_prefill<float, 64>(a, tiles, s);
-    else launch_prefill<float, 128>(a, tiles, s);
+    if (head_dim == 64) launch_prefill<float, 64>(a, plan, total_query_tokens, s, may_split);
+    else launch_prefill<float, 128>(a, plan, total_query_tokens, s, may_split);
   }
   return launched("varlen_prefill");
 }

@@ -94,9 +94,9 @@ _SIGNATURES = {
 _lib: ctypes.CDLL | None = None
 _lib_lock = threading.Lock()
 
-# Decode workspaces (split partials), one per (device, stream), grown as
-# needed and reused: calls on one stream are ordered, so they can share a
-# buffer; calls on different streams cannot.
+# Split-partial workspaces of the decode and prefill calls, one per (device,
+# stream), grown as needed and reused: calls on one stream are ordered, so
+# they can share a buffer; calls on different streams cannot.
 _decode_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _workspace_lock = threading.Lock()
 
@@ -415,7 +415,8 @@ def varlen_prefill(
     ws_bytes = lib.nie_varlen_prefill_workspace_bytes(
         num_seqs, total_tokens, max_query_len, max_seq_len, q_heads, kv_heads, head_dim
     )
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes > 0 else None
+    stream = _stream(query.device)
+    workspace = _decode_workspace(query.device, stream, ws_bytes) if ws_bytes > 0 else None
     rc = lib.nie_varlen_prefill(
         dtype_code(query.dtype),
         query.data_ptr(), query.stride(0), query.stride(1),
@@ -428,7 +429,7 @@ def varlen_prefill(
         float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
         None if workspace is None else workspace.data_ptr(), 0 if workspace is None else workspace.numel(),
-        _stream(query.device),
+        stream,
     )
     _check(rc, "nie_varlen_prefill")
     return out
@@ -545,18 +546,20 @@ class PreparedPrefill:
                 or not block_tables.is_contiguous()):
             raise ValueError("block_tables must be a contiguous int32 (num_seqs, max_blocks) tensor")
         lib = load_library()
-        if lib.nie_varlen_prefill_workspace_bytes(num_seqs, total_tokens, max_query_len, max_seq_len, q_heads,
-                                                  kv_heads, head_dim) != 0:
-            raise RuntimeError("varlen prefill unexpectedly needs a workspace")
+        ws_bytes = lib.nie_varlen_prefill_workspace_bytes(num_seqs, total_tokens, max_query_len, max_seq_len,
+                                                          q_heads, kv_heads, head_dim)
+        stream = _stream(k_cache.device)
+        workspace = _decode_workspace(k_cache.device, stream, ws_bytes) if ws_bytes > 0 else None
         self._fn = lib.nie_varlen_prefill
         self._dtype = k_cache.dtype
         self._device = k_cache.device
         self._shape = (total_tokens, q_heads, head_dim)
-        self._keep = (cu_seqlens, context_lens, block_tables)
+        self._keep = (cu_seqlens, context_lens, block_tables, workspace)
         self._args = (dtype_code(k_cache.dtype), cu_seqlens.data_ptr(), context_lens.data_ptr(), num_seqs,
                       total_tokens, max_query_len, max_seq_len, k_cache.data_ptr(), v_cache.data_ptr(), num_layers,
                       num_blocks, block_size, q_heads, kv_heads, head_dim, block_tables.data_ptr(),
-                      block_tables.shape[1], float(scale), _stream(k_cache.device))
+                      block_tables.shape[1], float(scale),
+                      (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel()), stream)
 
     def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
         for t in (query, out):
@@ -564,10 +567,10 @@ class PreparedPrefill:
                     or t.data_ptr() % 16):
                 raise ValueError("query/out must be aligned (tokens, q_heads, head_dim) tensors matching the batch")
         (code, cu, ctx, num_seqs, total, max_q, max_s, kptr, vptr, num_layers, num_blocks, block_size, q_heads,
-         kv_heads, head_dim, tables, tstride, scale, stream) = self._args
+         kv_heads, head_dim, tables, tstride, scale, (ws, ws_bytes), stream) = self._args
         rc = self._fn(code, query.data_ptr(), query.stride(0), query.stride(1), cu, ctx, num_seqs, total, max_q,
                       max_s, kptr, vptr, num_layers, layer_index, num_blocks, block_size, q_heads, kv_heads, head_dim,
-                      tables, tstride, scale, out.data_ptr(), out.stride(0), out.stride(1), None, 0, stream)
+                      tables, tstride, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes, stream)
         if rc:
             _check(rc, "nie_varlen_prefill")
         return out

@@ -264,3 +264,21 @@ def test_varlen_prefill_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")
     assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize(
+    "q_heads,kv_heads,head_dim,block_size",
+    [(4, 4, 64, 16), (8, 4, 64, 16), (16, 4, 64, 8), (32, 4, 64, 16), (32, 8, 128, 16), (16, 1, 128, 32)],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_varlen_prefill_split_keys(q_heads, kv_heads, head_dim, block_size, dtype):
+    """Contexts long enough that query tiles are split over several workgroups
+    (at least 8 key tiles per split) and merged, next to short requests and
+    decode rows."""
+    _log(f"varlen split hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype}")
+    wl = workloads.ragged([700, 0, 300, 1500, 33], [70, 130, 1, 9, 64], seed=17, pool_factor=1.3, q_heads=q_heads,
+                          kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
+    got, want = _prefill_case(wl, dtype)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
