@@ -43,6 +43,10 @@ def parse_args():
     p.add_argument("--skip-stress", action="store_true", help="do not run the 16x29600 decode figure")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
     p.add_argument("--skip-mixed", action="store_true", help="do not run the mixed chunked-prefill figure")
+    p.add_argument("--skip-e2e", action="store_true", help="do not run the end-to-end serving figure")
+    p.add_argument("--e2e-only", action="store_true", help="run only the end-to-end serving figure")
+    p.add_argument("--e2e-ref-steps", type=int, default=3,
+                   help="scheduler steps timed with the reference attention algorithm")
     p.add_argument("--mixed-only", action="store_true", help="run only the mixed chunked-prefill figure")
     p.add_argument("--stress-only", action="store_true",
                    help="run only the 16x29600 decode figure (for per-workload profiles)")
@@ -206,6 +210,8 @@ def run_gpu(args):
         result["stress_16x29600"] = run_stress(args)
     if not args.skip_mixed:
         result["mixed_prefill_step"] = run_mixed(args)
+    if not args.skip_e2e:
+        result["e2e_llama1b_serving"] = run_e2e(args)
     return result
 
 
@@ -305,6 +311,105 @@ def run_mixed(args):
     }
 
 
+E2E_REQUESTS = 64
+E2E_NEW_TOKENS = 256
+
+
+def build_e2e_model(device):
+    """Llama-3.2-1B shape (LlamaConfig defaults), bf16, Linear/Embedding weights N(0, 0.02), norms 1."""
+    import torch
+    from torch import nn
+
+    from nano_infer_engine.models.llama import Llama3_2, LlamaConfig
+
+    torch.manual_seed(3)
+    with torch.device(device):
+        model = Llama3_2(LlamaConfig())
+    model = model.to(torch.bfloat16).eval()
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding)):
+                m.weight.normal_(0.0, 0.02)
+    return model
+
+
+def e2e_prompts(device, vocab, count=E2E_REQUESTS, seed=3):
+    import numpy as np
+    import torch
+
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(128, 2049, size=count)
+    return [torch.from_numpy(rng.integers(0, vocab, size=(1, int(n)))).to(device) for n in lens]
+
+
+def e2e_run(model, prompts, device, max_new_tokens, max_steps=None):
+    """Serve every prompt through the continuous-batching scheduler; returns (seconds, steps, requests)."""
+    import torch
+
+    from nano_infer_engine.generation import ContinuousBatchingScheduler, GenerationConfig
+    from nano_infer_engine.paged_cache import PagedKVCache
+
+    cfg = model.config
+    blocks_per_request = -(-(max(p.shape[1] for p in prompts) + max_new_tokens) // 16)
+    cache = PagedKVCache(16 * blocks_per_request + 64, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim,
+                         torch.bfloat16, device)
+    gen = GenerationConfig(max_new_tokens=max_new_tokens, eos_token_id=None, prefill_chunk_size=128,
+                           max_prefill_tokens_per_step=512)
+    sched = ContinuousBatchingScheduler(model, gen, cache, max_batch_size=16)
+    reqs = [sched.add_request(f"request-{i}", p) for i, p in enumerate(prompts)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    steps = 0
+    while sched.has_work and (max_steps is None or steps < max_steps):
+        sched.step()
+        steps += 1
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, steps, reqs
+
+
+def run_e2e(args):
+    """Configuration-4 serving run, and the same model with the reference attention algorithm."""
+    import torch
+
+    import nano_infer_engine.layers.attention as attention_module
+    from oracle import reference_ops
+
+    device = torch.device("cuda:0")
+    model = build_e2e_model(device)
+    prompts = e2e_prompts(device, model.config.vocab_size)
+    e2e_run(model, prompts[:2], device, 8)  # warm-up: library load, GEMM heuristics
+    secs, steps, reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS)
+    out_tokens = sum(r.generated_tokens for r in reqs)
+    tok_s = out_tokens / secs
+    log(f"e2e: {out_tokens} output tokens from {len(prompts)} requests in {secs:.2f} s "
+        f"({steps} steps) -> {tok_s:.0f} tok/s")
+    # the reference attention algorithm (per-request gather / repeat_interleave /
+    # matmul / mask / softmax) under the same scheduler, on the first steps only
+    k = args.e2e_ref_steps
+    ours_k, _, ours_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
+    saved = attention_module.paged_attention
+    attention_module.paged_attention = reference_ops.attention_core_like_product
+    try:
+        ref_k, _, ref_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
+    finally:
+        attention_module.paged_attention = saved
+    same = all(torch.equal(a.sequence, b.sequence) for a, b in zip(ours_reqs, ref_reqs))
+    log(f"e2e first {k} steps: ours {ours_k * 1e3:.1f} ms, reference attention {ref_k * 1e3:.1f} ms "
+        f"({ref_k / ours_k:.1f}x); sequences identical: {same}")
+    del model
+    torch.cuda.empty_cache()
+    return {
+        "output_tok_per_s": round(tok_s, 1),
+        "output_tokens": out_tokens,
+        "seconds": round(secs, 3),
+        "scheduler_steps": steps,
+        "workload": "Llama-3.2-1B shape, bf16, random N(0, 0.02) weights; 64 requests, prompts U[128, 2048] "
+                    "(seed 3), 256 greedy tokens each, max batch 16, prefill chunk 128, 512 prefill tokens/step",
+        "reference_first_steps": {"steps": k, "ours_ms": round(ours_k * 1e3, 2), "reference_ms": round(ref_k * 1e3, 2),
+                                  "speedup": round(ref_k / ours_k, 2), "sequences_identical": same},
+    }
+
+
 def _measured_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if present."""
     path = os.path.join(REPO, "profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json")
@@ -370,6 +475,12 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         run_copy_calibration(args.copy_calibration)
+        return
+    if args.e2e_only:
+        from nano_infer_engine import _native
+
+        _native.load_library()
+        print(json.dumps({"e2e_llama1b_serving": run_e2e(args)}), flush=True)
         return
     if args.mixed_only:
         from nano_infer_engine import _native

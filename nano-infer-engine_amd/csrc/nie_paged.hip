@@ -139,17 +139,22 @@ __device__ __forceinline__ float round_storage(float x) {
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
 // Sum / max of a value over the four lane groups with equal l%16
-// (lanes l, l^16, l^32, l^48).
+// (lanes l, l^16, l^32, l^48).  v_permlane16_swap / v_permlane32_swap of a
+// value with itself give every lane its l^16 (then l^32) partner in one of
+// the two results, so the reduction needs no LDS crossbar; the order of the
+// operations (pairs first) makes every lane's result identical.
 __device__ __forceinline__ float sum_over_groups(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ float max_over_groups(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
@@ -383,6 +388,41 @@ __device__ __forceinline__ void softmax_tile(SoftmaxState<D>& st, v4f& s) {
     st.lsum += tsum;
   }
   st.m = m_new;
+}
+
+// softmax_tile for kBlocks row blocks at once, with one (wave-uniform)
+// rescale decision for all of them, so the blocks' chains interleave.
+template <int D, int kBlocks>
+__device__ __forceinline__ void softmax_tiles(SoftmaxState<D> (&st)[kBlocks], v4f (&s)[kBlocks]) {
+  float m_new[kBlocks], nref[kBlocks], tsum[kBlocks];
+  bool moved = false;
+#pragma unroll
+  for (int nb = 0; nb < kBlocks; ++nb) {
+    const float tmax = max_over_groups(fmaxf(fmaxf(s[nb][0], s[nb][1]), fmaxf(s[nb][2], s[nb][3])));
+    m_new[nb] = fmaxf(st[nb].m, tmax);
+    nref[nb] = (m_new[nb] == kNegInf) ? 0.f : -m_new[nb] * kLog2e;
+    tsum[nb] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[nb][i] = fast_exp2(fmaf(s[nb][i], kLog2e, nref[nb]));
+      tsum[nb] += s[nb][i];
+    }
+    moved |= m_new[nb] != st[nb].m;
+  }
+  if (__ballot(moved)) {
+#pragma unroll
+    for (int nb = 0; nb < kBlocks; ++nb) {
+      const float alpha = fast_exp2(fmaf(st[nb].m, kLog2e, nref[nb]));
+      st[nb].lsum = st[nb].lsum * alpha + tsum[nb];
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) st[nb].o[c] *= alpha;
+    }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < kBlocks; ++nb) st[nb].lsum += tsum[nb];
+  }
+#pragma unroll
+  for (int nb = 0; nb < kBlocks; ++nb) st[nb].m = m_new[nb];
 }
 
 // O^T += V^T . P^T for one 16-key tile.  `vt` is the LDS copy of the tile's
@@ -1166,7 +1206,71 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
     for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, 0, 16 * c + row);
   }
 
+  // Tiles every row of every block sees in full (below the first block's
+  // first position and the item's end): no masks, no per-block branches.
+  auto consume_full = [&](int slot) {
+    const unsigned char* stage = &ring[slot][0];
+    F kf;
+    if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t sb = lds_off(stage);
+      uint32_t ka[F::kVec];
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) ka[j] = sb + koff[j];
+      ring_read_k<F::kVec>(kf.v, ka);
+    } else {
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
+    }
+    v4f p[kRowBlocks];
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) {
+      p[nb] = qk_mfma<T, D>(kf, qf[nb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[nb][i] = scaled_score<T>(p[nb][i], a.scale);
+    }
+    softmax_tiles<D, kRowBlocks>(st, p);
+    if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t sb = lds_off(stage);
+      v4s pb[kRowBlocks];
+#pragma unroll
+      for (int nb = 0; nb < kRowBlocks; ++nb) pb[nb] = pack_bf16x4(p[nb][0], p[nb][1], p[nb][2], p[nb][3]);
+#pragma unroll
+      for (int c0 = 0; c0 < D / 16; c0 += 4) {
+        uint32_t va[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) va[i] = sb + voff[4 * c0 + i];
+        v4s vt[4];
+        ring_read_vt16(vt, va);
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            st[nb].o[c0 + c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[c], pb[nb], st[nb].o[c0 + c], 0, 0, 0);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        float vv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vv[j] = *reinterpret_cast<const float*>(stage + voff[4 * c + j]);
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], p[nb][j], st[nb].o[c], 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+
   auto consume = [&](int slot, int key0) {
+    if (key0 + kTileKeys - 1 <= min(block_first[0], last)) {
+      consume_full(slot);
+      return;
+    }
     const unsigned char* stage = &ring[slot][0];
     F kf;
     if constexpr (Elt<T>::kIsBf16) {
