@@ -387,12 +387,12 @@ def run_e2e(args):
     # matmul / mask / softmax) under the same scheduler, on the first steps only
     k = args.e2e_ref_steps
     ours_k, _, ours_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
-    saved = attention_module.paged_attention
-    attention_module.paged_attention = reference_ops.attention_core_like_product
+    saved = attention_module.attention_core
+    attention_module.attention_core = reference_ops.attention_core_like_product
     try:
         ref_k, _, ref_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
     finally:
-        attention_module.paged_attention = saved
+        attention_module.attention_core = saved
     same = all(torch.equal(a.sequence, b.sequence) for a, b in zip(ours_reqs, ref_reqs))
     log(f"e2e first {k} steps: ours {ours_k * 1e3:.1f} ms, reference attention {ref_k * 1e3:.1f} ms "
         f"({ref_k / ours_k:.1f}x); sequences identical: {same}")

@@ -116,6 +116,38 @@ int nie_kv_copy_blocks(int dtype,
                        void* stream);
 
 /*
+ * Fused RoPE + KV append for num_tokens new tokens of one layer: rotates the
+ * q rows in place, and writes the rotated k rows and the v rows to cache slot
+ * slot_mapping[t] (a negative or out-of-pool slot skips the K/V write).
+ *   q     : (num_tokens, q_heads, head_dim), element (t, h, d) at
+ *           t * q_stride_t + h * q_stride_h + d;  k_new / v_new likewise
+ *           with kv_heads heads.
+ *   positions  : (num_tokens,) int64 absolute positions.
+ *   cos_table / sin_table : (table_rows, head_dim / 2) in the storage dtype;
+ *           row p holds cos / sin of p * inv_freq[i] (positions past the
+ *           table are clamped to its last row; callers size the table).
+ * Rotate-half with every product and sum rounded to the storage dtype, so
+ * the output is bit-identical to the reference's elementwise torch ops fed
+ * the same sin/cos rows; the K/V writes are bit-exact copies of those rows.
+ * head_dim must be 64 or 128.
+ * Replaces: the RoPE of q and k (src/nano_infer_engine/layers/rope.py:6-23,
+ *           called at src/nano_infer_engine/layers/attention.py:238-239 and
+ *           :375-376) followed by PagedKVCache.write of the new K/V
+ *           (attention.py:246-253, :384-390; paged_cache.py:264-322).
+ */
+int nie_rope_kv_append(int dtype,
+                       void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t q_heads,
+                       const void* k_new, int64_t k_stride_t, int64_t k_stride_h,
+                       const void* v_new, int64_t v_stride_t, int64_t v_stride_h,
+                       const int64_t* positions, const int64_t* slot_mapping, int64_t num_tokens,
+                       const void* cos_table, const void* sin_table, int64_t table_rows,
+                       void* k_cache, void* v_cache,
+                       int64_t num_layers, int64_t layer_index,
+                       int64_t num_blocks, int64_t block_size,
+                       int64_t kv_heads, int64_t head_dim,
+                       void* stream);
+
+/*
  * Workspace bytes needed by nie_paged_decode for a call with these
  * arguments (same meaning as there; host values), whose sequence lengths
  * have maximum max_seq_len and sum total_seq_len.  The split of the work

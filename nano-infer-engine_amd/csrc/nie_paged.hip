@@ -566,6 +566,112 @@ __global__ __launch_bounds__(256) void kv_copy_blocks_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Fused RoPE + KV append
+// ---------------------------------------------------------------------------
+// One grid row = one head of one token: rows t*(Hq + 2*Hkv) + j cover the q
+// heads (j < Hq), then the k heads, then the v heads of token t.  A row takes
+// D/2 lanes; lane i rotates the pair (x[i], x[i + D/2]) by the angle of
+// frequency i at the token's position:
+//     out[i]       = x[i]*cos - x[i+D/2]*sin
+//     out[i + D/2] = x[i+D/2]*cos + x[i]*sin
+// with every product and sum rounded to the storage dtype, as the
+// reference's elementwise torch ops do (layers/rope.py:6-23), so the result
+// is bit-identical to them given the same sin/cos rows.  q rows are rotated
+// in place; rotated k rows and unrotated v rows go to the cache slot of the
+// token (a negative or out-of-pool slot is skipped, as in kv_append).
+struct RopeAppendArgs {
+  void* q;
+  int64_t q_st, q_sh;
+  const void* k;
+  int64_t k_st, k_sh;
+  const void* v;
+  int64_t v_st, v_sh;
+  const int64_t* positions;
+  const int64_t* slots;
+  int64_t num_tokens;
+  const void* cos_table;  // (table_rows, head_dim / 2)
+  const void* sin_table;
+  int64_t table_rows;
+  void* k_cache;
+  void* v_cache;
+  int64_t layer_offset;  // elements before the layer
+  int64_t pool_slots;    // num_blocks * block_size
+  int32_t q_heads;
+  int32_t kv_heads;
+};
+
+template <typename T>
+__device__ __forceinline__ float load_elt(const void* base, int64_t i) {
+  if constexpr (Elt<T>::kIsBf16) {
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+  } else {
+    return reinterpret_cast<const float*>(base)[i];
+  }
+}
+
+// a*b and a+-b in the storage dtype, each rounded on its own: contraction
+// into fused multiply-adds (hipcc's default) is switched off here, because
+// the reference computes every product and sum as a separate torch op.
+template <typename T>
+__device__ __forceinline__ float mul_t(float a, float b) {
+#pragma clang fp contract(off)
+  return round_storage<T>(a * b);
+}
+template <typename T>
+__device__ __forceinline__ float add_t(float a, float b) {
+#pragma clang fp contract(off)
+  return round_storage<T>(a + b);
+}
+template <typename T>
+__device__ __forceinline__ float sub_t(float a, float b) {
+#pragma clang fp contract(off)
+  return round_storage<T>(a - b);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
+  constexpr int kHalf = D / 2;
+  constexpr int kRowsPerBlock = 256 / kHalf;
+  const int sub = threadIdx.x / kHalf;
+  const int i = threadIdx.x % kHalf;
+  const int heads = a.q_heads + 2 * a.kv_heads;
+  const int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + sub;
+  if (r >= a.num_tokens * heads) return;
+  const int64_t t = r / heads;
+  const int j = (int)(r - t * heads);
+  int64_t pos = a.positions[t];
+  pos = pos < 0 ? 0 : (pos >= a.table_rows ? a.table_rows - 1 : pos);
+  const float c = load_elt<T>(a.cos_table, pos * kHalf + i);
+  const float s = load_elt<T>(a.sin_table, pos * kHalf + i);
+  if (j < a.q_heads) {
+    T* x = reinterpret_cast<T*>(a.q) + t * a.q_st + (int64_t)j * a.q_sh;
+    const float x1 = load_elt<T>(x, i);
+    const float x2 = load_elt<T>(x, i + kHalf);
+    store_elt<T>(x + i, sub_t<T>(mul_t<T>(x1, c), mul_t<T>(x2, s)));
+    store_elt<T>(x + i + kHalf, add_t<T>(mul_t<T>(x2, c), mul_t<T>(x1, s)));
+    return;
+  }
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.pool_slots) return;
+  const bool is_k = j < a.q_heads + a.kv_heads;
+  const int h = is_k ? j - a.q_heads : j - a.q_heads - a.kv_heads;
+  const int64_t dst_off = a.layer_offset + (slot * a.kv_heads + h) * D;
+  if (is_k) {
+    const T* x = reinterpret_cast<const T*>(a.k) + t * a.k_st + (int64_t)h * a.k_sh;
+    const float x1 = load_elt<T>(x, i);
+    const float x2 = load_elt<T>(x, i + kHalf);
+    T* dst = reinterpret_cast<T*>(a.k_cache) + dst_off;
+    store_elt<T>(dst + i, sub_t<T>(mul_t<T>(x1, c), mul_t<T>(x2, s)));
+    store_elt<T>(dst + i + kHalf, add_t<T>(mul_t<T>(x2, c), mul_t<T>(x1, s)));
+  } else {
+    const T* x = reinterpret_cast<const T*>(a.v) + t * a.v_st + (int64_t)h * a.v_sh;
+    T* dst = reinterpret_cast<T*>(a.v_cache) + dst_off;
+    dst[i] = x[i];
+    dst[i + kHalf] = x[i + kHalf];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Paged decode (split-K)
 // ---------------------------------------------------------------------------
 constexpr int kDecodeWaves = 8;  // KV heads handled by one workgroup (one per wave)
@@ -1783,6 +1889,62 @@ NIE_API int nie_kv_copy_blocks(int dtype, const void* src_k, const void* src_v,
                      (unsigned char*)dst_k, (unsigned char*)dst_v, dst_num_blocks, dst_blocks,
                      count, block_bytes, vec_ok);
   return launched("kv_copy_blocks");
+}
+
+NIE_API int nie_rope_kv_append(int dtype, void* q, int64_t q_stride_t, int64_t q_stride_h, int64_t q_heads,
+                               const void* k_new, int64_t k_stride_t, int64_t k_stride_h, const void* v_new,
+                               int64_t v_stride_t, int64_t v_stride_h, const int64_t* positions,
+                               const int64_t* slot_mapping, int64_t num_tokens, const void* cos_table,
+                               const void* sin_table, int64_t table_rows, void* k_cache, void* v_cache,
+                               int64_t num_layers, int64_t layer_index, int64_t num_blocks, int64_t block_size,
+                               int64_t kv_heads, int64_t head_dim, void* stream) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
+  if (rc) return rc;
+  if (head_dim != 64 && head_dim != 128) return fail(NIE_EUNSUPPORTED, "head_dim %lld not built", (long long)head_dim);
+  if (num_tokens < 0 || q_heads < 0) return fail(NIE_EINVAL, "num_tokens and q_heads must be non-negative");
+  if (num_tokens == 0) return NIE_OK;
+  if (!q || !k_new || !v_new || !positions || !slot_mapping || !cos_table || !sin_table || !k_cache || !v_cache) {
+    return fail(NIE_EINVAL, "null pointer argument");
+  }
+  if (table_rows <= 0) return fail(NIE_EINVAL, "the sin/cos table must have at least one row");
+  const int64_t heads = q_heads + 2 * kv_heads;
+  const int rows_per_block = 256 / (int)(head_dim / 2);
+  const int64_t blocks = cdiv(num_tokens * heads, rows_per_block);
+  if (heads > 0x7fffffffLL || blocks > 0x7fffffffLL) return fail(NIE_EINVAL, "too many tokens");
+  RopeAppendArgs a;
+  a.q = q;
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.k = k_new;
+  a.k_st = k_stride_t;
+  a.k_sh = k_stride_h;
+  a.v = v_new;
+  a.v_st = v_stride_t;
+  a.v_sh = v_stride_h;
+  a.positions = positions;
+  a.slots = slot_mapping;
+  a.num_tokens = num_tokens;
+  a.cos_table = cos_table;
+  a.sin_table = sin_table;
+  a.table_rows = table_rows;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.layer_offset = layer_index * num_blocks * block_size * kv_heads * head_dim;
+  a.pool_slots = num_blocks * block_size;
+  a.q_heads = (int32_t)q_heads;
+  a.kv_heads = (int32_t)kv_heads;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks);
+  if (dtype == NIE_DTYPE_BF16) {
+    if (head_dim == 64) hipLaunchKernelGGL((rope_kv_append_kernel<bf16_t, 64>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((rope_kv_append_kernel<bf16_t, 128>), grid, dim3(256), 0, s, a);
+  } else {
+    if (head_dim == 64) hipLaunchKernelGGL((rope_kv_append_kernel<float, 64>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((rope_kv_append_kernel<float, 128>), grid, dim3(256), 0, s, a);
+  }
+  return launched("rope_kv_append");
 }
 
 NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,

@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "nie_kv_append",
     "nie_kv_gather",
     "nie_kv_copy_blocks",
+    "nie_rope_kv_append",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_varlen_prefill_workspace_bytes",
@@ -57,6 +58,19 @@ _SIGNATURES = {
     "nie_kv_copy_blocks": (
         _i32,
         [_i32, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr],
+    ),
+    "nie_rope_kv_append": (
+        _i32,
+        [
+            _i32, _ptr, _i64, _i64, _i64,    # dtype, q, q strides, q_heads
+            _ptr, _i64, _i64,                # k, strides
+            _ptr, _i64, _i64,                # v, strides
+            _ptr, _ptr, _i64,                # positions, slots, tokens
+            _ptr, _ptr, _i64,                # cos, sin, table rows
+            _ptr, _ptr,                      # caches
+            _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
+            _i64, _i64, _ptr,                # kv_heads, head_dim, stream
+        ],
     ),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "nie_paged_decode": (
@@ -233,6 +247,60 @@ def kv_append(
         _stream(k_cache.device),
     )
     _check(rc, "nie_kv_append")
+
+
+def _check_rope_inputs(q, k, v, positions, slot_mapping, cos_table, sin_table, dtype, kv_heads, head_dim):
+    _require_gpu(q, k, v, positions, slot_mapping, cos_table, sin_table)
+    tokens = positions.shape[0] if positions.ndim == 1 else -1
+    for name, t in (("positions", positions), ("slot_mapping", slot_mapping)):
+        if t.dtype != torch.int64 or t.ndim != 1 or t.shape[0] != tokens or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous 1D int64 tensor with one entry per token")
+    for name, t, heads in (("q", q, None), ("k", k, kv_heads), ("v", v, kv_heads)):
+        if t.dtype != dtype or t.ndim != 3 or t.shape[0] != tokens or t.shape[2] != head_dim or t.stride(2) != 1:
+            raise ValueError(f"{name} must be (tokens, heads, head_dim) rows in the cache dtype")
+        if heads is not None and t.shape[1] != heads:
+            raise ValueError(f"{name} must have {heads} heads")
+    half = head_dim // 2
+    for name, t in (("cos_table", cos_table), ("sin_table", sin_table)):
+        if t.dtype != dtype or t.ndim != 2 or t.shape[1] != half or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous (positions, head_dim / 2) tensor in the cache dtype")
+    if cos_table.shape != sin_table.shape or cos_table.shape[0] == 0:
+        raise ValueError("cos_table and sin_table must have the same non-empty shape")
+
+
+def rope_kv_append(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    layer_index: int,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    positions: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+) -> None:
+    """RoPE of q (in place) and k at ``positions``, then k/v rows to slot ``slot_mapping[t]``.
+
+    ``cos_table``/``sin_table`` row p holds cos/sin of p * inv_freq in the
+    cache dtype; every position must have a row (checked on the host when the
+    positions are host-visible, clamped on the device otherwise).
+    """
+    num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+    _check_rope_inputs(q, k, v, positions, slot_mapping, cos_table, sin_table, k_cache.dtype, kv_heads, head_dim)
+    lib = load_library()
+    rc = lib.nie_rope_kv_append(
+        dtype_code(k_cache.dtype),
+        q.data_ptr(), q.stride(0), q.stride(1), q.shape[1],
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        positions.data_ptr(), slot_mapping.data_ptr(), positions.shape[0],
+        cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0],
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim,
+        _stream(k_cache.device),
+    )
+    _check(rc, "nie_rope_kv_append")
 
 
 def kv_gather(
@@ -475,6 +543,43 @@ class PreparedAppend:
                       self._stream)
         if rc:
             _check(rc, "nie_kv_append")
+
+
+class PreparedRopeAppend:
+    """``rope_kv_append`` for one batch (positions, slots, sin/cos table), any layer."""
+
+    __slots__ = ("_fn", "_args", "_tokens", "_dtype", "_device", "_kv", "_keep")
+
+    def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, positions: torch.Tensor,
+                 slot_mapping: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor):
+        num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
+        tokens = positions.shape[0] if positions.ndim == 1 else 0
+        empty = torch.empty((tokens, kv_heads, head_dim), dtype=k_cache.dtype, device=k_cache.device)
+        _check_rope_inputs(empty, empty, empty, positions, slot_mapping, cos_table, sin_table, k_cache.dtype,
+                           kv_heads, head_dim)
+        self._fn = load_library().nie_rope_kv_append
+        self._dtype = k_cache.dtype
+        self._device = k_cache.device
+        self._tokens = tokens
+        self._kv = (kv_heads, head_dim)
+        self._keep = (positions, slot_mapping, cos_table, sin_table)
+        self._args = (positions.data_ptr(), slot_mapping.data_ptr(), tokens, cos_table.data_ptr(),
+                      sin_table.data_ptr(), cos_table.shape[0], k_cache.data_ptr(), v_cache.data_ptr(), num_layers,
+                      num_blocks, block_size, kv_heads, head_dim, _stream(k_cache.device))
+
+    def __call__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_index: int) -> None:
+        kv_heads, head_dim = self._kv
+        for t, heads in ((q, None), (k, kv_heads), (v, kv_heads)):
+            if (t.dtype != self._dtype or t.device != self._device or t.ndim != 3 or t.shape[0] != self._tokens
+                    or t.shape[2] != head_dim or t.stride(2) != 1 or (heads is not None and t.shape[1] != heads)):
+                raise ValueError("q/k/v must be (tokens, heads, head_dim) rows matching the batch and the cache")
+        (pos, slots, tokens, cos, sin, rows, kptr, vptr, num_layers, num_blocks, block_size, _, _,
+         stream) = self._args
+        rc = self._fn(_DTYPE_CODES[self._dtype], q.data_ptr(), q.stride(0), q.stride(1), q.shape[1], k.data_ptr(),
+                      k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), pos, slots, tokens, cos, sin,
+                      rows, kptr, vptr, num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim, stream)
+        if rc:
+            _check(rc, "nie_rope_kv_append")
 
 
 class PreparedDecode:

@@ -4,9 +4,10 @@ Public surface of ``GroupedQueryAttention`` in ``layers/attention.py:121-414``
 of the reference engine: the constructor, ``forward`` with its paged decode
 branch (``paged_cache=``, ``layer_index=``, ``sequence_id=``,
 ``sequence_ids=``; same checks and messages) and ``forward_ragged``.  The
-projections, RoPE and output projection stay torch ops; the K/V write and
-the attention itself go through :func:`paged_batch.paged_attention`
-(one ``kv_append`` launch plus the decode / varlen-prefill kernels).
+projections and output projection stay torch ops; RoPE, the K/V write and
+the attention itself go through :data:`attention_core`
+(:func:`paged_batch.attention_core`: one fused RoPE + KV-append launch plus
+the decode / varlen-prefill kernels).
 
 Both methods take an optional ``paged_batch`` — the per-forward metadata the
 model builds once for all layers.  Without it they build their own, so the
@@ -21,8 +22,14 @@ import torch
 from torch import nn
 
 from nano_infer_engine.layers.rope import Rope
-from nano_infer_engine.paged_batch import RaggedBatch, build_ragged_batch, paged_attention
+from nano_infer_engine import paged_batch as _paged_batch
+from nano_infer_engine.paged_batch import RaggedBatch, build_ragged_batch
 from nano_infer_engine.paged_cache import PagedKVCache
+
+#: Per-layer attention core: (q, k, v, cache, layer_index, batch, scale, rope)
+#: -> context, with q/k not yet rotated.  Module-level so a caller can swap
+#: in another implementation of the same contract.
+attention_core = _paged_batch.attention_core
 
 
 class GroupedQueryAttention(nn.Module):
@@ -54,9 +61,7 @@ class GroupedQueryAttention(nn.Module):
         q = self.q_proj(x).view(tokens, self.q_head_num, self.head_dim)
         k = self.k_proj(x).view(tokens, self.kv_head_num, self.head_dim)
         v = self.v_proj(x).view(tokens, self.kv_head_num, self.head_dim)
-        q = self.rope.rotate_tokens(q, batch.positions)
-        k = self.rope.rotate_tokens(k, batch.positions)
-        context = paged_attention(q, k, v, paged_cache, layer_index, batch, self.head_dim**-0.5)
+        context = attention_core(q, k, v, paged_cache, layer_index, batch, self.head_dim**-0.5, self.rope)
         return self.o_proj(context.view(tokens, self.hidden_size))
 
     def forward(

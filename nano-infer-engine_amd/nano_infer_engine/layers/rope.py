@@ -4,7 +4,8 @@ Numerics follow ``layers/rope.py:6-200`` of the reference engine: inverse
 frequencies and angles in fp32, sin/cos cast to the activation dtype, then
 the rotate-half update ``(x1*cos - x2*sin, x2*cos + x1*sin)`` in the
 activation dtype.  The inverse-frequency vector is computed once per device
-instead of on every call.
+instead of on every call, and :meth:`_RopeBase.tables` keeps per-position
+sin/cos rows for the fused RoPE + KV-append kernel.
 """
 
 from __future__ import annotations
@@ -30,6 +31,7 @@ class _RopeBase(nn.Module):
         self.dim = dim
         self.theta_base = theta_base
         self._inv_freq: dict[torch.device, torch.Tensor] = {}
+        self._tables: dict[tuple[torch.device, torch.dtype], tuple[torch.Tensor, torch.Tensor]] = {}
 
     def _compute_inv_freq(self, device: torch.device) -> torch.Tensor:
         exponents = torch.arange(0, self.dim, 2, dtype=torch.float32, device=device) / self.dim
@@ -46,6 +48,23 @@ class _RopeBase(nn.Module):
         """sin/cos of shape positions.shape + (dim/2,), cast to ``dtype``."""
         angles = positions.to(torch.float32)[..., None] * self.inv_freq(positions.device)
         return torch.sin(angles).to(dtype), torch.cos(angles).to(dtype)
+
+    def tables(self, device: torch.device, dtype: torch.dtype, rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """(cos, sin) tables with at least ``rows`` rows: row p = cos/sin of p * inv_freq in ``dtype``.
+
+        Built with the same torch ops as :meth:`sin_cos`, so row p equals
+        ``sin_cos(p)`` bit for bit; the fused RoPE + KV-append kernel reads
+        them.  Grown (and rebuilt) in steps of 4096 positions.
+        """
+        key = (device, dtype)
+        cached = self._tables.get(key)
+        if cached is None or cached[0].shape[0] < rows:
+            size = max(4096, -(-rows // 4096) * 4096)
+            positions = torch.arange(size, dtype=torch.int64, device=device)
+            sin, cos = self.sin_cos(positions, dtype)
+            cached = (cos.contiguous(), sin.contiguous())
+            self._tables[key] = cached
+        return cached
 
     def forward(self, x: torch.Tensor, position_offset: int = 0, position_ids: torch.Tensor | None = None):
         """x: (B, S, H, D).  Positions are offset..offset+S-1 or ``position_ids`` (B, S)."""

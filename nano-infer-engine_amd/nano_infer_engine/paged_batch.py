@@ -10,9 +10,9 @@ every layer from Python tuples (``layers/attention.py:210-261``,
   the decode and varlen-prefill kernels read,
 * ``positions`` — absolute RoPE position of every new token.
 
-:func:`paged_attention` is the per-layer attention core: one ``kv_append``
-launch, then ``paged_decode`` for requests with a single new token and
-``varlen_prefill`` for the rest.
+:func:`attention_core` is the per-layer attention core: one fused RoPE +
+KV-append launch (``rope_kv_append``), then ``paged_decode`` for requests
+with a single new token and ``varlen_prefill`` for the rest.
 """
 
 from __future__ import annotations
@@ -53,18 +53,24 @@ class RaggedBatch:
         """Packed row of the first single-token (decode) request."""
         return self.num_tokens - (self.num_requests - self.decode_from)
 
-    def launchers(self, cache: PagedKVCache, q_heads: int, scale: float):
-        """(append, prefill or None, decode or None) launches of this batch on ``cache``.
+    @property
+    def max_seq_len(self) -> int:
+        """Longest sequence after this batch's tokens are appended."""
+        return max(c + n for c, n in zip(self.context_lens, self.query_lens))
+
+    def launchers(self, cache: PagedKVCache, q_heads: int, scale: float, rope):
+        """(rope + append, prefill or None, decode or None) launches of this batch on ``cache``.
 
         Built once and reused by every layer: the cache pointers, metadata,
-        launch plan, workspace and stream are resolved here, so a layer's
-        attention costs one C call per kernel family.
+        sin/cos tables, launch plan, workspace and stream are resolved here,
+        so a layer's attention costs one C call per kernel family.
         """
-        key = (cache.keys.data_ptr(), q_heads, float(scale))
+        key = (cache.keys.data_ptr(), q_heads, float(scale), id(rope))
         found = self._launch.get(key)
         if found is not None:
             return found
-        append = _native.PreparedAppend(cache.keys, cache.values, self.slot_mapping)
+        cos, sin = rope.tables(cache.keys.device, cache.keys.dtype, self.max_seq_len)
+        append = _native.PreparedRopeAppend(cache.keys, cache.values, self.positions, self.slot_mapping, cos, sin)
         split = self.decode_from
         prefill = decode = None
         if split > 0:
@@ -148,7 +154,7 @@ def build_ragged_batch(
     )
 
 
-def paged_attention(
+def attention_core(
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
@@ -156,17 +162,20 @@ def paged_attention(
     layer_index: int,
     batch: RaggedBatch,
     scale: float,
+    rope,
 ) -> torch.Tensor:
-    """Append the batch's new K/V to ``layer_index`` and attend.
+    """RoPE, append the batch's new K/V to ``layer_index``, and attend.
 
-    q: (num_tokens, Hq, D); k, v: (num_tokens, Hkv, D).  Returns the
-    attention context (num_tokens, Hq, D).  Every new token attends to its
-    sequence's cached prefix and, causally, to the new tokens before it
-    (``layers/attention.py:378-411`` of the reference).
+    q: (num_tokens, Hq, D); k, v: (num_tokens, Hkv, D), not yet rotated.
+    Returns the attention context (num_tokens, Hq, D).  q and k are rotated
+    at the batch's positions (``layers/attention.py:375-376`` of the
+    reference) by the fused RoPE + KV-append kernel, which rotates q in
+    place; every new token then attends to its sequence's cached prefix and,
+    causally, to the new tokens before it (``layers/attention.py:378-411``).
     """
-    append, prefill, decode = batch.launchers(cache, q.shape[1], scale)
-    append(_rows(k), _rows(v), layer_index)
+    append, prefill, decode = batch.launchers(cache, q.shape[1], scale, rope)
     q = _rows(q)
+    append(q, k, v, layer_index)
     out = torch.empty_like(q)
     split = batch.first_decode_token
     if prefill is not None:

@@ -10,6 +10,8 @@ CPU tests, the GPU for the reference-PyTorch-path comparison).
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 
@@ -116,13 +118,75 @@ def ragged_attention_reference(
     return torch.cat(outputs, dim=0)
 
 
-def attention_core_like_product(q, k, v, cache, layer_index, batch, scale):
-    """Same signature as the product's per-layer attention core, computed by
+def rope_inv_freq(dim: int, theta_base: float, scaling: dict | None = None, device=None) -> torch.Tensor:
+    """Inverse frequencies of the reference RoPE.
+
+    Plain: ``1 / theta ** (arange(0, dim, 2) / dim)`` (``layers/rope.py:33-35``).
+    With ``scaling`` (keys factor, low_freq_factor, high_freq_factor,
+    original_max_position_embeddings) the llama3 banded rescale of
+    ``layers/rope.py:99-147``: wavelengths above old_ctx/low are divided by the
+    factor, those below old_ctx/high kept, the band between interpolated.
+    """
+    i = torch.arange(0, dim, 2, dtype=torch.float32, device=device)
+    inv_freq = 1 / theta_base ** (i / dim)
+    if scaling is None:
+        return inv_freq
+    wavelen = 2 * math.pi / inv_freq
+    old_ctx = scaling["original_max_position_embeddings"]
+    low_freq_wavelen = old_ctx / scaling["low_freq_factor"]
+    high_freq_wavelen = old_ctx / scaling["high_freq_factor"]
+    scaled_inv_freq = inv_freq / scaling["factor"]
+    smooth_factor = (old_ctx / wavelen - scaling["low_freq_factor"]) / (
+        scaling["high_freq_factor"] - scaling["low_freq_factor"]
+    )
+    smooth_inv_freq = (1 - smooth_factor) * scaled_inv_freq + smooth_factor * inv_freq
+    is_low_freq = wavelen > low_freq_wavelen
+    is_high_freq = wavelen < high_freq_wavelen
+    is_medium_freq = ~(is_low_freq | is_high_freq)
+    inv_freq = torch.where(is_low_freq, scaled_inv_freq, inv_freq)
+    return torch.where(is_medium_freq, smooth_inv_freq, inv_freq)
+
+
+def rope_reference(x: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor) -> torch.Tensor:
+    """RoPE of packed rows x (T, H, D) at int64 ``positions`` (T,).
+
+    Follows the position_ids branches of ``layers/rope.py:59-75`` and
+    ``:184-200`` (fp32
+    angles ``position * inv_freq``, sin/cos cast to x's dtype) and
+    ``_apply_rotary_emb`` (``layers/rope.py:6-23``): halves by ``chunk``,
+    ``(x1*cos - x2*sin, x2*cos + x1*sin)`` concatenated.
+    """
+    angles = positions.to(device=x.device, dtype=torch.float32)[:, None] * inv_freq
+    sin = torch.sin(angles).to(x.dtype)[:, None, :]
+    cos = torch.cos(angles).to(x.dtype)[:, None, :]
+    x_first, x_second = x.chunk(2, dim=-1)
+    return torch.cat((x_first * cos - x_second * sin, x_second * cos + x_first * sin), dim=-1)
+
+
+def rope_module_inv_freq(rope, device) -> torch.Tensor:
+    """:func:`rope_inv_freq` for the hyperparameters of a product RoPE module."""
+    scaling = None
+    if hasattr(rope, "scaling_factor"):
+        scaling = {
+            "factor": rope.scaling_factor,
+            "low_freq_factor": rope.low_freq_factor,
+            "high_freq_factor": rope.high_freq_factor,
+            "original_max_position_embeddings": rope.original_max_position_embeddings,
+        }
+    return rope_inv_freq(rope.dim, rope.theta_base, scaling, device)
+
+
+def attention_core_like_product(q, k, v, cache, layer_index, batch, scale, rope):
+    """Same contract as the product's per-layer attention core (q, k not yet
+    rotated): :func:`rope_reference` on q and k, then
     :func:`ragged_attention_reference` on the cache's storage tensors.
 
     Used to run the product model with the reference algorithm swapped in
     (the "reference PyTorch path" of the end-to-end comparison).
     """
+    inv_freq = rope_module_inv_freq(rope, q.device)
+    q = rope_reference(q, batch.positions, inv_freq)
+    k = rope_reference(k, batch.positions, inv_freq)
     tables = [cache.get_block_table(s) for s in batch.sequence_ids]
     return ragged_attention_reference(
         q, k, v, cache.keys, cache.values, layer_index, tables, batch.context_lens, batch.query_lens, scale

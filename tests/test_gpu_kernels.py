@@ -128,6 +128,48 @@ def test_kv_copy_blocks_round_trip():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim", [(32, 8, 64), (8, 2, 128)])
+def test_rope_kv_append_bit_exact(dtype, q_heads, kv_heads, head_dim):
+    """Fused RoPE + append == the oracle's RoPE (torch ops, same device) + slot writes, bit for bit.
+
+    q/k/v are strided views of one (tokens, Hq + 2*Hkv, D) buffer, as a
+    fused QKV projection produces; one token has slot -1 (skipped) and the
+    positions reach the end of a 29600-token context.
+    """
+    from nano_infer_engine.layers.rope import RopeScale
+
+    _log(f"rope_kv_append {dtype} hq={q_heads} hkv={kv_heads} d={head_dim}")
+    gen = torch.Generator(device=DEV).manual_seed(31)
+    tokens, num_blocks, bs, layers, layer = 37, 64, 16, 2, 1
+    qkv = torch.randn((tokens, q_heads + 2 * kv_heads, head_dim), generator=gen, device=DEV).to(dtype)
+    q, k, v = qkv[:, :q_heads], qkv[:, q_heads : q_heads + kv_heads], qkv[:, q_heads + kv_heads :]
+    positions = torch.randint(0, 29600, (tokens,), generator=gen, device=DEV, dtype=torch.int64)
+    positions[:3] = torch.tensor([0, 1, 29599], device=DEV)
+    slots = torch.randperm(num_blocks * bs, generator=gen, device=DEV)[:tokens].to(torch.int64)
+    slots[5] = -1
+    kc = torch.randn((layers, num_blocks, bs, kv_heads, head_dim), generator=gen, device=DEV).to(dtype)
+    vc = torch.randn_like(kc)
+
+    rope = RopeScale(head_dim)
+    inv_freq = reference_ops.rope_module_inv_freq(rope, DEV)
+    q_want = reference_ops.rope_reference(q, positions, inv_freq)
+    k_want = reference_ops.rope_reference(k, positions, inv_freq)
+    kc_want, vc_want = kc.clone(), vc.clone()
+    keep = slots >= 0
+    kc_want[layer].view(-1, kv_heads, head_dim)[slots[keep]] = k_want[keep]
+    vc_want[layer].view(-1, kv_heads, head_dim)[slots[keep]] = v[keep]
+
+    cos, sin = rope.tables(DEV, dtype, 29600)
+    k_before, v_before = k.clone(), v.clone()
+    _native.rope_kv_append(kc, vc, layer, q, k, v, positions, slots, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_want)
+    assert torch.equal(kc, kc_want) and torch.equal(vc, vc_want)
+    # k and v inputs are left as they were
+    assert torch.equal(k, k_before) and torch.equal(v, v_before)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_small_matches_oracle(dtype):
     _log(f"decode_small dtype={dtype}")
     wl = workloads.decode_small()
@@ -193,8 +235,50 @@ def test_decode_ignores_garbage_past_length():
     assert (got.float() - want.float()).abs().max().item() <= 2e-2
 
 
+def test_decode_tolerates_stale_workspace():
+    """The decode workspace needs no clearing: a workspace full of garbage
+    (random bytes, all ones, small integers), or one just overwritten by a
+    prefill call's partials, gives correct output."""
+    _log("decode stale workspace")
+    wl = workloads.decode_ragged(seed=5)
+    kc, vc = wl.pool(torch.bfloat16)
+    q, _, _ = wl.new_tokens(torch.bfloat16)
+    want = _decode_oracle(wl, kc, vc, q)
+    dk, dv, dq = kc.to(DEV), vc.to(DEV), q.to(DEV)
+    tables = torch.from_numpy(wl.table_array()).to(DEV)
+    lens = torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)
+
+    def run():
+        out = _native.paged_decode(dq, dk, dv, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens),
+                                   wl.head_dim**-0.5)
+        torch.cuda.synchronize()
+        return (out.cpu().float() - want.float()).abs().max().item()
+
+    run()  # creates the cached workspace
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    fills = {
+        "random": lambda w: w.copy_(torch.randint(0, 256, w.shape, generator=gen, device=DEV, dtype=torch.uint8)),
+        "ones": lambda w: w.fill_(255),
+        "small integers": lambda w: w[: w.numel() // 8 * 8].view(torch.int64).copy_(
+            torch.arange(w.numel() // 8, device=DEV, dtype=torch.int64) % 7 + 1),
+    }
+    for name, fill in fills.items():
+        for ws in _native._decode_workspaces.values():
+            fill(ws)
+        err = run()
+        _log(f"  {name}: max_abs_err={err:.3e}")
+        assert err <= 2e-2
+    # a split-key prefill writes its partials over the same workspace
+    pwl = workloads.ragged([3000, 40], [64, 1], seed=11)
+    _prefill_case(pwl, torch.bfloat16)
+    err = run()
+    _log(f"  after prefill: max_abs_err={err:.3e}")
+    assert err <= 2e-2
+
+
 def test_decode_workspace_reuse_across_calls():
-    """Back-to-back launches share one workspace: split counters must be left at zero.
+    """Back-to-back launches share one workspace: what a call leaves behind
+    must not disturb the next call.
 
     Calls alternate between a long-context batch (many splits per sequence)
     and a short one, with no host synchronisation between them; every output

@@ -44,12 +44,12 @@ def _log(msg):
 @contextlib.contextmanager
 def oracle_attention():
     """Run the model with the reference attention algorithm instead of the HIP kernels."""
-    saved = attention_module.paged_attention
-    attention_module.paged_attention = reference_ops.attention_core_like_product
+    saved = attention_module.attention_core
+    attention_module.attention_core = reference_ops.attention_core_like_product
     try:
         yield
     finally:
-        attention_module.paged_attention = saved
+        attention_module.attention_core = saved
 
 
 def _model(dtype=torch.float32, hidden=256, q_heads=4, kv_heads=2, layers=2, vocab=64, max_seq_len=64, seed=0):

@@ -323,3 +323,96 @@ def test_pins_catch_planted_mistakes(kind, monkeypatch):
         exact = closed_form.decode(q[b].numpy(), ks.numpy(), vs.numpy(), 64**-0.5)
         worst = max(worst, float(np.nan_to_num(np.abs(got.numpy() - exact), nan=1e9).max()))
     assert worst > 1e-3, f"closed-form pin did not notice mutant {kind}"
+
+
+# ---------------------------------------------------------------------------
+# RoPE (layers/rope.py of the reference): frequencies, rotation, tables
+# ---------------------------------------------------------------------------
+_LLAMA3 = {"factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+
+
+def _rope_float64(x: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor) -> np.ndarray:
+    """Rotation of the pairs (i, i + D/2) by the fp32 angle p*f_i, in float64 (independent of torch's sin/cos)."""
+    half = x.shape[-1] // 2
+    angle = (positions.to(torch.float32)[:, None] * inv_freq).double().numpy()[:, None, :]
+    xs = x.double().numpy()
+    x1, x2 = xs[..., :half], xs[..., half:]
+    return np.concatenate((x1 * np.cos(angle) - x2 * np.sin(angle), x2 * np.cos(angle) + x1 * np.sin(angle)), -1)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_rope_inv_freq_closed_forms(dim):
+    plain = reference_ops.rope_inv_freq(dim, 500000.0).double().numpy()
+    exact = np.array([500000.0 ** (-2 * i / dim) for i in range(dim // 2)])
+    assert plain[0] == 1.0 and np.allclose(plain, exact, rtol=2e-6, atol=0)
+    scaled = reference_ops.rope_inv_freq(dim, 500000.0, _LLAMA3).double().numpy()
+    bands = {"low": 0, "mid": 0, "high": 0}
+    for f, got in zip(exact, scaled):
+        wavelength = 2 * math.pi / f
+        if wavelength > 8192:  # long wavelengths slowed by the factor
+            want, band = f / 32.0, "low"
+        elif wavelength < 2048:  # short ones kept
+            want, band = f, "high"
+        else:  # linear blend in 1/wavelength between the two
+            smooth = (8192 / wavelength - 1.0) / 3.0
+            want, band = (1 - smooth) * f / 32.0 + smooth * f, "mid"
+        bands[band] += 1
+        assert got == pytest.approx(want, rel=5e-6)
+    assert all(bands.values()), bands  # every band is exercised
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_reference_matches_float64_rotation(dtype):
+    g = torch.Generator().manual_seed(21)
+    inv_freq = reference_ops.rope_inv_freq(64, 500000.0, _LLAMA3)
+    positions = torch.tensor([0, 1, 7, 500, 4095, 8192, 29599, 131071], dtype=torch.int64)
+    x = torch.randn((8, 3, 64), generator=g).to(dtype)
+    got = reference_ops.rope_reference(x, positions, inv_freq)
+    # position 0 is the identity, exactly
+    assert torch.equal(got[0], x[0])
+    tol = 1e-5 if dtype == torch.float32 else 6e-2
+    assert np.abs(got.double().numpy() - _rope_float64(x, positions, inv_freq)).max() <= tol
+    if dtype == torch.float32:  # rotations keep each pair's length
+        half = 32
+        n_in = x[..., :half] ** 2 + x[..., half:] ** 2
+        n_out = got[..., :half] ** 2 + got[..., half:] ** 2
+        assert torch.allclose(n_in, n_out, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("kind", ["sign", "interleaved", "no_scaling"])
+def test_rope_pin_catches_planted_mistakes(kind):
+    g = torch.Generator().manual_seed(22)
+    inv_freq = reference_ops.rope_inv_freq(64, 500000.0, _LLAMA3)
+    positions = torch.tensor([3, 100, 9000, 20000], dtype=torch.int64)
+    x = torch.randn((4, 2, 64), generator=g)
+    if kind == "no_scaling":
+        got = reference_ops.rope_reference(x, positions, reference_ops.rope_inv_freq(64, 500000.0))
+    else:
+        angles = positions.float()[:, None] * inv_freq
+        sin, cos = torch.sin(angles)[:, None], torch.cos(angles)[:, None]
+        if kind == "sign":
+            a, b = x[..., :32], x[..., 32:]
+            got = torch.cat((a * cos + b * sin, b * cos - a * sin), -1)
+        else:  # pairs (2i, 2i+1) instead of (i, i + D/2)
+            a, b = x[..., 0::2], x[..., 1::2]
+            got = torch.stack((a * cos - b * sin, b * cos + a * sin), -1).flatten(-2)
+    assert np.abs(got.double().numpy() - _rope_float64(x, positions, inv_freq)).max() > 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("scaled", [False, True])
+def test_product_rope_and_tables_match_oracle_bit_for_bit(dtype, scaled):
+    from nano_infer_engine.layers.rope import Rope, RopeScale
+
+    rope = RopeScale(64) if scaled else Rope(64)
+    inv_freq = reference_ops.rope_module_inv_freq(rope, torch.device("cpu"))
+    assert torch.equal(rope.inv_freq(torch.device("cpu")), inv_freq)
+    g = torch.Generator().manual_seed(23)
+    positions = torch.tensor([0, 5, 17, 4096, 9000, 12287], dtype=torch.int64)
+    x = torch.randn((6, 4, 64), generator=g).to(dtype)
+    assert torch.equal(rope.rotate_tokens(x, positions), reference_ops.rope_reference(x, positions, inv_freq))
+    cos, sin = rope.tables(torch.device("cpu"), dtype, 12288)
+    assert cos.shape == (12288, 32) and sin.shape == (12288, 32)
+    angles = positions.float()[:, None] * inv_freq
+    assert torch.equal(cos[positions], torch.cos(angles).to(dtype))
+    assert torch.equal(sin[positions], torch.sin(angles).to(dtype))
