@@ -342,8 +342,11 @@ def e2e_prompts(device, vocab, count=E2E_REQUESTS, seed=3):
     return [torch.from_numpy(rng.integers(0, vocab, size=(1, int(n)))).to(device) for n in lens]
 
 
-def e2e_run(model, prompts, device, max_new_tokens, max_steps=None):
-    """Serve every prompt through the continuous-batching scheduler; returns (seconds, steps, requests)."""
+def e2e_run(model, prompts, device, max_new_tokens, max_steps=None, graphs=True):
+    """Serve every prompt through the continuous-batching scheduler; returns (seconds, steps, requests).
+
+    With ``graphs`` the all-decode steps replay captured HIP graphs (captures
+    happen inside the timed region, as in a fresh server)."""
     import torch
 
     from nano_infer_engine.generation import ContinuousBatchingScheduler, GenerationConfig
@@ -355,7 +358,7 @@ def e2e_run(model, prompts, device, max_new_tokens, max_steps=None):
                          torch.bfloat16, device)
     gen = GenerationConfig(max_new_tokens=max_new_tokens, eos_token_id=None, prefill_chunk_size=128,
                            max_prefill_tokens_per_step=512)
-    sched = ContinuousBatchingScheduler(model, gen, cache, max_batch_size=16)
+    sched = ContinuousBatchingScheduler(model, gen, cache, max_batch_size=16, decode_graphs=graphs)
     reqs = [sched.add_request(f"request-{i}", p) for i, p in enumerate(prompts)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -383,6 +386,11 @@ def run_e2e(args):
     tok_s = out_tokens / secs
     log(f"e2e: {out_tokens} output tokens from {len(prompts)} requests in {secs:.2f} s "
         f"({steps} steps) -> {tok_s:.0f} tok/s")
+    eager_secs, _, eager_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, graphs=False)
+    eager_tok_s = sum(r.generated_tokens for r in eager_reqs) / eager_secs
+    same_modes = all(torch.equal(a.sequence, b.sequence) for a, b in zip(reqs, eager_reqs))
+    log(f"e2e eager (no decode graphs): {eager_secs:.2f} s -> {eager_tok_s:.0f} tok/s; "
+        f"tokens identical to the graph run: {same_modes}")
     # the reference attention algorithm (per-request gather / repeat_interleave /
     # matmul / mask / softmax) under the same scheduler, on the first steps only
     k = args.e2e_ref_steps
@@ -400,6 +408,8 @@ def run_e2e(args):
     torch.cuda.empty_cache()
     return {
         "output_tok_per_s": round(tok_s, 1),
+        "output_tok_per_s_eager": round(eager_tok_s, 1),
+        "eager_tokens_identical": same_modes,
         "output_tokens": out_tokens,
         "seconds": round(secs, 3),
         "scheduler_steps": steps,

@@ -148,6 +148,18 @@ int nie_rope_kv_append(int dtype,
                        void* stream);
 
 /*
+ * Greedy token selection: out[r] = index of the largest of the cols values
+ * of row r (element (r, c) at r * row_stride + c), ties to the lowest index,
+ * NaN larger than every number — torch.argmax's result.  out is int64.
+ * Replaces: torch.stack(request_logits).argmax(dim=-1) of the scheduler step
+ *           (src/nano_infer_engine/generation/scheduler.py:399-401), here
+ *           run on the logits rows as the step's last kernel so a captured
+ *           decode step ends with the next token IDs on the device.
+ */
+int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t cols, int64_t row_stride,
+                    int64_t* out, void* stream);
+
+/*
  * Workspace bytes needed by nie_paged_decode for a call with these
  * arguments (same meaning as there; host values), whose sequence lengths
  * have maximum max_seq_len and sum total_seq_len.  The split of the work

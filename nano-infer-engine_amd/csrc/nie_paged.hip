@@ -672,6 +672,88 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Greedy token selection: argmax of each logits row
+// ---------------------------------------------------------------------------
+// (value, index) pairs ordered like torch.argmax: a larger value wins, NaN
+// beats every number, and equal values (or two NaNs) go to the lower index.
+__device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int64_t bi) {
+  const bool vn = v != v;
+  const bool bn = bv != bv;
+  if (vn != bn) return vn;
+  if (!vn && v != bv) return v > bv;
+  return i < bi;
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+// One workgroup per row; each thread scans 16-byte vectors of the row
+// (a scalar tail covers rows whose length or start is not vector aligned),
+// then the workgroup reduces (value, index) through LDS.
+template <typename T>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const void* logits, int64_t row_stride,
+                                                                     int64_t cols, int64_t* out) {
+  constexpr int kPerVec = 16 / Elt<T>::kBytes;
+  const int64_t row = blockIdx.x;
+  const T* x = reinterpret_cast<const T*>(logits) + row * row_stride;
+  float best = kNegInf;
+  int64_t best_i = cols;  // past the end: loses every comparison with a real element
+  const bool vec = ((uintptr_t)x % 16) == 0;
+  const int64_t nvec = vec ? cols / kPerVec : 0;
+  for (int64_t j = threadIdx.x; j < nvec; j += kArgmaxThreads) {
+    const uint4 w = reinterpret_cast<const uint4*>(x)[j];
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < kPerVec; ++e) {
+      float v;
+      if constexpr (Elt<T>::kIsBf16) {
+        v = bf16_bits_to_f32((words[e / 2] >> (16 * (e % 2))) & 0xffffu);
+      } else {
+        v = __uint_as_float(words[e]);
+      }
+      const int64_t i = j * kPerVec + e;
+      if (argmax_better(v, i, best, best_i)) {
+        best = v;
+        best_i = i;
+      }
+    }
+  }
+  for (int64_t i = nvec * kPerVec + threadIdx.x; i < cols; i += kArgmaxThreads) {
+    const float v = load_elt<T>(x, i);
+    if (argmax_better(v, i, best, best_i)) {
+      best = v;
+      best_i = i;
+    }
+  }
+  // wave reduction, then one pair per wave through LDS
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v = __shfl_xor(best, off);
+    const int64_t i = __shfl_xor(best_i, off);
+    if (argmax_better(v, i, best, best_i)) {
+      best = v;
+      best_i = i;
+    }
+  }
+  __shared__ float s_val[kArgmaxThreads / kWave];
+  __shared__ int64_t s_idx[kArgmaxThreads / kWave];
+  const int wave = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    s_val[wave] = best;
+    s_idx[wave] = best_i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w) {
+      if (argmax_better(s_val[w], s_idx[w], best, best_i)) {
+        best = s_val[w];
+        best_i = s_idx[w];
+      }
+    }
+    out[row] = best_i;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Paged decode (split-K)
 // ---------------------------------------------------------------------------
 constexpr int kDecodeWaves = 8;  // KV heads handled by one workgroup (one per wave)
@@ -1945,6 +2027,24 @@ NIE_API int nie_rope_kv_append(int dtype, void* q, int64_t q_stride_t, int64_t q
     else hipLaunchKernelGGL((rope_kv_append_kernel<float, 128>), grid, dim3(256), 0, s, a);
   }
   return launched("rope_kv_append");
+}
+
+NIE_API int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t cols, int64_t row_stride,
+                            int64_t* out, void* stream) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  if (rows < 0 || cols <= 0 || row_stride < cols) return fail(NIE_EINVAL, "bad logits shape");
+  if (rows == 0) return NIE_OK;
+  if (!logits || !out) return fail(NIE_EINVAL, "null pointer argument");
+  if (rows > 0x7fffffffLL) return fail(NIE_EINVAL, "too many rows");
+  if (dtype == NIE_DTYPE_BF16) {
+    hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, dim3((unsigned)rows), dim3(kArgmaxThreads), 0,
+                       (hipStream_t)stream, logits, row_stride, cols, out);
+  } else {
+    hipLaunchKernelGGL(argmax_rows_kernel<float>, dim3((unsigned)rows), dim3(kArgmaxThreads), 0,
+                       (hipStream_t)stream, logits, row_stride, cols, out);
+  }
+  return launched("argmax_rows");
 }
 
 NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,

@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "nie_kv_gather",
     "nie_kv_copy_blocks",
     "nie_rope_kv_append",
+    "nie_argmax_rows",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_varlen_prefill_workspace_bytes",
@@ -72,6 +73,7 @@ _SIGNATURES = {
             _i64, _i64, _ptr,                # kv_heads, head_dim, stream
         ],
     ),
+    "nie_argmax_rows": (_i32, [_i32, _ptr, _i64, _i64, _i64, _ptr, _ptr]),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "nie_paged_decode": (
         _i32,
@@ -301,6 +303,23 @@ def rope_kv_append(
         _stream(k_cache.device),
     )
     _check(rc, "nie_rope_kv_append")
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Index of the largest value of each row of a 2D logits tensor (torch.argmax(dim=-1) semantics), int64."""
+    _require_gpu(logits)
+    if logits.ndim != 2 or logits.shape[1] == 0 or logits.stride(1) != 1:
+        raise ValueError("logits must be a 2D tensor with contiguous, non-empty rows")
+    rows = logits.shape[0]
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    elif out.dtype != torch.int64 or out.shape != (rows,) or not out.is_contiguous() or out.device != logits.device:
+        raise ValueError("out must be a contiguous int64 tensor with one entry per row")
+    rc = load_library().nie_argmax_rows(dtype_code(logits.dtype), logits.data_ptr(), rows, logits.shape[1],
+                                        logits.stride(0) if rows > 1 else logits.shape[1], out.data_ptr(),
+                                        _stream(logits.device))
+    _check(rc, "nie_argmax_rows")
+    return out
 
 
 def kv_gather(

@@ -1,0 +1,180 @@
+"""HIP-graph replay of the all-decode step (one new token per request).
+
+The reference runs every decode iteration eagerly from Python and lists
+graph capture of stable decode shapes as future work
+(``docs/development-roadmap.md:89``, ``:190``).  Here the whole step of a
+:class:`~nano_infer_engine.models.llama.Llama3_2` — embedding, every layer
+(projections, fused RoPE + KV append, paged decode attention, MLP), final
+norm, LM head and the greedy argmax — is captured once per (batch size,
+length bucket) and replayed:
+
+* the step's inputs live in static device buffers: token IDs, block tables
+  (width = bucket / block_size), context and sequence lengths, slot mapping
+  and positions; one host-to-device copy refreshes the metadata per step;
+* the decode launch inside the graph is planned for the bucket
+  (:func:`~nano_infer_engine.paged_batch.decode_plan_bound`), exactly as the
+  eager step plans it, so a replay computes the same values as the eager
+  step;
+* the graph ends with :func:`~nano_infer_engine._native.argmax_rows`, so the
+  next token IDs are on the device when the replay finishes.
+
+Steps that carry prefill chunks, batches larger than ``max_batch_size`` and
+sequences past ``max_graph_len`` run eagerly.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from nano_infer_engine import _native
+from nano_infer_engine.paged_batch import RaggedBatch, decode_plan_bound
+from nano_infer_engine.paged_cache import PagedKVCache
+
+
+@dataclass
+class _CapturedStep:
+    graph: torch.cuda.CUDAGraph
+    batch: RaggedBatch
+    ids: torch.Tensor  # (B,) int64 input token IDs
+    ints: torch.Tensor  # device: tables (B*W), context lens (B), sequence lens (B)
+    longs: torch.Tensor  # device: slots (B), positions (B), cu_seqlens (B + 1)
+    ints_host: torch.Tensor  # pinned staging of ``ints``
+    longs_host: torch.Tensor  # pinned staging of ``longs``
+    width: int
+    copied: torch.cuda.Event  # recorded after the staging copies of the last step
+    logits: torch.Tensor  # (B, vocab) output of the last replay
+    next_ids: torch.Tensor  # (B,) int64 argmax of ``logits``
+
+
+class DecodeGraphRunner:
+    """Captures and replays the decode step of ``model`` over ``cache``."""
+
+    def __init__(self, model, cache: PagedKVCache, max_batch_size: int, max_graph_len: int = 32768):
+        if cache.keys.device.type != "cuda":
+            raise RuntimeError("decode graphs need the cache on a ROCm GPU")
+        self.model = model
+        self.cache = cache
+        self.max_batch_size = max_batch_size
+        self.max_graph_len = max_graph_len
+        self.device = cache.keys.device
+        # captures run on a side stream of default priority
+        self._stream = torch.cuda.Stream(self.device)
+        self._steps: dict[tuple[int, int], _CapturedStep] = {}
+        self.captures = 0
+        self.replays = 0
+
+    def supports(self, batch_size: int, max_seq_len: int) -> bool:
+        return 0 < batch_size <= self.max_batch_size and decode_plan_bound(max_seq_len) <= self.max_graph_len
+
+    # ---------------------------------------------------------------- capture
+    def _capture(self, batch_size: int, bound: int) -> _CapturedStep:
+        cache, model = self.cache, self.model
+        b, width = batch_size, -(-bound // cache.block_size)
+        ints = torch.zeros(b * width + 2 * b, dtype=torch.int32, device=self.device)
+        longs = torch.zeros(3 * b + 1, dtype=torch.int64, device=self.device)
+        ids = torch.zeros(b, dtype=torch.int64, device=self.device)
+        # capture-time contents: every slot -1 (the K/V writes are skipped),
+        # length-1 sequences over block 0, position 0
+        ints[b * width :] = 1
+        ints[b * width : b * width + b] = 0
+        longs[:b] = -1
+        longs[2 * b :] = torch.arange(b + 1, device=self.device)
+        batch = RaggedBatch(
+            sequence_ids=tuple(f"graph-row-{i}" for i in range(b)),
+            query_lens=(1,) * b,
+            context_lens=(bound - 1,) * b,  # sizes the RoPE tables for the bucket
+            num_tokens=b,
+            block_tables=ints[: b * width].view(b, width),
+            context_lens_t=ints[b * width : b * width + b],
+            seq_lens_t=ints[b * width + b :],
+            cu_seqlens=longs[2 * b :],
+            slot_mapping=longs[:b],
+            positions=longs[b : 2 * b],
+            decode_from=0,
+            decode_bound=bound,
+        )
+        next_ids = torch.zeros(b, dtype=torch.int64, device=self.device)
+        stream = self._stream
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream), torch.inference_mode():
+            # eager warm-up on the capture stream: builds the launches (which
+            # remember this stream), their workspaces and the GEMM plans
+            logits = model.run_tokens(ids, cache, batch)
+            _native.argmax_rows(logits, out=next_ids)
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                logits = model.run_tokens(ids, cache, batch)
+                _native.argmax_rows(logits, out=next_ids)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        self.captures += 1
+        return _CapturedStep(
+            graph=graph,
+            batch=batch,
+            ids=ids,
+            ints=ints,
+            longs=longs,
+            ints_host=torch.empty(ints.shape, dtype=ints.dtype, pin_memory=True),
+            longs_host=torch.empty(longs.shape, dtype=longs.dtype, pin_memory=True),
+            width=width,
+            copied=torch.cuda.Event(),
+            logits=logits,
+            next_ids=next_ids,
+        )
+
+    # ------------------------------------------------------------------ step
+    @torch.inference_mode()
+    def step(self, token_ids: torch.Tensor, sequence_ids: tuple[str, ...]) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append one token per sequence and run the model: returns (logits (B, vocab), next IDs (B,)).
+
+        Both are views of static buffers, valid until the next call with the
+        same batch size and bucket.  Validation and cache bookkeeping follow
+        the eager path (``Llama3_2._forward_packed``).
+        """
+        cache, config = self.cache, self.model.config
+        b = len(sequence_ids)
+        if token_ids.numel() != b:
+            raise ValueError("one token per sequence is required")
+        context = [cache.get_sequence_length(s) for s in sequence_ids]
+        for s, ctx in zip(sequence_ids, context):
+            if ctx + 1 > config.max_seq_len:
+                raise ValueError(f"Sequence length {ctx + 1} exceeds max_seq_len={config.max_seq_len}")
+            cache.ensure_capacity(s, ctx + 1)
+        bound = decode_plan_bound(max(context) + 1)
+        if not self.supports(b, max(context) + 1):
+            raise ValueError("batch size or sequence length outside the captured range")
+        key = (b, bound)
+        step = self._steps.get(key)
+        if step is None:
+            step = self._capture(b, bound)
+            self._steps[key] = step
+
+        # host metadata into the pinned staging buffers (once the previous
+        # step's copies out of them have run), then one copy each
+        step.copied.synchronize()
+        bs, width = cache.block_size, step.width
+        ints = step.ints_host.numpy()
+        longs = step.longs_host.numpy()
+        tables = ints[: b * width].reshape(b, width)
+        tables[:] = 0
+        ctx = np.asarray(context, dtype=np.int64)
+        for r, s in enumerate(sequence_ids):
+            row = cache._table(s)[:width]
+            tables[r, : len(row)] = row
+        ints[b * width : b * width + b] = ctx
+        ints[b * width + b :] = ctx + 1
+        longs[:b] = tables[np.arange(b), ctx // bs].astype(np.int64) * bs + ctx % bs
+        longs[b : 2 * b] = ctx
+        longs[2 * b :] = np.arange(b + 1)
+        step.ints.copy_(step.ints_host, non_blocking=True)
+        step.longs.copy_(step.longs_host, non_blocking=True)
+        step.copied.record()
+        step.ids.copy_(token_ids.reshape(-1))
+        step.graph.replay()
+        self.replays += 1
+        for s in sequence_ids:
+            cache.advance(s, 1)
+        return step.logits, step.next_ids

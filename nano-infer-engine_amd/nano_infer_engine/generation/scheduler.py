@@ -9,6 +9,11 @@ every step is one flattened forward over ``[prefill chunks..., decode
 tokens...]`` (prefill first), chunks picked round-robin under the global
 ``max_prefill_tokens_per_step`` budget — this is what feeds the varlen
 paged-attention path.
+
+With ``decode_graphs=True`` (a keyword this build adds) a step that carries
+only decode tokens replays a captured HIP graph of the whole model step
+(:mod:`nano_infer_engine.generation.decode_graph`), which also leaves the
+next greedy tokens on the device; every other step runs eagerly.
 """
 
 from __future__ import annotations
@@ -39,6 +44,7 @@ class ContinuousBatchingScheduler:
         max_batch_size: int,
         *,
         release_on_token_limit: bool = True,
+        decode_graphs: bool = False,
     ) -> None:
         if not config.use_cache:
             raise ValueError("continuous batching requires config.use_cache=True")
@@ -59,6 +65,13 @@ class ContinuousBatchingScheduler:
         self.reserved_blocks = 0
         self._requests: dict[str, PagedRequest] = {}
         self._closed = False
+        self._graphs = None
+        if decode_graphs:
+            from nano_infer_engine.generation.decode_graph import DecodeGraphRunner
+
+            self._graphs = DecodeGraphRunner(model, paged_cache, max_batch_size)
+        # requests of the last graph step, in order, and its argmax (device)
+        self._graph_step: tuple[tuple[PagedRequest, ...], torch.Tensor] | None = None
 
     # ------------------------------------------------------------------ state
     @property
@@ -279,6 +292,16 @@ class ContinuousBatchingScheduler:
         return tuple(cancelled)
 
     # ------------------------------------------------------------------ steps
+    def _graph_argmax(self) -> torch.Tensor | None:
+        """The last graph step's argmax, if the active requests are exactly that step's, in order."""
+        if self._graph_step is None:
+            return None
+        requests, next_ids = self._graph_step
+        active = self.active_requests
+        if len(requests) != len(active) or any(a is not b for a, b in zip(requests, active)):
+            return None
+        return next_ids.clone().view(-1, 1)
+
     def _sample_active(self) -> tuple[torch.Tensor, list[int], tuple[TokenEvent, ...]]:
         """Greedy next token of every active request (one device->host sync)."""
         rows = []
@@ -287,7 +310,9 @@ class ContinuousBatchingScheduler:
                 raise RuntimeError("active request is missing logits")
             rows.append(request.last_logits)
         if rows:
-            next_tokens = torch.stack(rows).argmax(dim=-1, keepdim=True)
+            next_tokens = self._graph_argmax()
+            if next_tokens is None:
+                next_tokens = torch.stack(rows).argmax(dim=-1, keepdim=True)
             token_ids = next_tokens.squeeze(-1).tolist()
         else:
             next_tokens = torch.empty((0, 1), dtype=torch.long, device=self.paged_cache.keys.device)
@@ -338,14 +363,21 @@ class ContinuousBatchingScheduler:
 
         prefill_requests, prefill_chunks = self._take_prefill_chunks()
         ragged_requests = [*prefill_requests, *survivors]
+        self._detach_graph_logits(survivors)
         if ragged_requests:
             try:
-                logits = paged_prefill_chunks(
-                    self.model,
-                    (*prefill_chunks, *survivor_tokens),
-                    self.paged_cache,
-                    tuple(r.sequence_id for r in ragged_requests),
-                )
+                if self._use_graph(prefill_requests, survivors):
+                    logits, next_ids = self._graphs.step(
+                        torch.cat(survivor_tokens).view(-1), tuple(r.sequence_id for r in survivors)
+                    )
+                    self._graph_step = (tuple(survivors), next_ids)
+                else:
+                    logits = paged_prefill_chunks(
+                        self.model,
+                        (*prefill_chunks, *survivor_tokens),
+                        self.paged_cache,
+                        tuple(r.sequence_id for r in ragged_requests),
+                    )
             except Exception as error:
                 self._fail_all(ragged_requests, error, completed)
             else:
@@ -355,6 +387,27 @@ class ContinuousBatchingScheduler:
                     request.last_logits = row
         self.completed_requests.extend(completed)
         return SchedulerStepOutput(events, tuple(completed))
+
+    def _use_graph(self, prefill_requests: list[PagedRequest], survivors: list[PagedRequest]) -> bool:
+        self._graph_step = None
+        if self._graphs is None or prefill_requests or not survivors:
+            return False
+        longest = max(self.paged_cache.get_sequence_length(r.sequence_id) for r in survivors) + 1
+        return self._graphs.supports(len(survivors), longest)
+
+    def _detach_graph_logits(self, survivors: list[PagedRequest]) -> None:
+        """Copies the logits rows of requests that leave the graph batch.
+
+        A graph step's logits are views of a buffer the next replay
+        overwrites; requests still decoding get new rows, the others keep a
+        copy of their last one.
+        """
+        if self._graph_step is None:
+            return
+        staying = {id(r) for r in survivors}
+        for request in self._graph_step[0]:
+            if id(request) not in staying and request.last_logits is not None:
+                request.last_logits = request.last_logits.clone()
 
     @torch.inference_mode()
     def step(self) -> SchedulerStepOutput:

@@ -26,6 +26,19 @@ from nano_infer_engine import _native
 from nano_infer_engine.paged_cache import PagedKVCache
 
 
+#: Decode launches are planned for the longest sequence rounded up to this
+#: many tokens (and every decode row at that length), so one plan serves every
+#: step until a sequence crosses the next multiple: a captured decode step
+#: (``generation.decode_graph``) replays with the same plan, and gives the
+#: same results, as the eager step.
+DECODE_PLAN_BUCKET = 512
+
+
+def decode_plan_bound(max_seq_len: int) -> int:
+    """Sequence-length bound a decode launch is planned for."""
+    return -(-max_seq_len // DECODE_PLAN_BUCKET) * DECODE_PLAN_BUCKET
+
+
 @dataclass
 class RaggedBatch:
     sequence_ids: tuple[str, ...]
@@ -41,6 +54,7 @@ class RaggedBatch:
     positions: torch.Tensor  # (num_tokens,) int64
     # host-side launch geometry
     decode_from: int  # requests [decode_from, R) have one new token each (a contiguous tail)
+    decode_bound: int = 0  # length bound the decode launch is planned for (0: no decode rows)
     # prepared per-layer launches, built on first use (see ``launchers``)
     _launch: dict = field(default_factory=dict, repr=False, compare=False)
 
@@ -81,10 +95,10 @@ class RaggedBatch:
                 q_heads, scale,
             )
         if split < self.num_requests:
-            seq_lens = [c + 1 for c in self.context_lens[split:]]
+            rows = self.num_requests - split
             decode = _native.PreparedDecode(
-                cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], max(seq_lens),
-                sum(seq_lens), q_heads, scale,
+                cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], self.decode_bound,
+                rows * self.decode_bound, q_heads, scale,
             )
         found = (append, prefill, decode)
         self._launch[key] = found
@@ -109,9 +123,16 @@ def build_ragged_batch(
         # every new token must already be backed by a block (same error as a write)
         cache._resolve_position(sequence_id, ctx + q - 1)
     tables = [cache._table(s) for s in sequence_ids]
-    width = max(1, max(len(t) for t in tables))
     num_requests = len(sequence_ids)
     num_tokens = int(sum(query_lens))
+    decode_from = num_requests
+    while decode_from > 0 and query_lens[decode_from - 1] == 1:
+        decode_from -= 1
+    decode_bound = 0
+    if decode_from < num_requests:
+        decode_bound = decode_plan_bound(max(c + 1 for c in context_lens[decode_from:]))
+    # rows cover the decode plan's bound, as the decode launch requires
+    width = max(1, max(len(t) for t in tables), -(-decode_bound // bs))
 
     ints = np.zeros(num_requests * width + 2 * num_requests, dtype=np.int32)
     table_view = ints[: num_requests * width].reshape(num_requests, width)
@@ -135,10 +156,6 @@ def build_ragged_batch(
     ints_t = torch.from_numpy(ints).to(device, non_blocking=True)
     longs_t = torch.from_numpy(longs).to(device, non_blocking=True)
 
-    decode_from = num_requests
-    while decode_from > 0 and query_lens[decode_from - 1] == 1:
-        decode_from -= 1
-
     return RaggedBatch(
         sequence_ids=tuple(sequence_ids),
         query_lens=tuple(query_lens),
@@ -151,6 +168,7 @@ def build_ragged_batch(
         slot_mapping=longs_t[:num_tokens],
         positions=longs_t[num_tokens : 2 * num_tokens],
         decode_from=decode_from,
+        decode_bound=decode_bound,
     )
 
 

@@ -1,0 +1,121 @@
+"""On-device greedy argmax and HIP-graph replay of the decode step.
+
+* ``argmax_rows`` == ``torch.argmax(dim=-1)`` (ties to the lowest index,
+  NaN largest), bit for bit.
+* A replayed decode step (``DecodeGraphRunner``) computes exactly what the
+  eager step computes on an identical cache: same logits bits, same next
+  tokens, same cache contents — across replays with eager work and
+  synchronisations between them, a batch-size change and a crossing of the
+  decode plan's length bucket (both of which capture a new graph).
+* The scheduler produces the same tokens with and without decode graphs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nano_infer_engine import _native
+from nano_infer_engine.generation import ContinuousBatchingScheduler, GenerationConfig, paged_prefill, paged_prefill_chunks
+from nano_infer_engine.generation.decode_graph import DecodeGraphRunner
+from nano_infer_engine.models.llama import Llama3_2, LlamaConfig
+from nano_infer_engine.paged_cache import PagedKVCache
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_rows_matches_torch(dtype):
+    _log(f"argmax_rows {dtype}")
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    wide = torch.randn((9, 1031), generator=gen, device=DEV).to(dtype)
+    logits = wide[:, 1:1026]  # rows start off 16-byte alignment
+    logits[2, 17] = logits[2, 900] = 50.0  # a tie: the lower index wins
+    logits[3] = 1.0  # all equal: index 0
+    logits[4, 333] = float("nan")  # NaN is the largest
+    logits[5, 1024] = 60.0  # the last element
+    got = _native.argmax_rows(logits)
+    assert torch.equal(got, logits.argmax(dim=-1))
+    aligned = torch.randn((16, 128256), generator=gen, device=DEV).to(dtype)
+    assert torch.equal(_native.argmax_rows(aligned), aligned.argmax(dim=-1))
+
+
+def _graph_model(dtype):
+    torch.manual_seed(0)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, mlp_inner_size=512, num_layers=2, q_head_num=4,
+                      kv_head_num=2, rope_type="llama3", max_seq_len=2048, tie_word_embeddings=False)
+    return Llama3_2(cfg).eval().to(DEV, dtype)
+
+
+def _cache(model, num_blocks=256):
+    cfg = model.config
+    return PagedKVCache(num_blocks, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim, model.embed.weight.dtype, DEV)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_graph_replays_match_eager_step(dtype):
+    _log(f"decode graph vs eager {dtype}")
+    model = _graph_model(dtype)
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    # the first prompt crosses the 512-token plan bucket during the decode steps
+    prompts = [torch.randint(0, 512, (1, n), generator=gen, device=DEV) for n in (500, 37, 300)]
+    ids = ("a", "b", "c")
+    graph_cache, eager_cache = _cache(model), _cache(model)
+    with torch.inference_mode():
+        first = paged_prefill(model, tuple(prompts), graph_cache, ids)
+        assert torch.equal(first, paged_prefill(model, tuple(prompts), eager_cache, ids))
+    runner = DecodeGraphRunner(model, graph_cache, max_batch_size=4)
+    tokens = first.argmax(dim=-1)
+    active = list(ids)
+    for step in range(24):
+        if step == 14:  # one sequence leaves: a new batch size
+            active, tokens = active[:2], tokens[:2]
+        with torch.inference_mode():
+            g_logits, g_next = runner.step(tokens, tuple(active))
+            g_logits, g_next = g_logits.clone(), g_next.clone()
+            e_logits = paged_prefill_chunks(model, tuple(t.view(1, 1) for t in tokens), eager_cache, tuple(active))
+        if step % 5 == 0:
+            torch.cuda.synchronize()
+        assert torch.equal(g_logits, e_logits), f"step {step}: logits differ"
+        assert torch.equal(g_next, e_logits.argmax(dim=-1)), f"step {step}: next tokens differ"
+        tokens = g_next
+    for sid in ids:  # the sequences' cached tokens (unused pool slots hold whatever the allocation held)
+        n = graph_cache.get_sequence_length(sid)
+        assert n == eager_cache.get_sequence_length(sid)
+        assert graph_cache.get_block_table(sid) == eager_cache.get_block_table(sid)
+        for layer in range(model.config.num_layers):
+            gk, gv = graph_cache.gather(layer, sid, n)
+            ek, ev = eager_cache.gather(layer, sid, n)
+            assert torch.equal(gk, ek) and torch.equal(gv, ev)
+    assert graph_cache.get_sequence_length("a") > 512  # the bucket was crossed
+    assert runner.captures == 3 and runner.replays == 24
+    _log(f"  captures={runner.captures} replays={runner.replays}")
+
+
+def test_scheduler_tokens_identical_with_decode_graphs():
+    _log("scheduler with decode graphs")
+    model = _graph_model(torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(2)
+    prompts = [torch.randint(0, 512, (1, n), generator=gen, device=DEV) for n in (40, 7, 90, 33, 64, 21)]
+    runs = []
+    for graphs in (False, True):
+        cache = _cache(model)
+        config = GenerationConfig(max_new_tokens=24, eos_token_id=None, prefill_chunk_size=16,
+                                  max_prefill_tokens_per_step=32)
+        sched = ContinuousBatchingScheduler(model, config, cache, max_batch_size=4, decode_graphs=graphs)
+        reqs = [sched.add_request(f"r{i}", p) for i, p in enumerate(prompts)]
+        sched.run_until_idle()
+        runs.append([r.sequence.clone() for r in reqs])
+        if graphs:
+            assert sched._graphs.replays > 0
+            _log(f"  graph captures={sched._graphs.captures} replays={sched._graphs.replays}")
+            # completed requests keep their own last logits
+            assert all(r.last_logits is not None for r in reqs)
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
