@@ -811,9 +811,10 @@ __device__ __forceinline__ void lds_dma16(const void* src, unsigned char* dst) {
 // LDS DMA (global_load_lds_dwordx4), 64 lanes x 16 bytes = 1 KiB of
 // consecutive bytes per op, spread round-robin over the waves, so every op
 // is a fully contiguous read — the access pattern of a streaming copy.
-// Chunk c of row r is stored at chunk position c ^ (r & 15): both the MFMA
-// K reads (16 lanes read one chunk of 16 different rows) and the V^T reads
-// (four lane groups read rows 4g+e) then hit distinct LDS banks.
+// Chunk c of row r is stored at chunk position c ^ (r & 15): the MFMA K
+// reads (16 lanes read one chunk of 16 different rows) hit distinct LDS
+// banks, and the transposing V^T reads (16 rows x two adjacent chunks) spread
+// over all 16 bank groups, two chunks each.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int kHeads>
 struct GroupTile {
@@ -833,6 +834,11 @@ struct GroupTile {
   __device__ static __forceinline__ int elt_offset(int r, int hl, int d) {
     const int byte = (hl * D + d) * Elt<T>::kBytes;
     return chunk_offset(r, byte >> 4) + (byte & 15);
+  }
+  // This lane's transposing-read address (relative to the V tile) for the
+  // V^T operand of dims 16c..16c+15 of head hl (see ring_read_vt4).
+  __device__ static __forceinline__ int vt_offset(int lane, int hl, int c) {
+    return elt_offset(4 * (lane >> 4) + ((lane >> 2) & 3), hl, 16 * c + 4 * (lane & 3));
   }
 };
 
@@ -867,20 +873,21 @@ __device__ __forceinline__ void ring_read_k(uint4 (&out)[kVec], const uint32_t (
   for (int j = 0; j < kVec; ++j) out[j] = uint4{r[j][0], r[j][1], r[j][2], r[j][3]};
 }
 
-// Sixteen bf16 V^T values (four MFMA A operands) at precomputed addresses.
-__device__ __forceinline__ void ring_read_vt16(v4s (&a)[4], const uint32_t (&addr)[16]) {
-  uint32_t r[16];
+// Four bf16 V^T MFMA A operands (16 dims x 16 keys each), one transposing
+// LDS read each (ds_read_b64_tr_b16).  Within each group of 16 lanes the
+// read transposes a 4 x 16 block: lane 16a + 4e + c supplies the address of
+// four consecutive dims 4c..4c+3 of key 4a + e, and lane 16a + m receives
+// dim m of keys 4a..4a+3 — the A layout of v_mfma_f32_16x16x16_bf16 for
+// V^T (row = dim, k = key).  vt_offset() gives those per-lane addresses.
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void ring_read_vt4(v4s (&a)[4], const uint32_t (&addr)[4]) {
+  v2u r[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) asm volatile("ds_read_u16 %0, %1" : "=v"(r[i]) : "v"(addr[i]));
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
-                 "+v"(r[7]), "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]),
-                 "+v"(r[13]), "+v"(r[14]), "+v"(r[15]));
+  for (int i = 0; i < 4; ++i) asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r[i]) : "v"(addr[i]));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) a[c][e] = (short)r[4 * c + e];
-  }
+  for (int c = 0; c < 4; ++c) a[c] = __builtin_bit_cast(v4s, r[c]);
 }
 
 // Merges nsplit split partials of one output row, one wave.  Split s of the
@@ -1050,9 +1057,11 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   for (int j = 0; j < F::kVec; ++j) {
     koff[j] = GT::chunk_offset(row, (wave * D * Elt<T>::kBytes + 64 * j + 16 * g) >> 4);
   }
-  uint32_t voff[(D / 16) * 4];
+  uint32_t voff[(D / 16) * 4];  // fp32: V^T elements read one by one
+  uint32_t vtr[D / 16];         // bf16: transposing reads
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
+    vtr[c] = GT::kBytes + GT::vt_offset(lane, wave, c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, wave, 16 * c + row);
   }
@@ -1083,11 +1092,11 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
       const uint32_t base = lds_off(stage);
 #pragma unroll
       for (int c0 = 0; c0 < D / 16; c0 += 4) {
-        uint32_t va[16];
+        uint32_t va[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) va[i] = base + voff[4 * c0 + i];
+        for (int i = 0; i < 4; ++i) va[i] = base + vtr[c0 + i];
         v4s vt[4];
-        ring_read_vt16(vt, va);
+        ring_read_vt4(vt, va);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           st.o[c0 + c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[c], pb, st.o[c0 + c], 0, 0, 0);
@@ -1387,9 +1396,11 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
   uint32_t koff[F::kVec];
 #pragma unroll
   for (int j = 0; j < F::kVec; ++j) koff[j] = GT::chunk_offset(row, (64 * j + 16 * g) >> 4);
-  uint32_t voff[(D / 16) * 4];
+  uint32_t voff[(D / 16) * 4];  // fp32: V^T elements read one by one
+  uint32_t vtr[D / 16];         // bf16: transposing reads
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
+    vtr[c] = GT::kBytes + GT::vt_offset(lane, 0, c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, 0, 16 * c + row);
   }
@@ -1424,11 +1435,11 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
       for (int nb = 0; nb < kRowBlocks; ++nb) pb[nb] = pack_bf16x4(p[nb][0], p[nb][1], p[nb][2], p[nb][3]);
 #pragma unroll
       for (int c0 = 0; c0 < D / 16; c0 += 4) {
-        uint32_t va[16];
+        uint32_t va[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) va[i] = sb + voff[4 * c0 + i];
+        for (int i = 0; i < 4; ++i) va[i] = sb + vtr[c0 + i];
         v4s vt[4];
-        ring_read_vt16(vt, va);
+        ring_read_vt4(vt, va);
 #pragma unroll
         for (int nb = 0; nb < kRowBlocks; ++nb) {
 #pragma unroll
@@ -1495,11 +1506,11 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
       const uint32_t sb = lds_off(stage);
 #pragma unroll
       for (int c0 = 0; c0 < D / 16; c0 += 4) {
-        uint32_t va[16];
+        uint32_t va[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) va[i] = sb + voff[4 * c0 + i];
+        for (int i = 0; i < 4; ++i) va[i] = sb + vtr[c0 + i];
         v4s vt[4];
-        ring_read_vt16(vt, va);
+        ring_read_vt4(vt, va);
 #pragma unroll
         for (int nb = 0; nb < kRowBlocks; ++nb) {
           if (!live[nb]) continue;
