@@ -270,7 +270,8 @@ def run_mixed(args):
     dec_lens = torch.tensor(seq_lens[n_pref:], dtype=torch.int32, device=device)
     scale = wl.head_dim ** -0.5
     prefill = _native.PreparedPrefill(kc, vc, cu, ctx, tables[:n_pref].contiguous(), pref_tokens,
-                                      max(wl.query_lens[:n_pref]), max(seq_lens[:n_pref]), wl.q_heads, scale)
+                                      max(wl.query_lens[:n_pref]), max(seq_lens[:n_pref]), wl.q_heads, scale,
+                                      cu_seqlens_host=cu.cpu().tolist(), context_lens_host=wl.context_lens[:n_pref])
     decode = _native.PreparedDecode(kc, vc, tables[n_pref:].contiguous(), dec_lens, max(seq_lens[n_pref:]),
                                     sum(seq_lens[n_pref:]), wl.q_heads, scale)
     out = torch.empty_like(q)

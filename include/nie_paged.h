@@ -212,12 +212,17 @@ int nie_paged_decode(int dtype,
 
 /*
  * Workspace bytes needed by nie_varlen_prefill (host values: number of
- * sequences, total and maximum query length, maximum context+query length).
+ * sequences, total and maximum query length, maximum context+query length,
+ * and the same optional host copies of cu_seqlens_q / context_lens as the
+ * call, which change the launch plan).  Returns 0 when no workspace is
+ * needed or the arguments are invalid.
  */
 int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query_tokens,
                                            int64_t max_query_len, int64_t max_seq_len,
                                            int64_t q_heads, int64_t kv_heads,
-                                           int64_t head_dim);
+                                           int64_t head_dim,
+                                           const int64_t* host_cu_seqlens,
+                                           const int32_t* host_context_lens);
 
 /*
  * Varlen (chunked-prefill) attention over the paged cache.  Sequence r owns
@@ -231,6 +236,15 @@ int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query
  *   context_lens : (num_seqs,) int32.
  *   total_query_tokens, max_query_len, max_seq_len: host values sizing the
  *         launch; they must be exact (max_seq_len = max of context + query).
+ *   host_cu_seqlens / host_context_lens: optional (both or neither) HOST
+ *         copies of cu_seqlens_q / context_lens.  With them the launch is
+ *         planned from the exact work: key splits sized so the work fills
+ *         the GPU about once, and a grid of exactly the work items.  Without
+ *         them the plan uses upper bounds from the sizes above.  They must
+ *         hold the same values as the device arrays; NIE_EINVAL if they do
+ *         not fit the sizes.
+ * Query tiles whose keys are split over several workgroups are merged
+ * exactly (log-sum-exp weights) by a second kernel on the same stream.
  * Numerics as nie_paged_decode.
  * Replaces: the per-request write/gather/repeat_interleave/matmul/mask/
  *           softmax/matmul loop of GroupedQueryAttention.forward_ragged
@@ -251,6 +265,7 @@ int nie_varlen_prefill(int dtype,
                        float scale,
                        void* out, int64_t out_stride_t, int64_t out_stride_h,
                        void* workspace, int64_t workspace_bytes,
+                       const int64_t* host_cu_seqlens, const int32_t* host_context_lens,
                        void* stream);
 
 #ifdef __cplusplus

@@ -29,6 +29,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -69,6 +70,7 @@ __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 
 // ---------------------------------------------------------------------------
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 constexpr int kTileKeys = 16;      // keys per attention tile (one MFMA M/N edge)
@@ -857,7 +859,7 @@ __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// K slice (MFMA A layout, kVec 16-byte chunks) at precomputed LDS addresses.
+// kVec 16-byte K chunks (MFMA A layout) at precomputed LDS addresses.
 template <int kVec>
 __device__ __forceinline__ void ring_read_k(uint4 (&out)[kVec], const uint32_t (&addr)[kVec]) {
   v4u r[kVec];
@@ -865,9 +867,12 @@ __device__ __forceinline__ void ring_read_k(uint4 (&out)[kVec], const uint32_t (
   for (int j = 0; j < kVec; ++j) asm volatile("ds_read_b128 %0, %1" : "=v"(r[j]) : "v"(addr[j]));
   if constexpr (kVec == 2) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]));
-  } else {
-    static_assert(kVec == 4, "bf16 slices are 2 or 4 chunks");
+  } else if constexpr (kVec == 4) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+  } else {
+    static_assert(kVec == 8, "2, 4 or 8 chunks");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
   }
 #pragma unroll
   for (int j = 0; j < kVec; ++j) out[j] = uint4{r[j][0], r[j][1], r[j][2], r[j][3]};
@@ -1235,7 +1240,7 @@ int64_t decode_max_items(int64_t batch, int64_t total_seq_len, int64_t tps) {
 // Varlen prefill
 // ---------------------------------------------------------------------------
 constexpr int kPrefillWaves = 4;
-constexpr int kPrefillLdsBudget = 64 * 1024;
+constexpr int kPrefillLdsBudget = 128 * 1024;
 
 // Query rows per wave: kRowBlocks MFMA row blocks of 16 rows, each block
 // = 16/G consecutive tokens x the G query heads of the workgroup's KV head.
@@ -1282,29 +1287,139 @@ __device__ __forceinline__ int64_t prefill_items_of(const PrefillArgs& a, int64_
   return n;
 }
 
+// Key steps of kPrefillStepTiles 16-key tiles (64 keys) stream through an LDS
+// ring of prefill_stages() steps.
+constexpr int kPrefillStepTiles = 4;
+
 template <typename T, int D>
-constexpr int prefill_stages() {
-  constexpr int stage = 2 * GroupTile<T, D, 1>::kBytes;
-  return kPrefillLdsBudget / stage >= 8 ? 8 : (kPrefillLdsBudget / stage >= 2 ? kPrefillLdsBudget / stage : 2);
+constexpr int prefill_stage_bytes() {
+  return kPrefillStepTiles * 2 * GroupTile<T, D, 1>::kBytes;
 }
 
-// One workgroup = one (request, query tile, key split) for one KV head.  The
-// head's K and V rows of each 16-key tile stream through an LDS ring by LDS
-// DMA (as in decode; the K and V DMA ops of a tile are spread evenly over
-// the waves); every wave reads the whole tile and applies it to its
-// kRowBlocks row blocks.  A row block whose tokens all precede the tile skips
-// it (causal mask).  With one split the rows are written out; with several,
-// the split's unnormalised partial goes to the workspace for
+template <typename T, int D>
+constexpr int prefill_stages() {
+  constexpr int fit = kPrefillLdsBudget / prefill_stage_bytes<T, D>();
+  return fit >= 4 ? 4 : (fit >= 2 ? fit : 2);
+}
+
+// Two 4-element bf16 operands (sub-tile a's keys, then sub-tile b's) as one
+// 8-element 16x16x32 operand.  With it, K slot 8(l/16) + e of an MFMA is key
+// 4(l/16) + e of sub-tile a for e < 4 and key 4(l/16) + e - 4 of sub-tile b
+// otherwise, the same on the V^T and the P^T side.
+__device__ __forceinline__ bf16x8_t join_bf16x4(v4s a, v4s b) {
+  const u32x2_t lo = __builtin_bit_cast(u32x2_t, a);
+  const u32x2_t hi = __builtin_bit_cast(u32x2_t, b);
+  return __builtin_bit_cast(bf16x8_t, v4u{lo[0], lo[1], hi[0], hi[1]});
+}
+
+// Online softmax over one key step: s[nb][t] holds the scores of sub-tile t
+// for row block nb (-inf where masked); the probabilities are
+// exp2((s - m) * c) with m the running maximum of s and c = log2(e) times
+// the factor still to be applied to s (1, or the power-of-two softmax
+// scale when it has been kept out of s).  s is overwritten with them.  The
+// maximum over the step's keys needs one cross-lane reduction per row
+// block; the rescale of O is skipped (exactly: alpha would be 1) unless
+// some row's maximum moved.
+template <int D, int kBlocks, int kSub>
+__device__ __forceinline__ void softmax_step(SoftmaxState<D> (&st)[kBlocks], v4f (&s)[kBlocks][kSub], float c) {
+  float m_new[kBlocks], nref[kBlocks], tsum[kBlocks];
+  bool moved = false;
+#pragma unroll
+  for (int nb = 0; nb < kBlocks; ++nb) {
+    float tm[kSub];
+#pragma unroll
+    for (int t = 0; t < kSub; ++t) tm[t] = fmaxf(fmaxf(s[nb][t][0], s[nb][t][1]), fmaxf(s[nb][t][2], s[nb][t][3]));
+#pragma unroll
+    for (int w = 1; w < kSub; w <<= 1) {
+#pragma unroll
+      for (int t = 0; t + w < kSub; t += 2 * w) tm[t] = fmaxf(tm[t], tm[t + w]);
+    }
+    const float tmax = max_over_groups(tm[0]);
+    m_new[nb] = fmaxf(st[nb].m, tmax);
+    // A row with nothing unmasked so far keeps m = -inf; 0 as the reference
+    // point makes its exponentials exact zeros, not NaN.
+    nref[nb] = (m_new[nb] == kNegInf) ? 0.f : -m_new[nb] * c;
+    float ps[kSub];
+#pragma unroll
+    for (int t = 0; t < kSub; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[nb][t][i] = fast_exp2(fmaf(s[nb][t][i], c, nref[nb]));
+      ps[t] = (s[nb][t][0] + s[nb][t][1]) + (s[nb][t][2] + s[nb][t][3]);
+    }
+#pragma unroll
+    for (int w = 1; w < kSub; w <<= 1) {
+#pragma unroll
+      for (int t = 0; t + w < kSub; t += 2 * w) ps[t] += ps[t + w];
+    }
+    tsum[nb] = ps[0];
+    moved |= m_new[nb] != st[nb].m;
+  }
+  if (__ballot(moved)) {
+#pragma unroll
+    for (int nb = 0; nb < kBlocks; ++nb) {
+      const float alpha = fast_exp2(fmaf(st[nb].m, c, nref[nb]));
+      st[nb].lsum = st[nb].lsum * alpha + tsum[nb];
+#pragma unroll
+      for (int d = 0; d < D / 16; ++d) st[nb].o[d] *= alpha;
+    }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < kBlocks; ++nb) st[nb].lsum += tsum[nb];
+  }
+#pragma unroll
+  for (int nb = 0; nb < kBlocks; ++nb) st[nb].m = m_new[nb];
+}
+
+// LDS reads of the ring whose results are waited for together (see
+// ring_read_k): issue, then one lgkmcnt(0) wait that all results pass
+// through.
+template <int N>
+__device__ __forceinline__ void ring_read_b128_n(v4u (&r)[N], const uint32_t (&addr)[N]) {
+  static_assert(N % 4 == 0, "groups of four");
+#pragma unroll
+  for (int j = 0; j < N; ++j) asm volatile("ds_read_b128 %0, %1" : "=v"(r[j]) : "v"(addr[j]));
+#pragma unroll
+  for (int j = 0; j < N; j += 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[j]), "+v"(r[j + 1]), "+v"(r[j + 2]), "+v"(r[j + 3]));
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void ring_read_tr_n(v2u (&r)[N], const uint32_t (&addr)[N]) {
+  static_assert(N % 4 == 0, "groups of four");
+#pragma unroll
+  for (int j = 0; j < N; ++j) asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r[j]) : "v"(addr[j]));
+#pragma unroll
+  for (int j = 0; j < N; j += 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[j]), "+v"(r[j + 1]), "+v"(r[j + 2]), "+v"(r[j + 3]));
+  }
+}
+
+// One workgroup = one (request, query tile, key split) for one KV head.
+// Wave w owns kRowBlocks MFMA row blocks of 16 query rows (16/G consecutive
+// tokens x the G query heads of the KV head each).  The head's K and V rows
+// stream through an LDS ring in steps of 64 keys (four 16-key tiles), fetched
+// by LDS DMA (as in decode) with the step's DMA ops spread evenly over the
+// waves; every wave applies each step to all of its row blocks: four QK tiles
+// per row block, one softmax over the step, and P.V in 16x16x32 MFMAs that
+// each cover two 16-key tiles (bf16).  Row blocks whose tokens all precede
+// the step skip it (causal mask).  With one split the rows are written out;
+// with several, the split's unnormalised partial goes to the workspace for
 // prefill_merge_kernel.
-template <typename T, int D, bool kUniform, int kRowBlocks>
-__global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(PrefillArgs a) {
+// kPow2Scale: the softmax scale is a power of two, so rounding the scaled
+// score to bf16 is exact and the scale can be kept out of the scores and
+// applied inside the exponential (bf16 only).
+template <typename T, int D, bool kUniform, int kRowBlocks, bool kPow2Scale>
+__global__ __launch_bounds__(kPrefillWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
+void varlen_prefill_kernel(PrefillArgs a) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, 1>;
+  constexpr int kSub = kPrefillStepTiles;
   constexpr int kStages = prefill_stages<T, D>();
-  constexpr int kStageBytes = 2 * GT::kBytes;
-  constexpr int kTileOps = 2 * GT::kOps;  // K then V DMA ops of one tile
-  static_assert(kTileOps % kPrefillWaves == 0, "tile DMA ops must spread evenly over the waves");
-  constexpr int kOwnOps = kTileOps / kPrefillWaves;
+  constexpr int kStageBytes = prefill_stage_bytes<T, D>();
+  constexpr int kStepOps = kSub * 2 * GT::kOps;  // DMA ops of one step: per tile, K ops then V ops
+  static_assert(kStepOps % kPrefillWaves == 0, "step DMA ops must spread evenly over the waves");
+  constexpr int kOwnOps = kStepOps / kPrefillWaves;
   constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
   constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
   __shared__ __attribute__((aligned(16))) unsigned char ring[kStages][kStageBytes];
@@ -1342,6 +1457,7 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
   const int tile_begin = split * S;
   const int tile_end = min(tile_begin + S, (key_end + kTileKeys - 1) / kTileKeys);
   const int last = min(tile_end * kTileKeys, key_end) - 1;  // last key this item reads
+  const int last_key0 = (last / kTileKeys) * kTileKeys;     // first key of the tile holding it
   const int32_t* table = a.tables + r * a.table_stride;
   const int tlen = (int)a.table_stride;
   const T* kc = reinterpret_cast<const T*>(a.k_cache) + h * D;
@@ -1365,8 +1481,8 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
     }
     st[nb].init();
   }
-  // first and last position of each row block (wave-uniform): tiles past
-  // the last are fully masked, tiles up to the first fully visible
+  // first and last position of each row block (wave-uniform): steps past
+  // the last are fully masked, steps up to the first fully visible
   int block_first[kRowBlocks], block_last[kRowBlocks];
 #pragma unroll
   for (int nb = 0; nb < kRowBlocks; ++nb) {
@@ -1377,22 +1493,30 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
   TableCache tc;
   if constexpr (kUniform) tc.load(table, tlen, (tile_begin * kTileKeys) >> a.geom.bs_shift);
 
+  // This wave's DMA ops of the step starting at key0: op = wave + i*kWaves,
+  // tile t = op / (2*kOps), then K ops and V ops of that tile.  Tiles past
+  // the item's last key are redirected to the tile that holds it, and rows
+  // past it to it (no lane reads a slot the sequence does not own; those
+  // keys are masked to p = 0).
   auto issue = [&](int slot, int key0) {
-    TileAddr<kUniform, false> ta;  // an item covers <= 64 tiles, so <= 64 blocks
-    ta.init(a.geom, table, tlen, tc, key0);
-    const int lim = last - key0;
     unsigned char* base = &ring[slot][0];
 #pragma unroll
     for (int i = 0; i < kOwnOps; ++i) {
-      const int op = wave + i * kPrefillWaves;  // 0 .. kTileOps-1: K ops, then V ops
-      const int kop = op % GT::kOps;
+      const int op = wave + i * kPrefillWaves;
+      const int t = op / (2 * GT::kOps);
+      const int within = op % (2 * GT::kOps);
+      const int kop = within % GT::kOps;
+      const int tkey0 = min(key0 + t * kTileKeys, last_key0);
+      TileAddr<kUniform, false> ta;  // an item covers <= 64 tiles, so <= 64 blocks
+      ta.init(a.geom, table, tlen, tc, tkey0);
       const int rr = kop * GT::kRowsPerOp + lane / GT::kChunks;
       const int chunk = (lane % GT::kChunks) ^ GT::swz(rr);
-      const int64_t src = ta.at(a.geom, table, tlen, key0, min(rr, lim)) + chunk * kEltPerChunk;
-      lds_dma16((op < GT::kOps ? kc : vc) + src, base + op * kWave * 16);
+      const int64_t src = ta.at(a.geom, table, tlen, tkey0, min(rr, last - tkey0)) + chunk * kEltPerChunk;
+      lds_dma16((within < GT::kOps ? kc : vc) + src, base + op * kWave * 16);
     }
   };
 
+  // Per-lane LDS offsets inside one 16-key tile (K at 0, V at GT::kBytes).
   uint32_t koff[F::kVec];
 #pragma unroll
   for (int j = 0; j < F::kVec; ++j) koff[j] = GT::chunk_offset(row, (64 * j + 16 * g) >> 4);
@@ -1404,160 +1528,153 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
 #pragma unroll
     for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, 0, 16 * c + row);
   }
+  constexpr int kTileStride = 2 * GT::kBytes;  // K tile + V tile
 
-  // Tiles every row of every block sees in full (below the first block's
-  // first position and the item's end): no masks, no per-block branches.
-  auto consume_full = [&](int slot) {
-    const unsigned char* stage = &ring[slot][0];
-    F kf;
-    if constexpr (Elt<T>::kIsBf16) {
-      const uint32_t sb = lds_off(stage);
-      uint32_t ka[F::kVec];
-#pragma unroll
-      for (int j = 0; j < F::kVec; ++j) ka[j] = sb + koff[j];
-      ring_read_k<F::kVec>(kf.v, ka);
-    } else {
-#pragma unroll
-      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
-    }
-    v4f p[kRowBlocks];
-#pragma unroll
-    for (int nb = 0; nb < kRowBlocks; ++nb) {
-      p[nb] = qk_mfma<T, D>(kf, qf[nb]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[nb][i] = scaled_score<T>(p[nb][i], a.scale);
-    }
-    softmax_tiles<D, kRowBlocks>(st, p);
-    if constexpr (Elt<T>::kIsBf16) {
-      const uint32_t sb = lds_off(stage);
-      v4s pb[kRowBlocks];
-#pragma unroll
-      for (int nb = 0; nb < kRowBlocks; ++nb) pb[nb] = pack_bf16x4(p[nb][0], p[nb][1], p[nb][2], p[nb][3]);
-#pragma unroll
-      for (int c0 = 0; c0 < D / 16; c0 += 4) {
-        uint32_t va[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) va[i] = sb + vtr[c0 + i];
-        v4s vt[4];
-        ring_read_vt4(vt, va);
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            st[nb].o[c0 + c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[c], pb[nb], st[nb].o[c0 + c], 0, 0, 0);
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        float vv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) vv[j] = *reinterpret_cast<const float*>(stage + voff[4 * c + j]);
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], p[nb][j], st[nb].o[c], 0, 0, 0);
-          }
-        }
-      }
-    }
-  };
+  // exp2 multiplier of the scores (see softmax_step)
+  const float exp_c = kPow2Scale ? a.scale * kLog2e : kLog2e;
 
   auto consume = [&](int slot, int key0) {
-    if (key0 + kTileKeys - 1 <= min(block_first[0], last)) {
-      consume_full(slot);
-      return;
-    }
     const unsigned char* stage = &ring[slot][0];
-    F kf;
+    // every key of the step is visible to every row of this wave
+    const bool full = key0 + kSub * kTileKeys - 1 <= min(block_first[0], last);
+    v4f p[kRowBlocks][kSub];
     if constexpr (Elt<T>::kIsBf16) {
       const uint32_t sb = lds_off(stage);
-      uint32_t ka[F::kVec];
+      // K slices of the step's tiles, one wait
+      constexpr int kK = kSub * F::kVec;
+      uint32_t ka[kK];
+      v4u kr[kK];
 #pragma unroll
-      for (int j = 0; j < F::kVec; ++j) ka[j] = sb + koff[j];
-      ring_read_k<F::kVec>(kf.v, ka);
+      for (int t = 0; t < kSub; ++t) {
+#pragma unroll
+        for (int j = 0; j < F::kVec; ++j) ka[t * F::kVec + j] = sb + t * kTileStride + koff[j];
+      }
+      ring_read_b128_n<kK>(kr, ka);
+#pragma unroll
+      for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+        for (int t = 0; t < kSub; ++t) {
+          v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < F::kVec; ++j) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[t * F::kVec + j]),
+                                                          __builtin_bit_cast(bf16x8_t, qf[nb].v[j]), acc, 0, 0, 0);
+          }
+          p[nb][t] = acc;
+        }
+      }
     } else {
+      F kf[kSub];
 #pragma unroll
-      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
+      for (int t = 0; t < kSub; ++t) {
+#pragma unroll
+        for (int j = 0; j < F::kVec; ++j) {
+          kf[t].v[j] = *reinterpret_cast<const uint4*>(stage + t * kTileStride + koff[j]);
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+        for (int t = 0; t < kSub; ++t) p[nb][t] = qk_mfma<T, D>(kf[t], qf[nb]);
+      }
     }
-    bool live[kRowBlocks];
-    v4f p[kRowBlocks];
+    __builtin_amdgcn_sched_barrier(0);
+    // V^T operands of the step (bf16), read while the QK MFMAs run: tile t,
+    // dims 16c.. -> vt[t * D/16 + c]
+    constexpr int kVt = Elt<T>::kIsBf16 ? kSub * (D / 16) : 4;
+    v2u vt[kVt];
+    if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t sb = lds_off(stage);
+      uint32_t va[kVt];
+#pragma unroll
+      for (int t = 0; t < kSub; ++t) {
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) va[t * (D / 16) + c] = sb + t * kTileStride + vtr[c];
+      }
+      ring_read_tr_n<kVt>(vt, va);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // scores in the reference's rounding: the q.k sum rounded to the storage
+    // dtype, times the scale, rounded again (the second rounding is exact,
+    // and the scale moves into exp_c, when the scale is a power of two)
 #pragma unroll
     for (int nb = 0; nb < kRowBlocks; ++nb) {
-      live[nb] = key0 <= block_last[nb];
-      if (live[nb]) {
-        v4f sc = qk_mfma<T, D>(kf, qf[nb]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = scaled_score<T>(sc[i], a.scale);
-        if (key0 + kTileKeys - 1 > min(block_first[nb], last)) {  // causal boundary or split end
+      for (int t = 0; t < kSub; ++t) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = key0 + 4 * g + i;
-            sc[i] = (key <= q_pos[nb] && key <= last) ? sc[i] : kNegInf;
-          }
+        for (int i = 0; i < 4; ++i) {
+          p[nb][t][i] = kPow2Scale ? round_storage<T>(p[nb][t][i]) : scaled_score<T>(p[nb][t][i], a.scale);
         }
-        softmax_tile<D>(st[nb], sc);
-        p[nb] = sc;
       }
     }
+    if (!full) {  // causal boundary or item end inside the step
+#pragma unroll
+      for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+        for (int t = 0; t < kSub; ++t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + t * kTileKeys + 4 * g + i;
+            p[nb][t][i] = (key <= q_pos[nb] && key <= last) ? p[nb][t][i] : kNegInf;
+          }
+        }
+      }
+    }
+    softmax_step<D, kRowBlocks, kSub>(st, p, exp_c);
     if constexpr (Elt<T>::kIsBf16) {
-      const uint32_t sb = lds_off(stage);
 #pragma unroll
-      for (int c0 = 0; c0 < D / 16; c0 += 4) {
-        uint32_t va[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) va[i] = sb + vtr[c0 + i];
-        v4s vt[4];
-        ring_read_vt4(vt, va);
+      for (int t = 0; t < kSub; t += 2) {
 #pragma unroll
         for (int nb = 0; nb < kRowBlocks; ++nb) {
-          if (!live[nb]) continue;
-          const v4s pb = pack_bf16x4(p[nb][0], p[nb][1], p[nb][2], p[nb][3]);
+          const bf16x8_t pp = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
+                                          pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
+                                                      p[nb][t + 1][3]));
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            st[nb].o[c0 + c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[c], pb, st[nb].o[c0 + c], 0, 0, 0);
+          for (int c = 0; c < D / 16; ++c) {
+            const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
+                                            __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
+            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp, st[nb].o[c], 0, 0, 0);
           }
         }
       }
     } else {
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        float vv[4];
+      for (int t = 0; t < kSub; ++t) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vv[j] = *reinterpret_cast<const float*>(stage + voff[4 * c + j]);
+        for (int c = 0; c < D / 16; ++c) {
+          float vv[4];
 #pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-          if (!live[nb]) continue;
+          for (int j = 0; j < 4; ++j) vv[j] = *reinterpret_cast<const float*>(stage + t * kTileStride + voff[4 * c + j]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], p[nb][j], st[nb].o[c], 0, 0, 0);
+          for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], p[nb][t][j], st[nb].o[c], 0, 0, 0);
+            }
           }
         }
       }
     }
   };
 
-  const int ntiles = tile_end - tile_begin;
-  const int last_key0 = (tile_end - 1) * kTileKeys;
+  const int nsteps = (tile_end - tile_begin + kSub - 1) / kSub;
   constexpr int kAhead = kStages - 1;
 #pragma unroll
-  for (int j = 0; j < kAhead; ++j) issue(j, min((tile_begin + j) * kTileKeys, last_key0));
-  for (int t = 0; t < ntiles; t += kStages) {
+  for (int j = 0; j < kAhead; ++j) issue(j, (tile_begin + j * kSub) * kTileKeys);
+  for (int s0 = 0; s0 < nsteps; s0 += kStages) {
 #pragma unroll
     for (int j = 0; j < kStages; ++j) {
-      const int tt = t + j;
-      if (tt >= ntiles) break;  // uniform over the workgroup
-      // this wave's ops for tile tt are done once at most the kAhead-1 later
-      // tiles' ops are outstanding; the barrier extends that to every wave
-      // and guarantees that every wave has finished reading tile tt-1
+      const int s = s0 + j;
+      if (s >= nsteps) break;  // uniform over the workgroup
+      // this wave's ops for step s are done once at most the kAhead-1 later
+      // steps' ops are outstanding; the barrier extends that to every wave
+      // and guarantees that every wave has finished reading step s-1
       __builtin_amdgcn_s_waitcnt(waitcnt_vm((kAhead - 1) * kOwnOps));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      issue((j + kAhead) % kStages, min((tile_begin + tt + kAhead) * kTileKeys, last_key0));
+      issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
       __builtin_amdgcn_sched_barrier(0);
-      consume(j, (tile_begin + tt) * kTileKeys);
+      consume(j, (tile_begin + s * kSub) * kTileKeys);
     }
   }
   // drain the redundant prefetches before the LDS is handed to another workgroup
@@ -1585,92 +1702,227 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void varlen_prefill_kernel(Pr
         *reinterpret_cast<float4*>(dst + 16 * c) =
             make_float4(st[nb].o[c][0], st[nb].o[c][1], st[nb].o[c][2], st[nb].o[c][3]);
       }
-      if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + slot * 2) = make_float2(st[nb].m, lsum);
+      // the merge expects the maximum of the scaled scores
+      const float m = kPow2Scale ? st[nb].m * a.scale : st[nb].m;
+      if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + slot * 2) = make_float2(m, lsum);
     }
   }
 }
 
-// Merge of split prefill rows: one wave per (query token, query head).  The
-// token's request, query tile and that tile's first item are recomputed
-// from cu_seqlens / context_lens exactly as the prefill kernel enumerates
-// its items; tiles with a single split were finished by the prefill kernel.
-template <typename T, int D, int kRowBlocks>
-__global__ __launch_bounds__(kMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a) {
-  constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
-  const int64_t t = blockIdx.x;  // packed query row
-  const int qh = (int)blockIdx.y * kMergeWaves + (int)(threadIdx.x / kWave);
-  if (qh >= a.geom.kv_heads * a.group) return;
-  const int lane = lane_id();
-  // request r with cu[r] <= t < cu[r+1], and the items of requests before it
-  int64_t r = -1, before = 0;
-  for (int64_t b0 = 0; b0 < a.num_seqs && r < 0; b0 += kWave) {
-    const int64_t b = b0 + lane;
-    const bool in = b < a.num_seqs && a.cu_seqlens[b] <= t && t < a.cu_seqlens[b + 1];
-    const uint64_t mask = __ballot(in);
-    const int64_t upto = mask ? b0 + __builtin_ctzll(mask) : a.num_seqs;  // requests before r (this chunk)
-    int64_t n = (b < upto) ? prefill_items_of(a, b) : 0;
+// Merge of split prefill rows: one workgroup per query tile (and KV head)
+// that has several splits, one wave per block of 16 of its rows.  Lane l
+// takes 4-dim chunk l%16 (and l%16 + 16, ... for larger head_dim) of rows
+// l/16 + 4i, and walks the splits in batches whose loads are all issued
+// before any is used, combining batches through a running maximum per row
+// (exact log-sum-exp weights, splits in order).
+template <int kRowBlocks>
+constexpr int prefill_merge_waves() {
+  return prefill_rows_per_item<kRowBlocks>() / 16;
+}
+
+// Sum of prefill_items_of over the sequences before r (wave-uniform).
+__device__ __forceinline__ int64_t prefill_items_before(const PrefillArgs& a, int64_t r) {
+  int64_t n = 0;
+  for (int64_t b = lane_id(); b < r; b += kWave) n += prefill_items_of(a, b);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) n += __shfl_xor(n, off);
-    before += n;
-    if (mask) r = upto;
-  }
-  if (r < 0) return;
-  r = uniform64(r);
-  before = uniform64(before);
+  for (int off = 32; off > 0; off >>= 1) n += __shfl_xor(n, off);
+  return uniform64(n);
+}
+
+template <typename T, int D, int kRowBlocks>
+__global__ __launch_bounds__(prefill_merge_waves<kRowBlocks>() * kWave) void prefill_merge_kernel(PrefillArgs a) {
+  constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
+  constexpr int kChunkPasses = D / 64;  // 4-dim chunks per lane and row
+  constexpr int kRowsPerLane = 4;
+  constexpr int kBatch = 4;
+  const int tpt = a.tokens_per_tile;
+  const int S = a.tiles_per_split;
+  int64_t r, qt64, first_q, count_q;
+  locate_item((int64_t)blockIdx.x, a.num_seqs,
+              [&](int64_t b) { return (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + tpt - 1) / tpt; }, &r, &qt64,
+              &first_q, &count_q);
+  if (r < 0) return;  // uniform over the workgroup
+  const int qt = (int)qt64;
+  const int h = (int)blockIdx.y;
   const int64_t q_begin = a.cu_seqlens[r];
   const int q_len = (int)(a.cu_seqlens[r + 1] - q_begin);
   const int ctx = a.context_lens[r];
-  const int tpt = a.tokens_per_tile;
-  const int S = a.tiles_per_split;
-  const int tt = (int)(t - q_begin);
-  const int qt = tt / tpt;
-  int64_t first = before;
-  for (int k = 0; k < qt; ++k) first += (prefill_key_tiles(ctx, q_len, tpt, k) + S - 1) / S;
   const int nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
-  if (nsplit <= 1 || first + nsplit > a.ws_items) return;
-  const int h = qh / a.group;
+  if (nsplit <= 1) return;  // the prefill kernel wrote these rows
+  int64_t first = prefill_items_before(a, r);  // the tile's first item
+  for (int k = 0; k < qt; ++k) first += (prefill_key_tiles(ctx, q_len, tpt, k) + S - 1) / S;
+  if (first + nsplit > a.ws_items) return;
+  const int lane = lane_id();
+  const int wave = (int)(threadIdx.x / kWave);
+  const int chunk = lane & 15;
   const int tpb = 16 / a.group;
-  const int in_tile = tt - qt * tpt;
-  const int row = (in_tile / tpb) * 16 + (in_tile % tpb) * a.group + qh % a.group;
-  const int64_t slot = (first * a.geom.kv_heads + h) * kRows + row;
-  const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;
-  merge_row<T, D>(a.ws_o + slot * D, split_stride * D, a.ws_ml + slot * 2, split_stride * 2, nsplit,
-                  reinterpret_cast<T*>(a.out) + t * a.o_st + qh * a.o_sh);
+  const int t0 = qt * tpt;
+  const int t_end = min(t0 + tpt, q_len);
+  const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;  // rows between consecutive items
+  const int64_t slot0 = (first * a.geom.kv_heads + h) * kRows + wave * 16;
+
+  float run_max[kRowsPerLane], denom[kRowsPerLane];
+  float4 acc[kRowsPerLane][kChunkPasses];
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) {
+    run_max[i] = kNegInf;
+    denom[i] = 0.f;
+#pragma unroll
+    for (int c = 0; c < kChunkPasses; ++c) acc[i][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+    float4 v[kBatch][kRowsPerLane][kChunkPasses];
+    float2 ml[kBatch][kRowsPerLane];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const bool in = s0 + b < nsplit;
+#pragma unroll
+      for (int i = 0; i < kRowsPerLane; ++i) {
+        const int64_t slot = slot0 + (s0 + b) * split_stride + (lane >> 4) + 4 * i;
+        ml[b][i] = in ? *reinterpret_cast<const float2*>(a.ws_ml + slot * 2) : make_float2(kNegInf, 0.f);
+#pragma unroll
+        for (int c = 0; c < kChunkPasses; ++c) {
+          v[b][i][c] = in ? *reinterpret_cast<const float4*>(a.ws_o + slot * D + 4 * (chunk + 16 * c))
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsPerLane; ++i) {
+      float bmax = ml[0][i].x;
+#pragma unroll
+      for (int b = 1; b < kBatch; ++b) bmax = fmaxf(bmax, ml[b][i].x);
+      const float new_max = fmaxf(run_max[i], bmax);
+      const float keep = run_max[i] == kNegInf ? 0.f : exp2f((run_max[i] - new_max) * kLog2e);
+      denom[i] *= keep;
+#pragma unroll
+      for (int c = 0; c < kChunkPasses; ++c) {
+        acc[i][c].x *= keep;
+        acc[i][c].y *= keep;
+        acc[i][c].z *= keep;
+        acc[i][c].w *= keep;
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const float w = ml[b][i].x == kNegInf ? 0.f : exp2f((ml[b][i].x - new_max) * kLog2e);
+        denom[i] += w * ml[b][i].y;
+#pragma unroll
+        for (int c = 0; c < kChunkPasses; ++c) {
+          acc[i][c].x += w * v[b][i][c].x;
+          acc[i][c].y += w * v[b][i][c].y;
+          acc[i][c].z += w * v[b][i][c].z;
+          acc[i][c].w += w * v[b][i][c].w;
+        }
+      }
+      run_max[i] = new_max;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRowsPerLane; ++i) {
+    const int rr = (lane >> 4) + 4 * i;  // row within the wave's block
+    const int tq = t0 + (wave * tpb) + rr / a.group;
+    if (tq >= t_end) continue;
+    const int qh = h * a.group + rr % a.group;
+    const float inv = 1.f / denom[i];
+    T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh;
+#pragma unroll
+    for (int c = 0; c < kChunkPasses; ++c) {
+      store4<T>(dst + 4 * (chunk + 16 * c), acc[i][c].x * inv, acc[i][c].y * inv, acc[i][c].z * inv,
+                acc[i][c].w * inv);
+    }
+  }
 }
 
-// Work decomposition of a prefill call, from host-side bounds only: query
-// tiles of tokens_per_tile tokens, each split into items of at most
-// tiles_per_split key tiles, chosen so an upper bound on the total work
-// gives about kPrefillTargetItems workgroups (several resident per CU).
+// Work decomposition of a prefill call: query tiles of tokens_per_tile
+// tokens, each split into items of at most tiles_per_split key tiles.  With
+// host copies of the lengths the split length fills the GPU's resident
+// workgroup slots about once and the grid is exact; without them an upper
+// bound on the total work gives about kPrefillTargetItems workgroups.
 constexpr int64_t kPrefillTargetItems = 2048;
 constexpr int64_t kPrefillMinTilesPerSplit = 8;
 constexpr int64_t kPrefillMaxTilesPerSplit = 64;
 
 struct PrefillPlan {
-  int row_blocks = 1;  // MFMA row blocks per wave
+  int row_blocks = 2;  // MFMA row blocks per wave
   int tokens_per_tile = 64;
   int64_t tps = kPrefillMaxTilesPerSplit;
-  int64_t items = 0;  // grid.x: an upper bound on the number of items
-  int64_t rows = 0;   // rows per item
+  int64_t items = 0;   // prefill grid.x: the item count (exact from host metadata, else a bound)
+  int64_t qtiles = 0;  // merge grid.x: the query-tile count (exact, else a bound)
+  int64_t rows = 0;    // rows per item
+  bool split = false;  // some query tile is split over several items
 };
 
+// Workgroups of the prefill kernel resident at once (two per CU at head_dim
+// 64): with host metadata the split length is chosen so the call's items
+// fill them about once.
+constexpr int64_t kPrefillSlots = 2 * kDecodeCUs;
+
+// Key tiles visible to query tile qt of a request with n query tokens after
+// ctx cached ones (host side of prefill_key_tiles).
+int64_t host_key_tiles(int64_t ctx, int64_t n, int64_t tpt, int64_t qt) {
+  const int64_t t_end = (qt + 1) * tpt < n ? (qt + 1) * tpt : n;
+  return cdiv(ctx + t_end, (int64_t)kTileKeys);
+}
+
+// host_cu / host_ctx: optional host copies of cu_seqlens / context_lens,
+// already validated by the caller; without them the plan uses bounds.
 PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int64_t total_tokens,
-                         int64_t max_seq_len) {
+                         int64_t max_seq_len, const int64_t* host_cu, const int32_t* host_ctx) {
   PrefillPlan p;
-  p.row_blocks = group >= 4 ? 4 : (int)group;
+  static const int forced_rb = env_int("NIE_PREFILL_ROW_BLOCKS");
+  if (forced_rb == 1 || forced_rb == 2) p.row_blocks = forced_rb;
   p.tokens_per_tile = kPrefillWaves * p.row_blocks * (int)(16 / group);
   p.rows = kPrefillWaves * p.row_blocks * 16;
-  const int64_t qtiles = total_tokens / p.tokens_per_tile + num_seqs;  // >= sum_r ceil(len_r / tpt)
-  const int64_t ktiles = cdiv(max_seq_len, kTileKeys);
-  const int64_t work = qtiles * ktiles;                                 // >= key tiles over all query tiles
-  int64_t tps = cdiv(work * kv_heads, kPrefillTargetItems);
-  tps = tps < kPrefillMinTilesPerSplit ? kPrefillMinTilesPerSplit : tps;
-  tps = tps > kPrefillMaxTilesPerSplit ? kPrefillMaxTilesPerSplit : tps;
+  const int64_t tpt = p.tokens_per_tile;
   static const int64_t forced = env_int("NIE_PREFILL_TILES_PER_SPLIT");
-  if (forced > 0) tps = forced < kPrefillMaxTilesPerSplit ? forced : kPrefillMaxTilesPerSplit;
-  p.tps = tps;
-  p.items = work / tps + qtiles + 1;  // sum ceil(n / tps) <= sum n / tps + count
+  auto clamp_tps = [&](int64_t tps) {
+    if (forced > 0) tps = forced;
+    tps = tps < kPrefillMinTilesPerSplit ? kPrefillMinTilesPerSplit : tps;
+    tps = tps > kPrefillMaxTilesPerSplit ? kPrefillMaxTilesPerSplit : tps;
+    return cdiv(tps, (int64_t)kPrefillStepTiles) * kPrefillStepTiles;  // whole key steps
+  };
+  if (host_cu != nullptr && host_ctx != nullptr) {
+    int64_t work = 0, qtiles = 0, max_kt = 0;
+    for (int64_t r = 0; r < num_seqs; ++r) {
+      const int64_t n = host_cu[r + 1] - host_cu[r];
+      const int64_t nqt = cdiv(n, tpt);
+      qtiles += nqt;
+      for (int64_t qt = 0; qt < nqt; ++qt) {
+        const int64_t kt = host_key_tiles(host_ctx[r], n, tpt, qt);
+        work += kt;
+        max_kt = kt > max_kt ? kt : max_kt;
+      }
+    }
+    p.tps = clamp_tps(cdiv(work * kv_heads, kPrefillSlots));
+    int64_t items = 0;
+    for (int64_t r = 0; r < num_seqs; ++r) {
+      const int64_t n = host_cu[r + 1] - host_cu[r];
+      for (int64_t qt = 0; qt < cdiv(n, tpt); ++qt) items += cdiv(host_key_tiles(host_ctx[r], n, tpt, qt), p.tps);
+    }
+    p.items = items;
+    p.qtiles = qtiles;
+    p.split = max_kt > p.tps;
+    return p;
+  }
+  const int64_t qtiles = total_tokens / tpt + num_seqs;  // >= sum_r ceil(len_r / tpt)
+  const int64_t ktiles = cdiv(max_seq_len, (int64_t)kTileKeys);
+  const int64_t work = qtiles * ktiles;                  // >= key tiles over all query tiles
+  p.tps = clamp_tps(cdiv(work * kv_heads, kPrefillTargetItems));
+  p.items = work / p.tps + qtiles + 1;  // sum ceil(n / tps) <= sum n / tps + count
+  p.qtiles = qtiles;
+  p.split = ktiles > p.tps;
   return p;
+}
+
+// Checks host copies of cu_seqlens / context_lens against the call's sizes.
+bool host_metadata_ok(const int64_t* host_cu, const int32_t* host_ctx, int64_t num_seqs, int64_t total_tokens,
+                      int64_t max_query_len, int64_t max_seq_len) {
+  if (host_cu[0] != 0 || host_cu[num_seqs] != total_tokens) return false;
+  for (int64_t r = 0; r < num_seqs; ++r) {
+    const int64_t n = host_cu[r + 1] - host_cu[r];
+    if (n < 0 || n > max_query_len || host_ctx[r] < 0 || host_ctx[r] + n > max_seq_len) return false;
+  }
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -1850,30 +2102,43 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
   }
 }
 
+template <typename T, int D, int NB, bool P2>
+void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, hipStream_t stream) {
+  const dim3 grid((unsigned)p.items, (unsigned)a.geom.kv_heads);
+  if (uniform_tiles(a.geom)) {
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+  }
+}
+
+// A positive power of two (the softmax scale of head_dim 64 is 1/8).
+bool is_pow2_scale(float scale) {
+  int e = 0;
+  return scale > 0.f && std::isfinite(scale) && std::frexp(scale, &e) == 0.5f && std::isnormal(scale);
+}
+
 template <typename T, int D, int NB>
 void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, int64_t total_tokens, hipStream_t stream,
                        bool merge) {
-  const dim3 grid((unsigned)p.items, (unsigned)a.geom.kv_heads);
-  if (uniform_tiles(a.geom)) {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+  if constexpr (Elt<T>::kIsBf16) {
+    if (is_pow2_scale(a.scale)) launch_prefill_kernel<T, D, NB, true>(a, p, stream);
+    else launch_prefill_kernel<T, D, NB, false>(a, p, stream);
   } else {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+    launch_prefill_kernel<T, D, NB, false>(a, p, stream);
   }
   if (merge) {
-    const int64_t q_heads = (int64_t)a.geom.kv_heads * a.group;
-    const dim3 mgrid((unsigned)total_tokens, (unsigned)cdiv(q_heads, (int64_t)kMergeWaves));
-    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a);
+    const dim3 grid((unsigned)p.qtiles, (unsigned)a.geom.kv_heads);
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(prefill_merge_waves<NB>() * kWave), 0, stream,
+                       a);
   }
 }
 
 template <typename T, int D>
 void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, int64_t total_tokens, hipStream_t stream,
                     bool merge) {
-  switch (p.row_blocks) {
-    case 1: launch_prefill_nb<T, D, 1>(a, p, total_tokens, stream, merge); break;
-    case 2: launch_prefill_nb<T, D, 2>(a, p, total_tokens, stream, merge); break;
-    default: launch_prefill_nb<T, D, 4>(a, p, total_tokens, stream, merge); break;
-  }
+  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, total_tokens, stream, merge);
+  else launch_prefill_nb<T, D, 2>(a, p, total_tokens, stream, merge);
 }
 
 int check_aligned(const void* p, int64_t stride_a, int64_t stride_b, int64_t es) {
@@ -2152,14 +2417,20 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
 NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query_tokens,
                                                    int64_t max_query_len, int64_t max_seq_len,
                                                    int64_t q_heads, int64_t kv_heads,
-                                                   int64_t head_dim) {
-  (void)max_query_len;
-  if (num_seqs <= 0 || total_query_tokens <= 0 || max_seq_len <= 0 ||
+                                                   int64_t head_dim, const int64_t* host_cu_seqlens,
+                                                   const int32_t* host_context_lens) {
+  if (num_seqs <= 0 || total_query_tokens <= 0 || max_seq_len <= 0 || max_query_len <= 0 ||
       check_attention_shape(q_heads, kv_heads, head_dim, 1, 1) != NIE_OK) {
     return 0;
   }
-  const PrefillPlan p = plan_prefill(q_heads / kv_heads, kv_heads, num_seqs, total_query_tokens, max_seq_len);
-  if (cdiv(max_seq_len, kTileKeys) <= p.tps) return 0;  // no query tile is split
+  const bool host = host_cu_seqlens != nullptr && host_context_lens != nullptr;
+  if (host && !host_metadata_ok(host_cu_seqlens, host_context_lens, num_seqs, total_query_tokens, max_query_len,
+                                max_seq_len)) {
+    return 0;
+  }
+  const PrefillPlan p = plan_prefill(q_heads / kv_heads, kv_heads, num_seqs, total_query_tokens, max_seq_len,
+                                     host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr);
+  if (!p.split) return 0;  // no query tile is split
   return p.items * kv_heads * p.rows * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
@@ -2172,7 +2443,8 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
                                int64_t kv_heads, int64_t head_dim, const int32_t* block_tables,
                                int64_t table_stride, float scale, void* out,
                                int64_t out_stride_t, int64_t out_stride_h, void* workspace,
-                               int64_t workspace_bytes, void* stream) {
+                               int64_t workspace_bytes, const int64_t* host_cu_seqlens,
+                               const int32_t* host_context_lens, void* stream) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -2196,10 +2468,19 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
       ((uintptr_t)k_cache % 16) || ((uintptr_t)v_cache % 16)) {
     return fail(NIE_EINVAL, "q/out/cache pointers and strides must be 16-byte aligned");
   }
+  const bool host = host_cu_seqlens != nullptr && host_context_lens != nullptr;
+  if (host && !host_metadata_ok(host_cu_seqlens, host_context_lens, num_seqs, total_query_tokens, max_query_len,
+                                max_seq_len)) {
+    return fail(NIE_EINVAL, "host cu_seqlens / context_lens do not match the sizes of the call");
+  }
   const int group = (int)(q_heads / kv_heads);
-  const PrefillPlan plan = plan_prefill(group, kv_heads, num_seqs, total_query_tokens, max_seq_len);
-  if (plan.items > 0x7fffffffLL || total_query_tokens > 0x7fffffffLL) return fail(NIE_EINVAL, "grid too large");
-  const bool may_split = cdiv(max_seq_len, kTileKeys) > plan.tps;
+  const PrefillPlan plan = plan_prefill(group, kv_heads, num_seqs, total_query_tokens, max_seq_len,
+                                        host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr);
+  if (plan.items > 0x7fffffffLL || plan.qtiles > 0x7fffffffLL || total_query_tokens > 0x7fffffffLL) {
+    return fail(NIE_EINVAL, "grid too large");
+  }
+  if (plan.items == 0) return NIE_OK;
+  const bool may_split = plan.split;
   const int64_t need = plan.items * kv_heads * plan.rows * (head_dim + 2) * (int64_t)sizeof(float);
   if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,

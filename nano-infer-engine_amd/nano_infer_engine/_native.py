@@ -12,6 +12,7 @@ import ctypes
 import os
 import threading
 
+import numpy as np
 import torch
 
 LIBRARY_NAME = "libnie_hip.so"
@@ -89,7 +90,7 @@ _SIGNATURES = {
             _ptr, _i64, _ptr,                # workspace, bytes, stream
         ],
     ),
-    "nie_varlen_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "nie_varlen_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr]),
     "nie_varlen_prefill": (
         _i32,
         [
@@ -102,7 +103,8 @@ _SIGNATURES = {
             _ptr, _i64,                      # block tables, stride
             _f32,                            # scale
             _ptr, _i64, _i64,                # out, strides
-            _ptr, _i64, _ptr,                # workspace, bytes, stream
+            _ptr, _i64,                      # workspace, bytes
+            _ptr, _ptr, _ptr,                # host cu_seqlens, host context_lens, stream
         ],
     ),
 }
@@ -126,6 +128,25 @@ def _decode_workspace(device: torch.device, stream: int, nbytes: int) -> torch.T
             ws = torch.empty(size, dtype=torch.uint8, device=device)
             _decode_workspaces[key] = ws
     return ws
+
+
+def _host_lengths(cu_seqlens_host, context_lens_host, num_seqs: int):
+    """Host copies of cu_seqlens / context_lens as C arrays (or (None, None)).
+
+    Given, they let the library plan a prefill launch from the exact work;
+    they must hold the same values as the device tensors.
+    """
+    if cu_seqlens_host is None or context_lens_host is None:
+        return None, None
+    cu = np.ascontiguousarray(np.asarray(cu_seqlens_host, dtype=np.int64))
+    ctx = np.ascontiguousarray(np.asarray(context_lens_host, dtype=np.int32))
+    if cu.shape != (num_seqs + 1,) or ctx.shape != (num_seqs,):
+        raise ValueError("host cu_seqlens / context_lens must have num_seqs + 1 / num_seqs entries")
+    return cu, ctx
+
+
+def _array_ptr(a) -> int | None:
+    return None if a is None else a.ctypes.data
 
 
 def library_path() -> str:
@@ -469,12 +490,16 @@ def varlen_prefill(
     max_seq_len: int,
     scale: float,
     out: torch.Tensor | None = None,
+    cu_seqlens_host=None,
+    context_lens_host=None,
 ) -> torch.Tensor:
     """Causal varlen attention of packed query rows (ΣT, Hq, D) over the paged cache.
 
     Sequence r owns rows cu_seqlens[r]..cu_seqlens[r+1]-1 at absolute
     positions context_lens[r] + i.  ``max_query_len`` and ``max_seq_len``
-    (max of context + query) are exact host-side values.
+    (max of context + query) are exact host-side values.  The optional
+    ``cu_seqlens_host`` / ``context_lens_host`` (sequences of ints equal to
+    the device tensors) let the launch be planned from the exact work.
     """
     num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
     _require_gpu(query, cu_seqlens, context_lens, block_tables)
@@ -498,9 +523,11 @@ def varlen_prefill(
         out = torch.empty((total_tokens, q_heads, head_dim), dtype=query.dtype, device=query.device)
     if total_tokens == 0 or num_seqs == 0:
         return out
+    host_cu, host_ctx = _host_lengths(cu_seqlens_host, context_lens_host, num_seqs)
     lib = load_library()
     ws_bytes = lib.nie_varlen_prefill_workspace_bytes(
-        num_seqs, total_tokens, max_query_len, max_seq_len, q_heads, kv_heads, head_dim
+        num_seqs, total_tokens, max_query_len, max_seq_len, q_heads, kv_heads, head_dim,
+        _array_ptr(host_cu), _array_ptr(host_ctx),
     )
     stream = _stream(query.device)
     workspace = _decode_workspace(query.device, stream, ws_bytes) if ws_bytes > 0 else None
@@ -516,6 +543,7 @@ def varlen_prefill(
         float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
         None if workspace is None else workspace.data_ptr(), 0 if workspace is None else workspace.numel(),
+        _array_ptr(host_cu), _array_ptr(host_ctx),
         stream,
     )
     _check(rc, "nie_varlen_prefill")
@@ -657,7 +685,7 @@ class PreparedPrefill:
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, cu_seqlens: torch.Tensor,
                  context_lens: torch.Tensor, block_tables: torch.Tensor, total_tokens: int, max_query_len: int,
-                 max_seq_len: int, q_heads: int, scale: float):
+                 max_seq_len: int, q_heads: int, scale: float, cu_seqlens_host=None, context_lens_host=None):
         num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
         _require_gpu(cu_seqlens, context_lens, block_tables)
         _check_attention_shapes(q_heads, kv_heads, head_dim)
@@ -669,21 +697,24 @@ class PreparedPrefill:
         if (block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != num_seqs
                 or not block_tables.is_contiguous()):
             raise ValueError("block_tables must be a contiguous int32 (num_seqs, max_blocks) tensor")
+        host_cu, host_ctx = _host_lengths(cu_seqlens_host, context_lens_host, num_seqs)
         lib = load_library()
         ws_bytes = lib.nie_varlen_prefill_workspace_bytes(num_seqs, total_tokens, max_query_len, max_seq_len,
-                                                          q_heads, kv_heads, head_dim)
+                                                          q_heads, kv_heads, head_dim, _array_ptr(host_cu),
+                                                          _array_ptr(host_ctx))
         stream = _stream(k_cache.device)
         workspace = _decode_workspace(k_cache.device, stream, ws_bytes) if ws_bytes > 0 else None
         self._fn = lib.nie_varlen_prefill
         self._dtype = k_cache.dtype
         self._device = k_cache.device
         self._shape = (total_tokens, q_heads, head_dim)
-        self._keep = (cu_seqlens, context_lens, block_tables, workspace)
+        self._keep = (cu_seqlens, context_lens, block_tables, workspace, host_cu, host_ctx)
         self._args = (dtype_code(k_cache.dtype), cu_seqlens.data_ptr(), context_lens.data_ptr(), num_seqs,
                       total_tokens, max_query_len, max_seq_len, k_cache.data_ptr(), v_cache.data_ptr(), num_layers,
                       num_blocks, block_size, q_heads, kv_heads, head_dim, block_tables.data_ptr(),
                       block_tables.shape[1], float(scale),
-                      (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel()), stream)
+                      (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel()),
+                      (_array_ptr(host_cu), _array_ptr(host_ctx)), stream)
 
     def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
         for t in (query, out):
@@ -691,10 +722,11 @@ class PreparedPrefill:
                     or t.data_ptr() % 16):
                 raise ValueError("query/out must be aligned (tokens, q_heads, head_dim) tensors matching the batch")
         (code, cu, ctx, num_seqs, total, max_q, max_s, kptr, vptr, num_layers, num_blocks, block_size, q_heads,
-         kv_heads, head_dim, tables, tstride, scale, (ws, ws_bytes), stream) = self._args
+         kv_heads, head_dim, tables, tstride, scale, (ws, ws_bytes), (hcu, hctx), stream) = self._args
         rc = self._fn(code, query.data_ptr(), query.stride(0), query.stride(1), cu, ctx, num_seqs, total, max_q,
                       max_s, kptr, vptr, num_layers, layer_index, num_blocks, block_size, q_heads, kv_heads, head_dim,
-                      tables, tstride, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes, stream)
+                      tables, tstride, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes, hcu, hctx,
+                      stream)
         if rc:
             _check(rc, "nie_varlen_prefill")
         return out

@@ -89,10 +89,13 @@ class RaggedBatch:
         prefill = decode = None
         if split > 0:
             seq_lens = [c + n for c, n in zip(self.context_lens[:split], self.query_lens[:split])]
+            cu_host = [0]
+            for n in self.query_lens[:split]:
+                cu_host.append(cu_host[-1] + n)
             prefill = _native.PreparedPrefill(
                 cache.keys, cache.values, self.cu_seqlens[: split + 1], self.context_lens_t[:split],
                 self.block_tables[:split], self.first_decode_token, max(self.query_lens[:split]), max(seq_lens),
-                q_heads, scale,
+                q_heads, scale, cu_seqlens_host=cu_host, context_lens_host=self.context_lens[:split],
             )
         if split < self.num_requests:
             rows = self.num_requests - split

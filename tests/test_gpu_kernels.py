@@ -307,7 +307,9 @@ def test_decode_workspace_reuse_across_calls():
         assert err <= 2e-2
 
 
-def _prefill_case(wl, dtype):
+def _prefill_case(wl, dtype, host_plan=True):
+    """The kernel's output and the oracle's.  host_plan: pass host copies of
+    the lengths (exact launch plan) or not (plan from upper bounds)."""
     kc, vc = wl.pool(dtype)
     q, k_new, v_new = wl.new_tokens(dtype)
     ref_k, ref_v = kc.clone(), vc.clone()
@@ -319,18 +321,20 @@ def _prefill_case(wl, dtype):
     cu = torch.tensor(np.concatenate([[0], np.cumsum(wl.query_lens)]), dtype=torch.int64, device=DEV)
     ctx = torch.tensor(wl.context_lens, dtype=torch.int32, device=DEV)
     tables = torch.from_numpy(wl.table_array()).to(DEV)
+    host = dict(cu_seqlens_host=cu.cpu().tolist(), context_lens_host=list(wl.context_lens)) if host_plan else {}
     got = _native.varlen_prefill(q.to(DEV), cu, ctx, dk, dv, 0, tables, max(wl.query_lens), max(wl.seq_lens),
-                                 wl.head_dim**-0.5)
+                                 wl.head_dim**-0.5, **host)
     torch.cuda.synchronize()
     assert torch.equal(dk.cpu(), ref_k) and torch.equal(dv.cpu(), ref_v)
     return got.cpu(), want
 
 
+@pytest.mark.parametrize("host_plan", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_varlen_prefill_mixed_batch(dtype):
-    _log(f"varlen mixed {dtype}")
+def test_varlen_prefill_mixed_batch(dtype, host_plan):
+    _log(f"varlen mixed {dtype} host_plan={host_plan}")
     wl = workloads.mixed_prefill()
-    got, want = _prefill_case(wl, dtype)
+    got, want = _prefill_case(wl, dtype, host_plan)
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")
     assert err <= TOL[dtype]
@@ -355,15 +359,16 @@ def test_varlen_prefill_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
     "q_heads,kv_heads,head_dim,block_size",
     [(4, 4, 64, 16), (8, 4, 64, 16), (16, 4, 64, 8), (32, 4, 64, 16), (32, 8, 128, 16), (16, 1, 128, 32)],
 )
+@pytest.mark.parametrize("host_plan", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_varlen_prefill_split_keys(q_heads, kv_heads, head_dim, block_size, dtype):
+def test_varlen_prefill_split_keys(q_heads, kv_heads, head_dim, block_size, dtype, host_plan):
     """Contexts long enough that query tiles are split over several workgroups
     (at least 8 key tiles per split) and merged, next to short requests and
-    decode rows."""
-    _log(f"varlen split hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype}")
+    decode rows; launches planned from host lengths and from bounds."""
+    _log(f"varlen split hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} host_plan={host_plan}")
     wl = workloads.ragged([700, 0, 300, 1500, 33], [70, 130, 1, 9, 64], seed=17, pool_factor=1.3, q_heads=q_heads,
                           kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
-    got, want = _prefill_case(wl, dtype)
+    got, want = _prefill_case(wl, dtype, host_plan)
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")
     assert err <= TOL[dtype]

@@ -284,4 +284,28 @@ def test_library_workspace_queries():
     assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1) == 0
     assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710) == 0  # bad dtype
     assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710) == 0  # head_dim 96
-    assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 64) >= 0
+    # prefill, planned from bounds
+    assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 64, None, None) > 0
+
+
+def test_library_prefill_plan_from_host_lengths():
+    """With host copies of the lengths the prefill plan uses the exact work:
+    split partials exist only when some query tile's keys are split, are a
+    whole number of (items x kv_heads x 128 rows x (64 + 2) floats), and
+    lengths that do not fit the call's sizes are rejected."""
+    lib = _native.load_library()
+
+    def query(cu, ctx, total, max_q, max_s):
+        cu = np.asarray(cu, dtype=np.int64)
+        ctx = np.asarray(ctx, dtype=np.int32)
+        return lib.nie_varlen_prefill_workspace_bytes(len(ctx), total, max_q, max_s, 32, 8, 64,
+                                                      cu.ctypes.data, ctx.ctypes.data)
+
+    # four 128-token chunks on empty contexts: at most 8 key tiles per query tile, never split
+    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 0
+    # the mixed step's chunks (contexts 0, 384, 1024, 4000): the long context is split
+    mixed = query([0, 128, 256, 384, 512], [0, 384, 1024, 4000], 512, 128, 4128)
+    assert mixed > 0 and mixed % (8 * 128 * 66 * 4) == 0
+    # lengths that do not match the sizes of the call
+    assert query([0, 128, 256, 384, 500], [0, 384, 1024, 4000], 512, 128, 4128) == 0
+    assert query([0, 128, 256, 384, 512], [0, 384, 1024, 4001], 512, 128, 4128) == 0
