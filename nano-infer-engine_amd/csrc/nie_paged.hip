@@ -117,6 +117,15 @@ __device__ __forceinline__ float round_to_bf16(float x) {
   return (float)(__bf16)x;
 }
 
+// Rounds four floats to bf16 (round to nearest even): one v_cvt_pk_bf16_f32
+// per pair, then each half widened back.
+__device__ __forceinline__ v4f round_bf16x4(v4f v) {
+  const uint32_t lo = pack_bf16x2(v[0], v[1]);
+  const uint32_t hi = pack_bf16x2(v[2], v[3]);
+  return v4f{__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u), __uint_as_float(hi << 16),
+             __uint_as_float(hi & 0xffff0000u)};
+}
+
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Four floats -> the bf16 MFMA operand (element i = x[i]).
@@ -1277,14 +1286,73 @@ __device__ __forceinline__ int prefill_key_tiles(int ctx, int q_len, int tpt, in
   return (ctx + t_end + kTileKeys - 1) / kTileKeys;
 }
 
+// Work items (query tile, key split) of a request with q_len query tokens
+// after ctx cached ones.
+__device__ __forceinline__ int prefill_items_of_len(int q_len, int ctx, int tpt, int S) {
+  const int nqt = (q_len + tpt - 1) / tpt;
+  int n = 0;
+  for (int qt = 0; qt < nqt; ++qt) n += (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
+  return n;
+}
+
 __device__ __forceinline__ int64_t prefill_items_of(const PrefillArgs& a, int64_t r) {
   const int q_len = (int)(a.cu_seqlens[r + 1] - a.cu_seqlens[r]);
-  const int ctx = a.context_lens[r];
-  const int tpt = a.tokens_per_tile;
-  const int nqt = (q_len + tpt - 1) / tpt;
-  int64_t n = 0;
-  for (int qt = 0; qt < nqt; ++qt) n += cdiv((int64_t)prefill_key_tiles(ctx, q_len, tpt, qt), (int64_t)a.tiles_per_split);
-  return n;
+  return prefill_items_of_len(q_len, a.context_lens[r], a.tokens_per_tile, a.tiles_per_split);
+}
+
+// The request of work item `item` (wave-uniform): like locate_item over
+// prefill_items_of, but each lane keeps its request's lengths from the scan,
+// so the found request's query start, length and context come out of the
+// lanes instead of another round trip to memory.
+struct PrefillItem {
+  int64_t r;        // request, -1 past the last item
+  int64_t local;    // item index within the request
+  int64_t first;    // the request's first item
+  int64_t q_begin;  // the request's first packed query row
+  int q_len;
+  int ctx;
+};
+
+__device__ __forceinline__ PrefillItem prefill_locate(const PrefillArgs& a, int64_t item) {
+  const int lane = lane_id();
+  PrefillItem it;
+  int64_t base = 0;
+  for (int64_t b0 = 0; b0 < a.num_seqs; b0 += kWave) {
+    const int64_t b = b0 + lane;
+    int64_t qb = 0;
+    int qn = 0, cx = 0;
+    int64_t n = 0;
+    if (b < a.num_seqs) {
+      qb = a.cu_seqlens[b];
+      qn = (int)(a.cu_seqlens[b + 1] - qb);
+      cx = a.context_lens[b];
+      n = prefill_items_of_len(qn, cx, a.tokens_per_tile, a.tiles_per_split);
+    }
+    int64_t incl = n;  // inclusive prefix sum over the wave
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int64_t up = __shfl_up(incl, off);
+      if (lane >= off) incl += up;
+    }
+    const int64_t excl = incl - n;
+    const int64_t total = __shfl(incl, kWave - 1);
+    if (item < base + total) {
+      const bool mine = (b < a.num_seqs) && (item >= base + excl) && (item < base + incl);
+      const int src = __builtin_ctzll(__ballot(mine));
+      it.r = (int64_t)__builtin_amdgcn_readfirstlane((int)(b0 + src));
+      it.first = uniform64(base + __shfl(excl, src));
+      it.local = uniform64(item) - it.first;
+      it.q_begin = uniform64(__shfl(qb, src));
+      it.q_len = __builtin_amdgcn_readfirstlane(__shfl(qn, src));
+      it.ctx = __builtin_amdgcn_readfirstlane(__shfl(cx, src));
+      return it;
+    }
+    base += total;
+  }
+  it.r = -1;
+  it.local = it.first = it.q_begin = 0;
+  it.q_len = it.ctx = 0;
+  return it;
 }
 
 // Key steps of kPrefillStepTiles 16-key tiles (64 keys) stream through an LDS
@@ -1313,17 +1381,21 @@ __device__ __forceinline__ bf16x8_t join_bf16x4(v4s a, v4s b) {
 }
 
 // Online softmax over one key step: s[nb][t] holds the scores of sub-tile t
-// for row block nb (-inf where masked); the probabilities are
-// exp2((s - m) * c) with m the running maximum of s and c = log2(e) times
-// the factor still to be applied to s (1, or the power-of-two softmax
-// scale when it has been kept out of s).  s is overwritten with them.  The
-// maximum over the step's keys needs one cross-lane reduction per row
-// block; the rescale of O is skipped (exactly: alpha would be 1) unless
-// some row's maximum moved.
+// for row block nb (-inf where masked); they are overwritten with the
+// unnormalised probabilities exp2((s - m) * c), where c = log2(e) times the
+// factor still to be applied to s (1, or the power-of-two softmax scale when
+// it has been kept out of s), and m is the row's reference maximum.  The
+// reference maximum is raised (rescaling O and the denominator) only when
+// some row of the wave has a score more than kRescaleLog2 above it (in
+// log2 units) or had no reference yet; otherwise the probabilities of the
+// step are at most 2^kRescaleLog2, which fp32 sums and bf16 operands hold
+// exactly as well as values below 1.  O / denominator is the same either way.
+constexpr float kRescaleLog2 = 8.f;
+
 template <int D, int kBlocks, int kSub>
 __device__ __forceinline__ void softmax_step(SoftmaxState<D> (&st)[kBlocks], v4f (&s)[kBlocks][kSub], float c) {
-  float m_new[kBlocks], nref[kBlocks], tsum[kBlocks];
-  bool moved = false;
+  float m_new[kBlocks];
+  bool grow = false;
 #pragma unroll
   for (int nb = 0; nb < kBlocks; ++nb) {
     float tm[kSub];
@@ -1334,16 +1406,30 @@ __device__ __forceinline__ void softmax_step(SoftmaxState<D> (&st)[kBlocks], v4f
 #pragma unroll
       for (int t = 0; t + w < kSub; t += 2 * w) tm[t] = fmaxf(tm[t], tm[t + w]);
     }
-    const float tmax = max_over_groups(tm[0]);
-    m_new[nb] = fmaxf(st[nb].m, tmax);
+    m_new[nb] = fmaxf(st[nb].m, max_over_groups(tm[0]));
+    grow |= m_new[nb] != kNegInf && (st[nb].m == kNegInf || (m_new[nb] - st[nb].m) * c > kRescaleLog2);
+  }
+  if (__ballot(grow)) {
+#pragma unroll
+    for (int nb = 0; nb < kBlocks; ++nb) {
+      // alpha = 0 for a row without a reference yet (its O and sum are 0)
+      const float alpha = st[nb].m == kNegInf ? 0.f : fast_exp2((st[nb].m - m_new[nb]) * c);
+      st[nb].lsum *= alpha;
+#pragma unroll
+      for (int d = 0; d < D / 16; ++d) st[nb].o[d] *= alpha;
+      st[nb].m = m_new[nb];
+    }
+  }
+#pragma unroll
+  for (int nb = 0; nb < kBlocks; ++nb) {
     // A row with nothing unmasked so far keeps m = -inf; 0 as the reference
     // point makes its exponentials exact zeros, not NaN.
-    nref[nb] = (m_new[nb] == kNegInf) ? 0.f : -m_new[nb] * c;
+    const float nref = (st[nb].m == kNegInf) ? 0.f : -st[nb].m * c;
     float ps[kSub];
 #pragma unroll
     for (int t = 0; t < kSub; ++t) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[nb][t][i] = fast_exp2(fmaf(s[nb][t][i], c, nref[nb]));
+      for (int i = 0; i < 4; ++i) s[nb][t][i] = fast_exp2(fmaf(s[nb][t][i], c, nref));
       ps[t] = (s[nb][t][0] + s[nb][t][1]) + (s[nb][t][2] + s[nb][t][3]);
     }
 #pragma unroll
@@ -1351,23 +1437,8 @@ __device__ __forceinline__ void softmax_step(SoftmaxState<D> (&st)[kBlocks], v4f
 #pragma unroll
       for (int t = 0; t + w < kSub; t += 2 * w) ps[t] += ps[t + w];
     }
-    tsum[nb] = ps[0];
-    moved |= m_new[nb] != st[nb].m;
+    st[nb].lsum += ps[0];
   }
-  if (__ballot(moved)) {
-#pragma unroll
-    for (int nb = 0; nb < kBlocks; ++nb) {
-      const float alpha = fast_exp2(fmaf(st[nb].m, c, nref[nb]));
-      st[nb].lsum = st[nb].lsum * alpha + tsum[nb];
-#pragma unroll
-      for (int d = 0; d < D / 16; ++d) st[nb].o[d] *= alpha;
-    }
-  } else {
-#pragma unroll
-    for (int nb = 0; nb < kBlocks; ++nb) st[nb].lsum += tsum[nb];
-  }
-#pragma unroll
-  for (int nb = 0; nb < kBlocks; ++nb) st[nb].m = m_new[nb];
 }
 
 // LDS reads of the ring whose results are waited for together (see
@@ -1431,14 +1502,13 @@ void varlen_prefill_kernel(PrefillArgs a) {
   const int tpt = a.tokens_per_tile;
   const int S = a.tiles_per_split;
 
-  int64_t r, local, first_r, count_r;
-  locate_item((int64_t)blockIdx.x, a.num_seqs, [&](int64_t q) { return prefill_items_of(a, q); }, &r, &local,
-              &first_r, &count_r);
-  if (r < 0) return;  // uniform over the workgroup
+  const PrefillItem pit = prefill_locate(a, (int64_t)blockIdx.x);
+  if (pit.r < 0) return;  // uniform over the workgroup
+  const int64_t r = pit.r, local = pit.local, first_r = pit.first;
   const int h = (int)blockIdx.y;
-  const int64_t q_begin = a.cu_seqlens[r];
-  const int q_len = (int)(a.cu_seqlens[r + 1] - q_begin);
-  const int ctx = a.context_lens[r];
+  const int64_t q_begin = pit.q_begin;
+  const int q_len = pit.q_len;
+  const int ctx = pit.ctx;
   // (query tile, split) of this item; the loop is wave-uniform
   int qt = 0, split = (int)local, nsplit = 0;
   for (;;) {
@@ -1498,6 +1568,17 @@ void varlen_prefill_kernel(PrefillArgs a) {
   // the item's last key are redirected to the tile that holds it, and rows
   // past it to it (no lane reads a slot the sequence does not own; those
   // keys are masked to p = 0).
+  // Per-lane element offsets of this wave's ops inside a tile (the same for
+  // every tile): the lane's row and its swizzled 16-byte chunk.
+  int op_row[kOwnOps], op_row_off[kOwnOps], op_chunk_off[kOwnOps];
+#pragma unroll
+  for (int i = 0; i < kOwnOps; ++i) {
+    const int kop = ((wave + i * kPrefillWaves) % (2 * GT::kOps)) % GT::kOps;
+    const int rr = kop * GT::kRowsPerOp + lane / GT::kChunks;
+    op_row[i] = rr;
+    op_row_off[i] = rr * a.geom.row_elems32;
+    op_chunk_off[i] = ((lane % GT::kChunks) ^ GT::swz(rr)) * kEltPerChunk;
+  }
   auto issue = [&](int slot, int key0) {
     unsigned char* base = &ring[slot][0];
 #pragma unroll
@@ -1505,14 +1586,23 @@ void varlen_prefill_kernel(PrefillArgs a) {
       const int op = wave + i * kPrefillWaves;
       const int t = op / (2 * GT::kOps);
       const int within = op % (2 * GT::kOps);
-      const int kop = within % GT::kOps;
       const int tkey0 = min(key0 + t * kTileKeys, last_key0);
-      TileAddr<kUniform, false> ta;  // an item covers <= 64 tiles, so <= 64 blocks
-      ta.init(a.geom, table, tlen, tc, tkey0);
-      const int rr = kop * GT::kRowsPerOp + lane / GT::kChunks;
-      const int chunk = (lane % GT::kChunks) ^ GT::swz(rr);
-      const int64_t src = ta.at(a.geom, table, tlen, tkey0, min(rr, last - tkey0)) + chunk * kEltPerChunk;
-      lds_dma16((within < GT::kOps ? kc : vc) + src, base + op * kWave * 16);
+      const T* src_base = within < GT::kOps ? kc : vc;
+      if constexpr (kUniform) {
+        // the tile lies in one block: one wave-uniform table lookup, then the
+        // lane's row (clamped to the item's last key) and chunk
+        const int lb = min(tkey0 >> a.geom.bs_shift, tlen - 1);
+        int phys = tc.template lookup<false>(table, tlen, lb);
+        phys = phys < 0 ? 0 : (phys >= a.geom.num_blocks ? a.geom.num_blocks - 1 : phys);
+        const int64_t tile = a.geom.layer_offset +
+                             ((int64_t)phys * a.geom.block_size + (tkey0 & (a.geom.block_size - 1))) *
+                                 a.geom.row_elems;
+        const int off = min(op_row_off[i], (last - tkey0) * a.geom.row_elems32) + op_chunk_off[i];
+        lds_dma16(src_base + tile + off, base + op * kWave * 16);
+      } else {
+        const int64_t src = token_offset(a.geom, table, tlen, tkey0 + min(op_row[i], last - tkey0)) + op_chunk_off[i];
+        lds_dma16(src_base + src, base + op * kWave * 16);
+      }
     }
   };
 
@@ -1601,9 +1691,11 @@ void varlen_prefill_kernel(PrefillArgs a) {
     for (int nb = 0; nb < kRowBlocks; ++nb) {
 #pragma unroll
       for (int t = 0; t < kSub; ++t) {
+        if constexpr (kPow2Scale) {
+          p[nb][t] = round_bf16x4(p[nb][t]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[nb][t][i] = kPow2Scale ? round_storage<T>(p[nb][t][i]) : scaled_score<T>(p[nb][t][i], a.scale);
+          for (int i = 0; i < 4; ++i) p[nb][t][i] = scaled_score<T>(p[nb][t][i], a.scale);
         }
       }
     }
@@ -1709,16 +1801,15 @@ void varlen_prefill_kernel(PrefillArgs a) {
   }
 }
 
-// Merge of split prefill rows: one workgroup per query tile (and KV head)
-// that has several splits, one wave per block of 16 of its rows.  Lane l
-// takes 4-dim chunk l%16 (and l%16 + 16, ... for larger head_dim) of rows
-// l/16 + 4i, and walks the splits in batches whose loads are all issued
-// before any is used, combining batches through a running maximum per row
+// Merge of split prefill rows: a workgroup takes 32 rows (blockIdx.z) of a
+// query tile (blockIdx.x) with several splits, for one KV head (blockIdx.y);
+// wave w takes 4 of those rows, lane l the 4-dim chunk l%16 (and l%16 + 16,
+// ... for larger head_dim) of row l/16.  Every split's loads of a batch of
+// up to kBatch splits are issued before any is used, so the usual merge is
+// one memory round trip; batches combine through a running maximum per row
 // (exact log-sum-exp weights, splits in order).
-template <int kRowBlocks>
-constexpr int prefill_merge_waves() {
-  return prefill_rows_per_item<kRowBlocks>() / 16;
-}
+constexpr int kPrefillMergeWaves = 8;
+constexpr int kPrefillMergeRows = kPrefillMergeWaves * 4;
 
 // Sum of prefill_items_of over the sequences before r (wave-uniform).
 __device__ __forceinline__ int64_t prefill_items_before(const PrefillArgs& a, int64_t r) {
@@ -1730,11 +1821,10 @@ __device__ __forceinline__ int64_t prefill_items_before(const PrefillArgs& a, in
 }
 
 template <typename T, int D, int kRowBlocks>
-__global__ __launch_bounds__(prefill_merge_waves<kRowBlocks>() * kWave) void prefill_merge_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a) {
   constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
-  constexpr int kChunkPasses = D / 64;  // 4-dim chunks per lane and row
-  constexpr int kRowsPerLane = 4;
-  constexpr int kBatch = 4;
+  constexpr int kChunkPasses = D / 64;  // 4-dim chunks per lane
+  constexpr int kBatch = 64 / (3 * kChunkPasses);  // splits per round trip (register budget)
   const int tpt = a.tokens_per_tile;
   const int S = a.tiles_per_split;
   int64_t r, qt64, first_q, count_q;
@@ -1755,81 +1845,65 @@ __global__ __launch_bounds__(prefill_merge_waves<kRowBlocks>() * kWave) void pre
   const int lane = lane_id();
   const int wave = (int)(threadIdx.x / kWave);
   const int chunk = lane & 15;
+  const int rr = (int)blockIdx.z * kPrefillMergeRows + wave * 4 + (lane >> 4);  // row within the item
   const int tpb = 16 / a.group;
-  const int t0 = qt * tpt;
-  const int t_end = min(t0 + tpt, q_len);
+  const int tq = qt * tpt + (rr / 16) * tpb + (rr % 16) / a.group;
+  const int t_end = min(qt * tpt + tpt, q_len);
   const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;  // rows between consecutive items
-  const int64_t slot0 = (first * a.geom.kv_heads + h) * kRows + wave * 16;
+  const int64_t slot0 = (first * a.geom.kv_heads + h) * kRows + rr;
 
-  float run_max[kRowsPerLane], denom[kRowsPerLane];
-  float4 acc[kRowsPerLane][kChunkPasses];
+  float run_max = kNegInf, denom = 0.f;
+  float4 acc[kChunkPasses];
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) {
-    run_max[i] = kNegInf;
-    denom[i] = 0.f;
-#pragma unroll
-    for (int c = 0; c < kChunkPasses; ++c) acc[i][c] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int c = 0; c < kChunkPasses; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
-    float4 v[kBatch][kRowsPerLane][kChunkPasses];
-    float2 ml[kBatch][kRowsPerLane];
+    float4 v[kBatch][kChunkPasses];
+    float2 ml[kBatch];
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       const bool in = s0 + b < nsplit;
-#pragma unroll
-      for (int i = 0; i < kRowsPerLane; ++i) {
-        const int64_t slot = slot0 + (s0 + b) * split_stride + (lane >> 4) + 4 * i;
-        ml[b][i] = in ? *reinterpret_cast<const float2*>(a.ws_ml + slot * 2) : make_float2(kNegInf, 0.f);
-#pragma unroll
-        for (int c = 0; c < kChunkPasses; ++c) {
-          v[b][i][c] = in ? *reinterpret_cast<const float4*>(a.ws_o + slot * D + 4 * (chunk + 16 * c))
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kRowsPerLane; ++i) {
-      float bmax = ml[0][i].x;
-#pragma unroll
-      for (int b = 1; b < kBatch; ++b) bmax = fmaxf(bmax, ml[b][i].x);
-      const float new_max = fmaxf(run_max[i], bmax);
-      const float keep = run_max[i] == kNegInf ? 0.f : exp2f((run_max[i] - new_max) * kLog2e);
-      denom[i] *= keep;
+      const int64_t slot = slot0 + (s0 + b) * split_stride;
+      ml[b] = in ? *reinterpret_cast<const float2*>(a.ws_ml + slot * 2) : make_float2(kNegInf, 0.f);
 #pragma unroll
       for (int c = 0; c < kChunkPasses; ++c) {
-        acc[i][c].x *= keep;
-        acc[i][c].y *= keep;
-        acc[i][c].z *= keep;
-        acc[i][c].w *= keep;
+        v[b][c] = in ? *reinterpret_cast<const float4*>(a.ws_o + slot * D + 4 * (chunk + 16 * c))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        const float w = ml[b][i].x == kNegInf ? 0.f : exp2f((ml[b][i].x - new_max) * kLog2e);
-        denom[i] += w * ml[b][i].y;
-#pragma unroll
-        for (int c = 0; c < kChunkPasses; ++c) {
-          acc[i][c].x += w * v[b][i][c].x;
-          acc[i][c].y += w * v[b][i][c].y;
-          acc[i][c].z += w * v[b][i][c].z;
-          acc[i][c].w += w * v[b][i][c].w;
-        }
-      }
-      run_max[i] = new_max;
     }
-  }
+    float bmax = ml[0].x;
 #pragma unroll
-  for (int i = 0; i < kRowsPerLane; ++i) {
-    const int rr = (lane >> 4) + 4 * i;  // row within the wave's block
-    const int tq = t0 + (wave * tpb) + rr / a.group;
-    if (tq >= t_end) continue;
-    const int qh = h * a.group + rr % a.group;
-    const float inv = 1.f / denom[i];
-    T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh;
+    for (int b = 1; b < kBatch; ++b) bmax = fmaxf(bmax, ml[b].x);
+    const float new_max = fmaxf(run_max, bmax);
+    const float keep = run_max == kNegInf ? 0.f : exp2f((run_max - new_max) * kLog2e);
+    denom *= keep;
 #pragma unroll
     for (int c = 0; c < kChunkPasses; ++c) {
-      store4<T>(dst + 4 * (chunk + 16 * c), acc[i][c].x * inv, acc[i][c].y * inv, acc[i][c].z * inv,
-                acc[i][c].w * inv);
+      acc[c].x *= keep;
+      acc[c].y *= keep;
+      acc[c].z *= keep;
+      acc[c].w *= keep;
     }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const float w = ml[b].x == kNegInf ? 0.f : exp2f((ml[b].x - new_max) * kLog2e);
+      denom += w * ml[b].y;
+#pragma unroll
+      for (int c = 0; c < kChunkPasses; ++c) {
+        acc[c].x += w * v[b][c].x;
+        acc[c].y += w * v[b][c].y;
+        acc[c].z += w * v[b][c].z;
+        acc[c].w += w * v[b][c].w;
+      }
+    }
+    run_max = new_max;
+  }
+  if (rr >= kRows || tq >= t_end) return;
+  const int qh = h * a.group + (rr % 16) % a.group;
+  const float inv = 1.f / denom;
+  T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh;
+#pragma unroll
+  for (int c = 0; c < kChunkPasses; ++c) {
+    store4<T>(dst + 4 * (chunk + 16 * c), acc[c].x * inv, acc[c].y * inv, acc[c].z * inv, acc[c].w * inv);
   }
 }
 
@@ -1852,10 +1926,10 @@ struct PrefillPlan {
   bool split = false;  // some query tile is split over several items
 };
 
-// Workgroups of the prefill kernel resident at once (two per CU at head_dim
-// 64): with host metadata the split length is chosen so the call's items
-// fill them about once.
-constexpr int64_t kPrefillSlots = 2 * kDecodeCUs;
+// Workgroups a prefill call aims for with host metadata: the split length is
+// chosen so the items fill the GPU about once (two workgroups fit a CU at
+// head_dim 64; 1.5 per CU measured fastest on the mixed chunked-prefill step).
+constexpr int64_t kPrefillSlots = 3 * kDecodeCUs / 2;
 
 // Key tiles visible to query tile qt of a request with n query tokens after
 // ctx cached ones (host side of prefill_key_tiles).
@@ -2128,9 +2202,9 @@ void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, int64_t total
     launch_prefill_kernel<T, D, NB, false>(a, p, stream);
   }
   if (merge) {
-    const dim3 grid((unsigned)p.qtiles, (unsigned)a.geom.kv_heads);
-    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(prefill_merge_waves<NB>() * kWave), 0, stream,
-                       a);
+    const dim3 grid((unsigned)p.qtiles, (unsigned)a.geom.kv_heads,
+                    (unsigned)(prefill_rows_per_item<NB>() / kPrefillMergeRows));
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(kPrefillMergeWaves * kWave), 0, stream, a);
   }
 }
 
