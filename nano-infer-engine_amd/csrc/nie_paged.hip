@@ -1802,7 +1802,8 @@ void varlen_prefill_kernel(PrefillArgs a) {
 }
 
 // Merge of split prefill rows: a workgroup takes 32 rows (blockIdx.z) of a
-// query tile (blockIdx.x) with several splits, for one KV head (blockIdx.y);
+// split query tile (blockIdx.x: merge job j, or without jobs the x-th query
+// tile of the call, located on the device), for one KV head (blockIdx.y);
 // wave w takes 4 of those rows, lane l the 4-dim chunk l%16 (and l%16 + 16,
 // ... for larger head_dim) of row l/16.  Every split's loads of a batch of
 // up to kBatch splits are issued before any is used, so the usual merge is
@@ -1820,35 +1821,59 @@ __device__ __forceinline__ int64_t prefill_items_before(const PrefillArgs& a, in
   return uniform64(n);
 }
 
+// The split query tiles of a call, listed on the host from its exact plan
+// and passed by value as a kernel argument: job j = {first item, first
+// packed query row, split count, token count} of the j-th split tile.
+constexpr int kMaxMergeJobs = 128;
+
+struct PrefillMergeJobs {
+  int32_t count;  // 0: locate the tiles on the device instead
+  int32_t first_item[kMaxMergeJobs];
+  int32_t row0[kMaxMergeJobs];
+  int32_t nsplit_tokens[kMaxMergeJobs];  // nsplit << 16 | tokens
+};
+
 template <typename T, int D, int kRowBlocks>
-__global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a,
+                                                                                 PrefillMergeJobs jobs) {
   constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
   constexpr int kChunkPasses = D / 64;  // 4-dim chunks per lane
   constexpr int kBatch = 64 / (3 * kChunkPasses);  // splits per round trip (register budget)
   const int tpt = a.tokens_per_tile;
-  const int S = a.tiles_per_split;
-  int64_t r, qt64, first_q, count_q;
-  locate_item((int64_t)blockIdx.x, a.num_seqs,
-              [&](int64_t b) { return (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + tpt - 1) / tpt; }, &r, &qt64,
-              &first_q, &count_q);
-  if (r < 0) return;  // uniform over the workgroup
-  const int qt = (int)qt64;
   const int h = (int)blockIdx.y;
-  const int64_t q_begin = a.cu_seqlens[r];
-  const int q_len = (int)(a.cu_seqlens[r + 1] - q_begin);
-  const int ctx = a.context_lens[r];
-  const int nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
-  if (nsplit <= 1) return;  // the prefill kernel wrote these rows
-  int64_t first = prefill_items_before(a, r);  // the tile's first item
-  for (int k = 0; k < qt; ++k) first += (prefill_key_tiles(ctx, q_len, tpt, k) + S - 1) / S;
+  int64_t first, row0;
+  int nsplit, tokens;
+  if (jobs.count > 0) {
+    const int j = (int)blockIdx.x;
+    first = jobs.first_item[j];
+    row0 = jobs.row0[j];
+    nsplit = jobs.nsplit_tokens[j] >> 16;
+    tokens = jobs.nsplit_tokens[j] & 0xffff;
+  } else {
+    const int S = a.tiles_per_split;
+    int64_t r, qt64, first_q, count_q;
+    locate_item((int64_t)blockIdx.x, a.num_seqs,
+                [&](int64_t b) { return (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + tpt - 1) / tpt; }, &r, &qt64,
+                &first_q, &count_q);
+    if (r < 0) return;  // uniform over the workgroup
+    const int qt = (int)qt64;
+    const int64_t q_begin = a.cu_seqlens[r];
+    const int q_len = (int)(a.cu_seqlens[r + 1] - q_begin);
+    const int ctx = a.context_lens[r];
+    nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
+    if (nsplit <= 1) return;  // the prefill kernel wrote these rows
+    first = prefill_items_before(a, r);  // the tile's first item
+    for (int k = 0; k < qt; ++k) first += (prefill_key_tiles(ctx, q_len, tpt, k) + S - 1) / S;
+    row0 = q_begin + qt * tpt;
+    tokens = min(tpt, q_len - qt * tpt);
+  }
   if (first + nsplit > a.ws_items) return;
   const int lane = lane_id();
   const int wave = (int)(threadIdx.x / kWave);
   const int chunk = lane & 15;
   const int rr = (int)blockIdx.z * kPrefillMergeRows + wave * 4 + (lane >> 4);  // row within the item
   const int tpb = 16 / a.group;
-  const int tq = qt * tpt + (rr / 16) * tpb + (rr % 16) / a.group;
-  const int t_end = min(qt * tpt + tpt, q_len);
+  const int tq = (rr / 16) * tpb + (rr % 16) / a.group;  // token within the tile
   const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;  // rows between consecutive items
   const int64_t slot0 = (first * a.geom.kv_heads + h) * kRows + rr;
 
@@ -1897,10 +1922,10 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
     }
     run_max = new_max;
   }
-  if (rr >= kRows || tq >= t_end) return;
+  if (rr >= kRows || tq >= tokens) return;
   const int qh = h * a.group + (rr % 16) % a.group;
   const float inv = 1.f / denom;
-  T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh;
+  T* dst = reinterpret_cast<T*>(a.out) + (row0 + tq) * a.o_st + qh * a.o_sh;
 #pragma unroll
   for (int c = 0; c < kChunkPasses; ++c) {
     store4<T>(dst + 4 * (chunk + 16 * c), acc[c].x * inv, acc[c].y * inv, acc[c].z * inv, acc[c].w * inv);
@@ -1915,6 +1940,10 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
 constexpr int64_t kPrefillTargetItems = 2048;
 constexpr int64_t kPrefillMinTilesPerSplit = 8;
 constexpr int64_t kPrefillMaxTilesPerSplit = 64;
+
+struct PrefillPlan;
+void fill_merge_jobs(const PrefillPlan& p, int64_t num_seqs, const int64_t* host_cu, const int32_t* host_ctx,
+                     PrefillMergeJobs* jobs);
 
 struct PrefillPlan {
   int row_blocks = 2;  // MFMA row blocks per wave
@@ -1986,6 +2015,36 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
   p.qtiles = qtiles;
   p.split = ktiles > p.tps;
   return p;
+}
+
+// The split query tiles of a host-planned call as merge jobs (count 0 when
+// there are more than kMaxMergeJobs: the merge then locates them itself).
+void fill_merge_jobs(const PrefillPlan& p, int64_t num_seqs, const int64_t* host_cu, const int32_t* host_ctx,
+                     PrefillMergeJobs* jobs) {
+  jobs->count = 0;
+  if (host_cu == nullptr || host_ctx == nullptr) return;
+  const int64_t tpt = p.tokens_per_tile;
+  int64_t item = 0;
+  int n = 0;
+  for (int64_t r = 0; r < num_seqs; ++r) {
+    const int64_t len = host_cu[r + 1] - host_cu[r];
+    for (int64_t qt = 0; qt < cdiv(len, tpt); ++qt) {
+      const int64_t nsplit = cdiv(host_key_tiles(host_ctx[r], len, tpt, qt), p.tps);
+      if (nsplit > 1) {
+        if (n == kMaxMergeJobs || item > 0x7fffffffLL || host_cu[r] + qt * tpt > 0x7fffffffLL || nsplit > 0x7fff) {
+          jobs->count = 0;
+          return;
+        }
+        jobs->first_item[n] = (int32_t)item;
+        jobs->row0[n] = (int32_t)(host_cu[r] + qt * tpt);
+        const int64_t tokens = len - qt * tpt < tpt ? len - qt * tpt : tpt;
+        jobs->nsplit_tokens[n] = (int32_t)((nsplit << 16) | tokens);
+        ++n;
+      }
+      item += nsplit;
+    }
+  }
+  jobs->count = n;
 }
 
 // Checks host copies of cu_seqlens / context_lens against the call's sizes.
@@ -2193,7 +2252,7 @@ bool is_pow2_scale(float scale) {
 }
 
 template <typename T, int D, int NB>
-void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, int64_t total_tokens, hipStream_t stream,
+void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const PrefillMergeJobs& jobs, hipStream_t stream,
                        bool merge) {
   if constexpr (Elt<T>::kIsBf16) {
     if (is_pow2_scale(a.scale)) launch_prefill_kernel<T, D, NB, true>(a, p, stream);
@@ -2202,17 +2261,17 @@ void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, int64_t total
     launch_prefill_kernel<T, D, NB, false>(a, p, stream);
   }
   if (merge) {
-    const dim3 grid((unsigned)p.qtiles, (unsigned)a.geom.kv_heads,
-                    (unsigned)(prefill_rows_per_item<NB>() / kPrefillMergeRows));
-    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(kPrefillMergeWaves * kWave), 0, stream, a);
+    const unsigned tiles = (unsigned)(jobs.count > 0 ? jobs.count : p.qtiles);
+    const dim3 grid(tiles, (unsigned)a.geom.kv_heads, (unsigned)(prefill_rows_per_item<NB>() / kPrefillMergeRows));
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(kPrefillMergeWaves * kWave), 0, stream, a, jobs);
   }
 }
 
 template <typename T, int D>
-void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, int64_t total_tokens, hipStream_t stream,
+void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, const PrefillMergeJobs& jobs, hipStream_t stream,
                     bool merge) {
-  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, total_tokens, stream, merge);
-  else launch_prefill_nb<T, D, 2>(a, p, total_tokens, stream, merge);
+  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, jobs, stream, merge);
+  else launch_prefill_nb<T, D, 2>(a, p, jobs, stream, merge);
 }
 
 int check_aligned(const void* p, int64_t stride_a, int64_t stride_b, int64_t es) {
@@ -2583,13 +2642,16 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + plan.items * kv_heads * plan.rows * head_dim : nullptr;
   a.ws_items = have_ws ? plan.items : 0;
+  PrefillMergeJobs jobs;
+  jobs.count = 0;
+  if (may_split) fill_merge_jobs(plan, num_seqs, host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr, &jobs);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, total_query_tokens, s, may_split);
-    else launch_prefill<bf16_t, 128>(a, plan, total_query_tokens, s, may_split);
+    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, jobs, s, may_split);
+    else launch_prefill<bf16_t, 128>(a, plan, jobs, s, may_split);
   } else {
-    if (head_dim == 64) launch_prefill<float, 64>(a, plan, total_query_tokens, s, may_split);
-    else launch_prefill<float, 128>(a, plan, total_query_tokens, s, may_split);
+    if (head_dim == 64) launch_prefill<float, 64>(a, plan, jobs, s, may_split);
+    else launch_prefill<float, 128>(a, plan, jobs, s, may_split);
   }
   return launched("varlen_prefill");
 }
