@@ -247,31 +247,37 @@ __device__ __forceinline__ int64_t token_offset(const CacheGeom& g, const int32_
   return g.layer_offset + ((int64_t)phys * g.block_size + off) * g.row_elems;
 }
 
-// Caches 64 consecutive block-table entries of one sequence in a VGPR
-// (entry base+i in lane i), so the per-tile physical-block lookup is a
-// v_readlane instead of a memory load whose wait would also drain the
-// prefetched K/V loads.
+// Caches kTableWindow consecutive block-table entries of one sequence in
+// two VGPRs (entry base+i in lane i of the first, base+64+i of the second),
+// so the per-tile physical-block lookup is a v_readlane instead of a memory
+// load whose wait would also drain the prefetched K/V loads.
+constexpr int kTableWindow = 2 * kWave;
+
 struct TableCache {
-  int base;     // first cached logical block (wave-uniform)
-  int entries;  // lane i: table[base + i], 0 past the end of the table row
+  int base;        // first cached logical block (wave-uniform)
+  int entries[2];  // lane i: table[base + i], table[base + 64 + i]; 0 past the end of the table row
 
   __device__ __forceinline__ void load(const int32_t* table, int table_len, int first) {
     base = __builtin_amdgcn_readfirstlane(first);
     const int i = base + lane_id();
-    entries = i < table_len ? table[i] : 0;
+    entries[0] = i < table_len ? table[i] : 0;
+    entries[1] = i + kWave < table_len ? table[i + kWave] : 0;
   }
   // Physical block of logical block `lb` (wave-uniform).  With kRefill the
   // window moves when `lb` leaves it; without, the caller guarantees
-  // base <= lb < base + 64 (no load inside the caller's loop, so the
-  // compiler can keep counting that loop's outstanding K/V loads exactly).
+  // base <= lb < base + kTableWindow (no load inside the caller's loop, so
+  // the compiler can keep counting that loop's outstanding K/V loads exactly).
   template <bool kRefill>
   __device__ __forceinline__ int lookup(const int32_t* table, int table_len, int lb) {
     lb = __builtin_amdgcn_readfirstlane(lb);
     if constexpr (kRefill) {
-      if (lb < base || lb - base >= kWave) load(table, table_len, lb);
+      if (lb < base || lb - base >= kTableWindow) load(table, table_len, lb);
     }
-    const int idx = lb - base;
-    return __builtin_amdgcn_readlane(entries, idx < 0 ? 0 : (idx >= kWave ? kWave - 1 : idx));
+    int idx = lb - base;
+    idx = idx < 0 ? 0 : (idx >= kTableWindow ? kTableWindow - 1 : idx);
+    const int lo = __builtin_amdgcn_readlane(entries[0], idx & (kWave - 1));
+    const int hi = __builtin_amdgcn_readlane(entries[1], idx & (kWave - 1));
+    return idx < kWave ? lo : hi;
   }
 };
 
@@ -1048,7 +1054,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // last key (so no lane reads a slot the sequence does not own; those keys
   // are masked to p = 0).
   auto issue = [&](int slot, int key0) {
-    TileAddr<kUniform, false> ta;  // a split covers <= 64 tiles, so <= 64 blocks
+    TileAddr<kUniform, false> ta;  // a split covers <= kTableWindow tiles, so <= kTableWindow blocks
     ta.init(a.geom, table, tlen, tc, key0);
     const int lim = last - key0;
     unsigned char* kdst = &ring[slot][0];
@@ -1206,11 +1212,11 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
 // and the workgroups of a call run in rounds of (CUs x resident workgroups
 // per CU).  The planner takes the number of rounds r that minimises
 // r * (kDecodeFixedTiles + tiles per split), where tiles per split is the
-// smallest that fits the call into r rounds, within [4, 64] (64 = the
-// per-split block-table window, one VGPR per lane).
+// smallest that fits the call into r rounds, within [4, 128] (128 = the
+// per-split block-table window, two VGPRs per lane).
 constexpr int64_t kDecodeCUs = 256;  // MI355X
 constexpr int64_t kDecodeMinTilesPerSplit = 4;
-constexpr int64_t kDecodeMaxTilesPerSplit = 64;
+constexpr int64_t kDecodeMaxTilesPerSplit = kTableWindow;
 constexpr int64_t kDecodeFixedTiles = 4;
 constexpr int64_t kDecodeMaxRounds = 8;
 

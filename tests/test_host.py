@@ -279,8 +279,8 @@ def test_library_workspace_queries():
     assert small > 0 and small % (32 * 66 * 4) == 0
     big = lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600)
     assert big >= small
-    # at most 64 tiles of 16 keys per split: at least 16 * ceil(1850 / 64) items
-    assert big >= 16 * 29 * 32 * 66 * 4
+    # at most 128 tiles of 16 keys per split (the block-table window): at least 16 * ceil(1850 / 128) items
+    assert big >= 16 * 15 * 32 * 66 * 4
     assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1) == 0
     assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710) == 0  # bad dtype
     assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710) == 0  # head_dim 96
