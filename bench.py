@@ -119,7 +119,8 @@ class DecodeBench:
 
         append = _native.PreparedAppend(self.k_cache, self.v_cache, self.slots[s])
         decode = _native.PreparedDecode(self.k_cache, self.v_cache, self.tables, self.lens[s], self.max_len[s],
-                                        self.total_len[s], self.wl.q_heads, self.scale)
+                                        self.total_len[s], self.wl.q_heads, self.scale,
+                                        seq_lens_host=self.seq_lens_host[s])
         for layer in range(self.wl.num_layers):
             append(self.k_new, self.v_new, layer)
             if events is not None:
@@ -273,7 +274,7 @@ def run_mixed(args):
                                       max(wl.query_lens[:n_pref]), max(seq_lens[:n_pref]), wl.q_heads, scale,
                                       cu_seqlens_host=cu.cpu().tolist(), context_lens_host=wl.context_lens[:n_pref])
     decode = _native.PreparedDecode(kc, vc, tables[n_pref:].contiguous(), dec_lens, max(seq_lens[n_pref:]),
-                                    sum(seq_lens[n_pref:]), wl.q_heads, scale)
+                                    sum(seq_lens[n_pref:]), wl.q_heads, scale, seq_lens_host=seq_lens[n_pref:])
     out = torch.empty_like(q)
     qp, op = q[:pref_tokens], out[:pref_tokens]
     qd, od = q[pref_tokens:], out[pref_tokens:]

@@ -162,15 +162,17 @@ int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t cols, i
 /*
  * Workspace bytes needed by nie_paged_decode for a call with these
  * arguments (same meaning as there; host values), whose sequence lengths
- * have maximum max_seq_len and sum total_seq_len.  The split of the work
- * depends on all of them, so query with the values of the call.
+ * have maximum max_seq_len and sum total_seq_len, and the same optional
+ * host copy of the lengths as the call.  The split of the work depends on
+ * all of them, so query with the values of the call.
  * Layout: fp32 split partials (unnormalised O rows, then (max, sum) pairs).
  * The pointer must be 16-byte aligned.  Returns 0 for invalid arguments.
  */
 int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,
                                          int64_t kv_heads, int64_t head_dim,
                                          int64_t block_size, int64_t max_seq_len,
-                                         int64_t total_seq_len);
+                                         int64_t total_seq_len,
+                                         const int32_t* host_seq_lens);
 
 /*
  * Paged decode attention: one query token per sequence attends to the first
@@ -185,6 +187,12 @@ int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_hea
  *   seq_lens     : (batch,) int32 device copy of the lengths, each >= 1.
  *   max_seq_len / total_seq_len : host copies of max and sum of seq_lens;
  *           they size the launch and must be exact.
+ *   host_seq_lens : optional HOST copy of seq_lens (NULL: none).  With it the
+ *           launch is planned from the exact lengths (split length chosen so
+ *           the work fills the GPU's resident workgroups, every workgroup a
+ *           real work item), and the work items are passed to the kernels in
+ *           their arguments.  It must hold the same values as seq_lens;
+ *           NIE_EINVAL if it does not match max_seq_len / total_seq_len.
  * Long sequences are split over several workgroups whose fp32 partials a
  * second kernel, on the same stream, merges exactly (log-sum-exp weights).
  * Numerics follow the reference: the q.k score is rounded to the storage
@@ -208,6 +216,7 @@ int nie_paged_decode(int dtype,
                      float scale,
                      void* out, int64_t out_stride_b, int64_t out_stride_h,
                      void* workspace, int64_t workspace_bytes,
+                     const int32_t* host_seq_lens,
                      void* stream);
 
 /*

@@ -796,6 +796,20 @@ struct DecodeArgs {
   int64_t ws_items;  // partial slots in the workspace (0 when there is none)
 };
 
+// Work items of a decode call planned from host copies of the lengths,
+// passed by value as a kernel argument: item i = sequence << 16 | split, and
+// per sequence its length and first item.  count 0: the kernels locate
+// their work from the device lengths instead.
+constexpr int kMaxDecodeItems = 256;
+constexpr int kMaxDecodeSeqs = 128;
+
+struct DecodeItems {
+  int32_t count;
+  uint32_t item[kMaxDecodeItems];
+  int32_t seq_len[kMaxDecodeSeqs];
+  int32_t seq_first[kMaxDecodeSeqs];
+};
+
 __device__ __forceinline__ int64_t decode_splits_of(const DecodeArgs& a, int64_t b) {
   const int64_t len = a.seq_lens[b];
   return len > 0 ? cdiv(cdiv(len, kTileKeys), a.tiles_per_split) : (int64_t)0;
@@ -999,7 +1013,7 @@ constexpr int decode_stages() {
 // One workgroup = one (sequence, key split, head group); wave w handles KV
 // head group*kHeads + w and its GQA query heads.
 template <typename T, int D, bool kUniform, int kHeads>
-__global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs a, DecodeItems items) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, kHeads>;
   constexpr int kStages = decode_stages<T, D, kHeads>();
@@ -1014,13 +1028,24 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   const int row = lane & 15;
 
   int64_t b, split, first_item, nsplit;
-  locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s); },
-              &b, &split, &first_item, &nsplit);
-  if (b < 0) return;  // uniform over the workgroup
+  int seq_len;
+  if (items.count > 0) {
+    if ((int)blockIdx.x >= items.count) return;  // uniform over the workgroup
+    const uint32_t it = items.item[blockIdx.x];
+    b = it >> 16;
+    split = it & 0xffffu;
+    seq_len = items.seq_len[b];
+    first_item = items.seq_first[b];
+    nsplit = cdiv(cdiv((int64_t)seq_len, (int64_t)kTileKeys), (int64_t)a.tiles_per_split);
+  } else {
+    locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s); },
+                &b, &split, &first_item, &nsplit);
+    if (b < 0) return;  // uniform over the workgroup
+    seq_len = a.seq_lens[b];
+  }
   const int h0 = (int)blockIdx.y * kHeads;  // first KV head of the group
   const int h = h0 + wave;
 
-  const int seq_len = a.seq_lens[b];
   const int32_t* table = a.tables + b * a.table_stride;
   const int tlen = (int)a.table_stride;
   const int key_begin = (int)split * a.tiles_per_split * kTileKeys;
@@ -1190,16 +1215,21 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
 constexpr int kMergeWaves = 4;
 
 template <typename T, int D>
-__global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(DecodeArgs a, DecodeItems items) {
   const int64_t b = blockIdx.x;
   const int qh = (int)blockIdx.y * kMergeWaves + (int)(threadIdx.x / kWave);
   if (qh >= a.q_heads) return;
-  const int64_t nsplit = decode_splits_of(a, b);
-  if (nsplit <= 1) return;
-  int64_t first = 0;
-  for (int64_t s = lane_id(); s < b; s += kWave) first += decode_splits_of(a, s);
+  int64_t nsplit, first = 0;
+  if (items.count > 0) {
+    nsplit = cdiv(cdiv((int64_t)items.seq_len[b], (int64_t)kTileKeys), (int64_t)a.tiles_per_split);
+    first = items.seq_first[b];
+  } else {
+    nsplit = decode_splits_of(a, b);
+    for (int64_t s = lane_id(); s < b; s += kWave) first += decode_splits_of(a, s);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
+    for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
+  }
+  if (nsplit <= 1) return;
   if (first + nsplit > a.ws_items) return;
   merge_row<T, D>(a.ws_o + (first * a.q_heads + qh) * D, (int64_t)a.q_heads * D,
                   a.ws_ml + (first * a.q_heads + qh) * 2, (int64_t)a.q_heads * 2, (int)nsplit,
@@ -2176,19 +2206,20 @@ int decode_resident_u(int heads) {
 }
 
 template <typename T, int D, bool U, int H>
-void launch_decode_h(const DecodeArgs& a, int64_t items, hipStream_t stream) {
-  const dim3 grid((unsigned)items, (unsigned)(a.geom.kv_heads / H));
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a);
+void launch_decode_h(const DecodeArgs& a, const DecodeItems& items, int64_t grid_items, hipStream_t stream) {
+  const dim3 grid((unsigned)grid_items, (unsigned)(a.geom.kv_heads / H));
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a, items);
 }
 
 template <typename T, int D, bool U>
-void launch_decode_u(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+void launch_decode_u(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& items, hipStream_t stream) {
   constexpr int kMax = decode_max_heads<T, D>();
+  const int64_t n = items.count > 0 ? items.count : p.items;
   switch (p.heads) {
-    case 1: launch_decode_h<T, D, U, 1>(a, p.items, stream); break;
-    case 2: launch_decode_h<T, D, U, heads_clamp<kMax, 2>()>(a, p.items, stream); break;
-    case 4: launch_decode_h<T, D, U, heads_clamp<kMax, 4>()>(a, p.items, stream); break;
-    default: launch_decode_h<T, D, U, heads_clamp<kMax, 8>()>(a, p.items, stream); break;
+    case 1: launch_decode_h<T, D, U, 1>(a, items, n, stream); break;
+    case 2: launch_decode_h<T, D, U, heads_clamp<kMax, 2>()>(a, items, n, stream); break;
+    case 4: launch_decode_h<T, D, U, heads_clamp<kMax, 4>()>(a, items, n, stream); break;
+    default: launch_decode_h<T, D, U, heads_clamp<kMax, 8>()>(a, items, n, stream); break;
   }
 }
 
@@ -2220,24 +2251,91 @@ DecodePlan plan_decode_t(int64_t kv_heads, bool uniform, int64_t batch, int64_t 
   return p;
 }
 
-DecodePlan plan_decode(int dtype, int64_t head_dim, int64_t kv_heads, int64_t block_size, int64_t batch,
-                       int64_t total_seq_len) {
-  const bool uniform = block_size >= 16 && (block_size & (block_size - 1)) == 0;
-  if (dtype == NIE_DTYPE_BF16) {
-    return head_dim == 64 ? plan_decode_t<bf16_t, 64>(kv_heads, uniform, batch, total_seq_len)
-                          : plan_decode_t<bf16_t, 128>(kv_heads, uniform, batch, total_seq_len);
+// Work items of host lengths `lens` split into tiles_per_split-tile pieces.
+int64_t decode_items_exact(const int32_t* lens, int64_t batch, int64_t tps) {
+  int64_t n = 0;
+  for (int64_t b = 0; b < batch; ++b) n += cdiv(cdiv((int64_t)lens[b], (int64_t)kTileKeys), tps);
+  return n;
+}
+
+// The plan from host copies of the lengths: for each number of rounds r the
+// smallest split length whose exact item count fits r rounds (the item count
+// only falls as the split length grows), then the r with the lowest
+// r * (kDecodeFixedTiles + tiles per split), as in plan_decode_t.
+DecodePlan plan_decode_exact(DecodePlan p, int64_t kv_heads, const int32_t* lens, int64_t batch) {
+  const int64_t groups = kv_heads / p.heads;
+  const int64_t slots = (kDecodeCUs * p.resident) / groups > 0 ? (kDecodeCUs * p.resident) / groups : 1;
+  int64_t best = -1;
+  for (int64_t r = 1; r <= kDecodeMaxRounds; ++r) {
+    if (decode_items_exact(lens, batch, kDecodeMaxTilesPerSplit) > r * slots) continue;
+    int64_t lo = kDecodeMinTilesPerSplit, hi = kDecodeMaxTilesPerSplit;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      if (decode_items_exact(lens, batch, mid) <= r * slots) hi = mid;
+      else lo = mid + 1;
+    }
+    const int64_t cost = r * (kDecodeFixedTiles + lo);
+    if (best < 0 || cost < best) {
+      best = cost;
+      p.tps = lo;
+    }
   }
-  return head_dim == 64 ? plan_decode_t<float, 64>(kv_heads, uniform, batch, total_seq_len)
-                        : plan_decode_t<float, 128>(kv_heads, uniform, batch, total_seq_len);
+  const int64_t forced = decode_tiles_override();
+  if (forced > 0) p.tps = forced < kDecodeMaxTilesPerSplit ? forced : kDecodeMaxTilesPerSplit;
+  p.items = decode_items_exact(lens, batch, p.tps);
+  return p;
+}
+
+// host_lens: optional host copy of the lengths (validated by the caller).
+DecodePlan plan_decode(int dtype, int64_t head_dim, int64_t kv_heads, int64_t block_size, int64_t batch,
+                       int64_t total_seq_len, const int32_t* host_lens) {
+  const bool uniform = block_size >= 16 && (block_size & (block_size - 1)) == 0;
+  DecodePlan p;
+  if (dtype == NIE_DTYPE_BF16) {
+    p = head_dim == 64 ? plan_decode_t<bf16_t, 64>(kv_heads, uniform, batch, total_seq_len)
+                       : plan_decode_t<bf16_t, 128>(kv_heads, uniform, batch, total_seq_len);
+  } else {
+    p = head_dim == 64 ? plan_decode_t<float, 64>(kv_heads, uniform, batch, total_seq_len)
+                       : plan_decode_t<float, 128>(kv_heads, uniform, batch, total_seq_len);
+  }
+  return host_lens != nullptr ? plan_decode_exact(p, kv_heads, host_lens, batch) : p;
+}
+
+// The work-item table of a host-planned decode call (count 0 when the call
+// does not fit the table: the kernels then locate their work themselves).
+void fill_decode_items(const DecodePlan& p, const int32_t* host_lens, int64_t batch, DecodeItems* items) {
+  items->count = 0;
+  if (host_lens == nullptr || batch > kMaxDecodeSeqs || p.items > kMaxDecodeItems) return;
+  int64_t n = 0;
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t nsplit = cdiv(cdiv((int64_t)host_lens[b], (int64_t)kTileKeys), p.tps);
+    items->seq_len[b] = host_lens[b];
+    items->seq_first[b] = (int32_t)n;
+    for (int64_t k = 0; k < nsplit; ++k) items->item[n++] = (uint32_t)((b << 16) | k);
+  }
+  items->count = (int32_t)n;
+}
+
+// Host lengths that match the call: each in [1, max_seq_len], maximum
+// max_seq_len, sum total_seq_len.
+bool host_lens_ok(const int32_t* lens, int64_t batch, int64_t max_seq_len, int64_t total_seq_len) {
+  int64_t sum = 0, mx = 0;
+  for (int64_t b = 0; b < batch; ++b) {
+    if (lens[b] < 1 || lens[b] > max_seq_len) return false;
+    sum += lens[b];
+    mx = lens[b] > mx ? lens[b] : mx;
+  }
+  return sum == total_seq_len && mx == max_seq_len;
 }
 
 template <typename T, int D>
-void launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream, bool merge) {
-  if (uniform_tiles(a.geom)) launch_decode_u<T, D, true>(a, p, stream);
-  else launch_decode_u<T, D, false>(a, p, stream);
+void launch_decode(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& items, hipStream_t stream,
+                   bool merge) {
+  if (uniform_tiles(a.geom)) launch_decode_u<T, D, true>(a, p, items, stream);
+  else launch_decode_u<T, D, false>(a, p, items, stream);
   if (merge) {
     const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv((int64_t)a.q_heads, (int64_t)kMergeWaves));
-    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a);
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a, items);
   }
 }
 
@@ -2465,13 +2563,13 @@ NIE_API int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t
 NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,
                                                  int64_t kv_heads, int64_t head_dim,
                                                  int64_t block_size, int64_t max_seq_len,
-                                                 int64_t total_seq_len) {
-  (void)max_seq_len;
+                                                 int64_t total_seq_len, const int32_t* host_seq_lens) {
   if (check_dtype(dtype) != NIE_OK || batch <= 0 || q_heads <= 0 || total_seq_len <= 0 || block_size <= 0 ||
       check_attention_shape(q_heads, kv_heads, head_dim, 1, block_size) != NIE_OK) {
     return 0;
   }
-  const DecodePlan p = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len);
+  if (host_seq_lens != nullptr && !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) return 0;
+  const DecodePlan p = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
   return p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
@@ -2483,7 +2581,7 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
                              const int32_t* seq_lens, int64_t batch, int64_t max_seq_len,
                              int64_t total_seq_len, float scale, void* out,
                              int64_t out_stride_b, int64_t out_stride_h, void* workspace,
-                             int64_t workspace_bytes, void* stream) {
+                             int64_t workspace_bytes, const int32_t* host_seq_lens, void* stream) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -2508,7 +2606,10 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
       ((uintptr_t)k_cache % 16) || ((uintptr_t)v_cache % 16)) {
     return fail(NIE_EINVAL, "q/out/cache pointers and strides must be 16-byte aligned");
   }
-  const DecodePlan plan = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len);
+  if (host_seq_lens != nullptr && !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) {
+    return fail(NIE_EINVAL, "host seq_lens do not match max_seq_len / total_seq_len");
+  }
+  const DecodePlan plan = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
   const int64_t tps = plan.tps;
   const int64_t items = plan.items;
   const bool may_split = cdiv(max_seq_len, kTileKeys) > tps;
@@ -2542,13 +2643,15 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
   a.ws_items = have_ws ? items : 0;
   // The grid is an upper bound on the item count (exact to within `batch`);
   // workgroups past the last real item return immediately.
+  DecodeItems work;
+  fill_decode_items(plan, host_seq_lens, batch, &work);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, s, may_split);
-    else launch_decode<bf16_t, 128>(a, plan, s, may_split);
+    if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, work, s, may_split);
+    else launch_decode<bf16_t, 128>(a, plan, work, s, may_split);
   } else {
-    if (head_dim == 64) launch_decode<float, 64>(a, plan, s, may_split);
-    else launch_decode<float, 128>(a, plan, s, may_split);
+    if (head_dim == 64) launch_decode<float, 64>(a, plan, work, s, may_split);
+    else launch_decode<float, 128>(a, plan, work, s, may_split);
   }
   return launched("paged_decode");
 }

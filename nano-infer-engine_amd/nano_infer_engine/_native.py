@@ -75,7 +75,7 @@ _SIGNATURES = {
         ],
     ),
     "nie_argmax_rows": (_i32, [_i32, _ptr, _i64, _i64, _i64, _ptr, _ptr]),
-    "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
         [
@@ -87,7 +87,8 @@ _SIGNATURES = {
             _ptr, _i64, _i64, _i64,          # seq_lens, batch, max, total
             _f32,                            # scale
             _ptr, _i64, _i64,                # out, strides
-            _ptr, _i64, _ptr,                # workspace, bytes, stream
+            _ptr, _i64,                      # workspace, bytes
+            _ptr, _ptr,                      # host seq_lens, stream
         ],
     ),
     "nie_varlen_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr]),
@@ -143,6 +144,16 @@ def _host_lengths(cu_seqlens_host, context_lens_host, num_seqs: int):
     if cu.shape != (num_seqs + 1,) or ctx.shape != (num_seqs,):
         raise ValueError("host cu_seqlens / context_lens must have num_seqs + 1 / num_seqs entries")
     return cu, ctx
+
+
+def _host_seq_lens(seq_lens_host, batch: int):
+    """Host copy of a decode call's lengths as a C int32 array (or None)."""
+    if seq_lens_host is None:
+        return None
+    lens = np.ascontiguousarray(np.asarray(seq_lens_host, dtype=np.int32))
+    if lens.shape != (batch,):
+        raise ValueError("host seq_lens must have batch entries")
+    return lens
 
 
 def _array_ptr(a) -> int | None:
@@ -429,12 +440,15 @@ def paged_decode(
     total_seq_len: int,
     scale: float,
     out: torch.Tensor | None = None,
+    seq_lens_host=None,
 ) -> torch.Tensor:
     """Decode attention of query (B, Hq, D) over each sequence's first seq_lens[b] tokens.
 
     ``block_tables`` (B, W) int32 and ``seq_lens`` (B,) int32 are device
     tensors; ``max_seq_len`` and ``total_seq_len`` are their host-side max
-    and sum (they size the launch and must be exact).
+    and sum (they size the launch and must be exact).  The optional
+    ``seq_lens_host`` (ints equal to ``seq_lens``) lets the launch be planned
+    from the exact lengths.
     """
     num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
     _require_gpu(query, block_tables, seq_lens)
@@ -455,9 +469,11 @@ def paged_decode(
         out = torch.empty((batch, q_heads, head_dim), dtype=query.dtype, device=query.device)
     if batch == 0:
         return out
+    host_lens = _host_seq_lens(seq_lens_host, batch)
     lib = load_library()
     ws_bytes = lib.nie_paged_decode_workspace_bytes(
-        dtype_code(query.dtype), batch, q_heads, kv_heads, head_dim, block_size, max_seq_len, total_seq_len
+        dtype_code(query.dtype), batch, q_heads, kv_heads, head_dim, block_size, max_seq_len, total_seq_len,
+        _array_ptr(host_lens),
     )
     stream = _stream(query.device)
     workspace = _decode_workspace(query.device, stream, ws_bytes)
@@ -472,6 +488,7 @@ def paged_decode(
         float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
         workspace.data_ptr(), workspace.numel(),
+        _array_ptr(host_lens),
         stream,
     )
     _check(rc, "nie_paged_decode")
@@ -635,7 +652,8 @@ class PreparedDecode:
     __slots__ = ("_fn", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep")
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
-                 seq_lens: torch.Tensor, max_seq_len: int, total_seq_len: int, q_heads: int, scale: float):
+                 seq_lens: torch.Tensor, max_seq_len: int, total_seq_len: int, q_heads: int, scale: float,
+                 seq_lens_host=None):
         num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
         _require_gpu(block_tables, seq_lens)
         _check_attention_shapes(q_heads, kv_heads, head_dim)
@@ -645,22 +663,23 @@ class PreparedDecode:
         if (block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != batch
                 or not block_tables.is_contiguous()):
             raise ValueError("block_tables must be a contiguous int32 (batch, max_blocks) tensor")
+        host_lens = _host_seq_lens(seq_lens_host, batch)
         lib = load_library()
         code = dtype_code(k_cache.dtype)
         ws_bytes = lib.nie_paged_decode_workspace_bytes(code, batch, q_heads, kv_heads, head_dim, block_size,
-                                                        max_seq_len, total_seq_len)
+                                                        max_seq_len, total_seq_len, _array_ptr(host_lens))
         stream = _stream(k_cache.device)
         workspace = _decode_workspace(k_cache.device, stream, ws_bytes)
         self._fn = lib.nie_paged_decode
         self._dtype = k_cache.dtype
         self._device = k_cache.device
         self._shape = (batch, q_heads, head_dim)
-        self._keep = (block_tables, seq_lens, workspace)
+        self._keep = (block_tables, seq_lens, workspace, host_lens)
         self._pre = (code,)
         self._mid = (k_cache.data_ptr(), v_cache.data_ptr(), num_layers)
         self._post = (num_blocks, block_size, q_heads, kv_heads, head_dim, block_tables.data_ptr(),
                       block_tables.shape[1], seq_lens.data_ptr(), batch, max_seq_len, total_seq_len, float(scale),
-                      (workspace.data_ptr(), workspace.numel(), stream))
+                      (workspace.data_ptr(), workspace.numel(), _array_ptr(host_lens), stream))
 
     def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
         for t in (query, out):
@@ -669,10 +688,11 @@ class PreparedDecode:
                 raise ValueError("query/out must be aligned (batch, q_heads, head_dim) tensors matching the batch")
         kptr, vptr, num_layers = self._mid
         (num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch, max_len, total_len,
-         scale, (ws, ws_bytes, stream)) = self._post
+         scale, (ws, ws_bytes, hlens, stream)) = self._post
         rc = self._fn(self._pre[0], query.data_ptr(), query.stride(0), query.stride(1), kptr, vptr, num_layers,
                       layer_index, num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch,
-                      max_len, total_len, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes, stream)
+                      max_len, total_len, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes, hlens,
+                      stream)
         if rc:
             _check(rc, "nie_paged_decode")
         return out

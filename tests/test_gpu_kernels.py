@@ -25,11 +25,14 @@ def _log(msg: str) -> None:
     print(msg, flush=True)
 
 
-def _decode_hip(wl: workloads.PagedWorkload, kc, vc, q, dtype):
+def _decode_hip(wl: workloads.PagedWorkload, kc, vc, q, dtype, host_plan=False):
+    """The kernel's output.  host_plan: pass a host copy of the lengths (exact
+    launch plan, work items in the kernel arguments)."""
     tables = torch.from_numpy(wl.table_array()).to(DEV)
     lens = torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)
     out = _native.paged_decode(
-        q.to(DEV), kc, vc, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens), wl.head_dim**-0.5
+        q.to(DEV), kc, vc, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens), wl.head_dim**-0.5,
+        seq_lens_host=list(wl.seq_lens) if host_plan else None,
     )
     torch.cuda.synchronize()
     return out.cpu()
@@ -188,13 +191,15 @@ def test_decode_small_matches_oracle(dtype):
             assert np.abs(got[b].numpy() - exact).max() <= 1e-4
 
 
-def test_decode_ragged_lognormal_bf16():
-    """16 sequences, lognormal lengths up to 29600 (split-K with merge)."""
-    _log("decode_ragged bf16")
+@pytest.mark.parametrize("host_plan", [False, True])
+def test_decode_ragged_lognormal_bf16(host_plan):
+    """16 sequences, lognormal lengths up to 29600 (split-K with merge);
+    launches planned from bounds and from host lengths."""
+    _log(f"decode_ragged bf16 host_plan={host_plan}")
     wl = workloads.decode_ragged()
     kc, vc = wl.pool(torch.bfloat16)
     q, _, _ = wl.new_tokens(torch.bfloat16)
-    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, torch.bfloat16)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, torch.bfloat16, host_plan)
     want = _decode_oracle(wl, kc, vc, q)
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  lengths={wl.seq_lens} max_abs_err={err:.3e}")
@@ -206,13 +211,14 @@ def test_decode_ragged_lognormal_bf16():
     [(4, 4, 64, 16), (4, 2, 64, 2), (8, 2, 64, 1), (16, 2, 64, 4), (16, 1, 64, 32), (32, 8, 128, 16), (8, 8, 128, 3)],
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_decode_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
-    _log(f"decode shapes hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype}")
+@pytest.mark.parametrize("host_plan", [False, True])
+def test_decode_shapes(q_heads, kv_heads, head_dim, block_size, dtype, host_plan):
+    _log(f"decode shapes hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} host_plan={host_plan}")
     wl = workloads.ragged([0, 4, 70, 300, 1000], [1] * 5, seed=7, pool_factor=1.5, q_heads=q_heads,
                           kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
     kc, vc = wl.pool(dtype)
     q, _, _ = wl.new_tokens(dtype)
-    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, dtype)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), q, dtype, host_plan)
     want = _decode_oracle(wl, kc, vc, q)
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")

@@ -275,17 +275,35 @@ def test_library_exports_every_header_symbol():
 def test_library_workspace_queries():
     lib = _native.load_library()
     # decode partials: items * q_heads * (head_dim + 2) floats, items bounded by the split count
-    small = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710)
+    small = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710, None)
     assert small > 0 and small % (32 * 66 * 4) == 0
-    big = lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600)
+    big = lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None)
     assert big >= small
     # at most 128 tiles of 16 keys per split (the block-table window): at least 16 * ceil(1850 / 128) items
     assert big >= 16 * 15 * 32 * 66 * 4
-    assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1) == 0
-    assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710) == 0  # bad dtype
-    assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710) == 0  # head_dim 96
+    assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1, None) == 0
+    assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710, None) == 0  # bad dtype
+    assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710, None) == 0  # head_dim 96
     # prefill, planned from bounds
     assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 64, None, None) > 0
+
+
+def test_library_decode_plan_from_host_lengths():
+    """With host lengths the decode plan is exact: 16 sequences of 29,600
+    tokens (1,850 tiles each) fill the 256 resident workgroups with 16 splits
+    of 116 tiles (the bound-based plan uses 240), and lengths that do not
+    match max / total are rejected."""
+    lib = _native.load_library()
+
+    def query(lens, mx, total):
+        lens = np.asarray(lens, dtype=np.int32)
+        return lib.nie_paged_decode_workspace_bytes(1, len(lens), 32, 8, 64, 16, mx, total, lens.ctypes.data)
+
+    assert query([29600] * 16, 29600, 16 * 29600) == 256 * 32 * 66 * 4
+    # the bound-based plan (124-tile splits: 240 items) sizes for an upper bound on its items
+    assert lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None) >= 240 * 32 * 66 * 4
+    assert query([29600] * 16, 29600, 16 * 29600 - 1) == 0  # sum does not match
+    assert query([29600] * 15 + [0], 29600, 15 * 29600) == 0  # a length below 1
 
 
 def test_library_prefill_plan_from_host_lengths():
