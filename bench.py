@@ -40,6 +40,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--layers", type=int, default=16)
     p.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
+    p.add_argument("--unfused-append", action="store_true",
+                   help="decode step as nie_kv_append then nie_paged_decode (two launches per layer)")
     p.add_argument("--skip-stress", action="store_true", help="do not run the 16x29600 decode figure")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
     p.add_argument("--skip-mixed", action="store_true", help="do not run the mixed chunked-prefill figure")
@@ -107,26 +109,33 @@ class DecodeBench:
         self.out = torch.empty_like(self.q)
         self.scale = wl.head_dim**-0.5
 
-    def step(self, s: int, events: list | None = None) -> None:
+    def step(self, s: int, events: list | None = None, fused: bool = True) -> None:
         """One decode step over every layer; optionally brackets each decode launch with HIP events.
 
-        The append and decode launches are prepared once per step and reused
-        by every layer, as a model forward does (``RaggedBatch.launchers``).
+        fused: one ``nie_paged_decode_append`` launch per layer writes the new
+        token and attends; otherwise ``nie_kv_append`` then ``nie_paged_decode``
+        (the events then bracket the decode call only).  The launches are
+        prepared once per step and reused by every layer, as a model forward
+        does (``RaggedBatch.launchers``).
         """
         import torch
 
         from nano_infer_engine import _native
 
-        append = _native.PreparedAppend(self.k_cache, self.v_cache, self.slots[s])
+        append = None if fused else _native.PreparedAppend(self.k_cache, self.v_cache, self.slots[s])
         decode = _native.PreparedDecode(self.k_cache, self.v_cache, self.tables, self.lens[s], self.max_len[s],
                                         self.total_len[s], self.wl.q_heads, self.scale,
                                         seq_lens_host=self.seq_lens_host[s])
         for layer in range(self.wl.num_layers):
-            append(self.k_new, self.v_new, layer)
+            if append is not None:
+                append(self.k_new, self.v_new, layer)
             if events is not None:
                 start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 start.record()
-            decode(self.q, layer, self.out)
+            if append is None:
+                decode.append_decode(self.q, self.k_new, self.v_new, layer, self.out)
+            else:
+                decode(self.q, layer, self.out)
             if events is not None:
                 end.record()
                 events.append((start, end))
@@ -141,34 +150,45 @@ def run_gpu(args):
     torch.cuda.set_device(device)
     _native.load_library()
     wl = workloads.decode_ragged(num_layers=args.layers)
-    total_steps = args.warmup + args.steps
+    # steps [0, W) warm up, [W, W+K) are the timed steps, [W+K, W+2K) are
+    # timed again per call with HIP events (kept out of the wall-clock pass,
+    # whose host and queue work they would add to)
+    timed_end = args.warmup + args.steps
+    total_steps = timed_end + args.steps
     bench = DecodeBench(wl, total_steps, device, seed=1)
     log(f"workload: {len(wl.context_lens)} seqs, contexts {wl.context_lens}, layers {args.layers}, "
         f"pool {bench.num_blocks} blocks ({2 * bench.k_cache.numel() * 2 / 1e9:.2f} GB)")
 
+    fused = not args.unfused_append
     for s in range(args.warmup):
-        bench.step(s)
+        bench.step(s, fused=fused)
     torch.cuda.synchronize()
 
-    ev: list = []
     t0 = time.perf_counter()
-    for s in range(args.warmup, total_steps):
-        bench.step(s, ev)
+    for s in range(args.warmup, timed_end):
+        bench.step(s, fused=fused)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
-    decode_bytes = 0
-    append_bytes = 0
-    for s in range(args.warmup, total_steps):
-        decode_bytes += workloads.decode_bytes(bench.seq_lens_host[s]) * args.layers
-        append_bytes += workloads.append_bytes(len(wl.context_lens)) * args.layers
+    ev: list = []
+    for s in range(timed_end, total_steps):
+        bench.step(s, ev, fused=fused)
+    torch.cuda.synchronize()
+
+    step_append = workloads.append_bytes(len(wl.context_lens))
+    decode_bytes = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(args.warmup, timed_end))
+    decode_bytes *= args.layers
+    append_bytes = step_append * args.layers * args.steps
+    event_bytes = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(timed_end, total_steps))
     launch_ms = [a.elapsed_time(b) for a, b in ev]
     avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
-    bytes_per_launch = decode_bytes / len(launch_ms)
+    # a fused call also moves the appended rows
+    bytes_per_launch = event_bytes * args.layers / len(launch_ms) + (step_append if fused else 0)
     achieved = bytes_per_launch / avg_launch_s / 1e9
     value = (decode_bytes + append_bytes) / elapsed / 1e9
-    log(f"timed {args.steps} steps in {elapsed * 1e3:.2f} ms; decode launch avg {avg_launch_s * 1e6:.2f} us "
-        f"for {bytes_per_launch / 1e6:.2f} MB -> {achieved:.0f} GB/s")
+    call = "nie_paged_decode_append" if fused else "nie_paged_decode"
+    log(f"timed {args.steps} steps in {elapsed * 1e3:.2f} ms ({value:.0f} GB/s); {call} call avg "
+        f"{avg_launch_s * 1e6:.2f} us for {bytes_per_launch / 1e6:.2f} MB -> {achieved:.0f} GB/s")
 
     result = {
         "metric": "paged-attn HBM GB/s (% of peak); e2e output tok/s, Llama-1B-shape batch 16",
@@ -186,7 +206,8 @@ def run_gpu(args):
         "config": {
             "workload": "continuous-batching decode step: 16 ragged sequences (lognormal median 2048, "
                         "sigma 1, clip [32, 29600], seed 1), 32 q / 8 kv heads, head_dim 64, block_size 16, "
-                        f"append 1 token/seq then paged decode attention, x{args.layers} layers",
+                        f"append 1 token/seq then paged decode attention, x{args.layers} layers"
+                        + (" (one fused launch per layer)" if fused else " (separate append launch)"),
             "sequences": len(wl.context_lens),
             "context_tokens_first_step": int(sum(wl.context_lens)),
             "layers": args.layers,
@@ -195,7 +216,7 @@ def run_gpu(args):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "nie_paged_decode call: paged_decode_kernel + decode_merge_kernel (HIP events around the call)",
+            "kernel": f"{call} call: paged_decode_kernel + decode_merge_kernel (HIP events around the call)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -226,16 +247,19 @@ def run_stress(args):
     steps, warmup = 20, 3
     wl = workloads.decode_long(num_layers=1)
     bench = DecodeBench(wl, steps + warmup, device, seed=4)
+    fused = not args.unfused_append
     for s in range(warmup):
-        bench.step(s)
+        bench.step(s, fused=fused)
     torch.cuda.synchronize()
     ev: list = []
     for s in range(warmup, warmup + steps):
-        bench.step(s, ev)
+        bench.step(s, ev, fused=fused)
     torch.cuda.synchronize()
     launch_ms = [a.elapsed_time(b) for a, b in ev]
     avg = sum(launch_ms) / len(launch_ms) / 1e3
     per_launch = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(warmup, warmup + steps)) / steps
+    if fused:
+        per_launch += workloads.append_bytes(len(wl.context_lens))
     gbs = per_launch / avg / 1e9
     log(f"stress 16x29600: {avg * 1e6:.1f} us per layer-step, {gbs:.0f} GB/s")
     del bench

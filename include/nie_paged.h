@@ -220,6 +220,41 @@ int nie_paged_decode(int dtype,
                      void* stream);
 
 /*
+ * Decode step with the cache update in the same launch: for each sequence b
+ * it writes the new key/value rows k_new[b] / v_new[b] (kv_heads x head_dim,
+ * heads contiguous; row strides k_new_stride / v_new_stride elements) at
+ * logical position seq_lens[b] - 1, in the slot its block table gives
+ * (block_tables[b][p / block_size] * block_size + p % block_size), then
+ * attends over positions [0, seq_lens[b]) exactly as nie_paged_decode.  The
+ * cache and the output equal those of nie_kv_append with that slot mapping
+ * followed by nie_paged_decode, provided no other sequence of the call reads
+ * that slot (the block of a sequence's newest token is its own).  A table
+ * entry outside [0, num_blocks) skips the write, as an out-of-range slot
+ * skips nie_kv_append.  Workspace: nie_paged_decode_workspace_bytes.
+ * Replaces: the decode step of GroupedQueryAttention.forward's paged branch
+ *           (src/nano_infer_engine/layers/attention.py:246-269): one
+ *           PagedKVCache.write per sequence at its cached length
+ *           (paged_cache.py:264-322), then batched_paged_attention_reference
+ *           with lengths + 1.
+ */
+int nie_paged_decode_append(int dtype,
+                            const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void* k_new, int64_t k_new_stride,
+                            const void* v_new, int64_t v_new_stride,
+                            void* k_cache, void* v_cache,
+                            int64_t num_layers, int64_t layer_index,
+                            int64_t num_blocks, int64_t block_size,
+                            int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                            const int32_t* block_tables, int64_t table_stride,
+                            const int32_t* seq_lens, int64_t batch,
+                            int64_t max_seq_len, int64_t total_seq_len,
+                            float scale,
+                            void* out, int64_t out_stride_b, int64_t out_stride_h,
+                            void* workspace, int64_t workspace_bytes,
+                            const int32_t* host_seq_lens,
+                            void* stream);
+
+/*
  * Workspace bytes needed by nie_varlen_prefill (host values: number of
  * sequences, total and maximum query length, maximum context+query length,
  * and the same optional host copies of cu_seqlens_q / context_lens as the

@@ -794,6 +794,11 @@ struct DecodeArgs {
   float* ws_o;   // (ws_items, q_heads, head_dim)
   float* ws_ml;  // (ws_items, q_heads, 2)
   int64_t ws_items;  // partial slots in the workspace (0 when there is none)
+  // Fused append (nie_paged_decode_append): new K/V rows (batch, kv_heads,
+  // head_dim), row strides in elements; k_new == nullptr: no append.
+  const void* k_new = nullptr;
+  const void* v_new = nullptr;
+  int64_t kn_s = 0, vn_s = 0;
 };
 
 // Work items of a decode call planned from host copies of the lengths,
@@ -1043,6 +1048,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     if (b < 0) return;  // uniform over the workgroup
     seq_len = a.seq_lens[b];
   }
+  seq_len = __builtin_amdgcn_readfirstlane(seq_len);
   const int h0 = (int)blockIdx.y * kHeads;  // first KV head of the group
   const int h = h0 + wave;
 
@@ -1069,8 +1075,31 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   SoftmaxState<D> st;
   st.init();
 
+  // Fused append: the workgroup whose split ends the sequence takes the new
+  // K/V row of position seq_len - 1.  In wave w, lanes [0, kHeadChunks)
+  // carry the 16-byte K chunks of head h0 + w and the next kHeadChunks lanes
+  // its V chunks.  At the last tile the wave writes them over its LDS copy of
+  // that row (only this wave reads its head's chunks), and once the ring has
+  // drained, into the cache slot of the position.  A table entry outside the
+  // pool skips both, as an out-of-range slot skips nie_kv_append.
+  constexpr int kHeadChunks = D * Elt<T>::kBytes / 16;
+  const bool appender = a.k_new != nullptr && key_end == seq_len;  // uniform over the workgroup
+  const bool carrier = appender && lane < 2 * kHeadChunks;
+  const bool carries_k = lane < kHeadChunks;
+  const int new_c = carries_k ? lane : lane - kHeadChunks;  // chunk within the head's row
+  v4u new_chunk;  // defined on carrier lanes, used only there
+  if (carrier) {
+    const T* src = reinterpret_cast<const T*>(carries_k ? a.k_new : a.v_new) + b * (carries_k ? a.kn_s : a.vn_s) +
+                   h * D + new_c * kEltPerChunk;
+    new_chunk = *reinterpret_cast<const v4u*>(src);
+  }
+  bool carry = false;  // set at the last tile: the chunk goes to new_dst
+  T* new_dst = nullptr;
+
   TableCache tc;
   if constexpr (kUniform) tc.load(table, tlen, key_begin >> a.geom.bs_shift);
+  // the new chunk's load completes with the table loads (one round trip)
+  asm volatile("" : "+v"(new_chunk));
 
   // This wave's share of the DMA ops of a tile: op = wave + i*kHeads; in op
   // `op`, lane l fills LDS position op*64 + l, i.e. row r = op*kRowsPerOp +
@@ -1177,6 +1206,35 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
       __builtin_amdgcn_sched_barrier(0);
       issue((j + kAhead) % kStages, min(key_begin + (tt + kAhead) * kTileKeys, last_key0));
       __builtin_amdgcn_sched_barrier(0);
+      if (appender && tt == ntiles - 1) {
+        const int pos = seq_len - 1;
+        int lb, off;
+        if (a.geom.bs_shift >= 0) {
+          lb = pos >> a.geom.bs_shift;
+          off = pos & (a.geom.block_size - 1);
+        } else {
+          lb = (int)((uint32_t)pos / (uint32_t)a.geom.block_size);
+          off = pos - lb * a.geom.block_size;
+        }
+        int phys;
+        if constexpr (kUniform) {
+          phys = tc.template lookup<false>(table, tlen, lb);  // the split's blocks are in the window
+        } else {
+          phys = table[lb];
+        }
+        if (carrier && lb < tlen && phys >= 0 && phys < a.geom.num_blocks) {
+          T* cache = reinterpret_cast<T*>(const_cast<void*>(carries_k ? a.k_cache : a.v_cache));
+          new_dst = cache + a.geom.layer_offset + ((int64_t)phys * a.geom.block_size + off) * a.geom.row_elems +
+                    h * D + new_c * kEltPerChunk;
+          carry = true;
+          const uint32_t patch = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)GT::kBytes) +
+                                 (uint32_t)GT::chunk_offset(pos - key_begin - tt * kTileKeys,
+                                                            wave * kHeadChunks + new_c);
+          // the wait + barrier above ordered the tile's DMA before this write
+          asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(patch), "v"(new_chunk) : "memory");
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
       consume(j, key_begin + tt * kTileKeys);
     }
   }
@@ -1184,6 +1242,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // Drain the redundant prefetches issued past the last tile before this
   // workgroup's LDS can be handed to another one.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  if (carry) *reinterpret_cast<v4u*>(new_dst) = new_chunk;
   const float lsum = sum_over_groups(st.lsum);
   if (nsplit == 1) {
     if (!row_valid) return;
@@ -2573,15 +2632,23 @@ NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64
   return p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
-NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                             const void* k_cache, const void* v_cache, int64_t num_layers,
-                             int64_t layer_index, int64_t num_blocks, int64_t block_size,
-                             int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                             const int32_t* block_tables, int64_t table_stride,
-                             const int32_t* seq_lens, int64_t batch, int64_t max_seq_len,
-                             int64_t total_seq_len, float scale, void* out,
-                             int64_t out_stride_b, int64_t out_stride_h, void* workspace,
-                             int64_t workspace_bytes, const int32_t* host_seq_lens, void* stream) {
+namespace {
+
+// New K/V rows of a fused decode step (nie_paged_decode_append).
+struct DecodeAppend {
+  const void* k_new = nullptr;
+  int64_t k_stride = 0;
+  const void* v_new = nullptr;
+  int64_t v_stride = 0;
+};
+
+int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                      const void* v_cache, int64_t num_layers, int64_t layer_index, int64_t num_blocks,
+                      int64_t block_size, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                      const int32_t* block_tables, int64_t table_stride, const int32_t* seq_lens, int64_t batch,
+                      int64_t max_seq_len, int64_t total_seq_len, float scale, void* out, int64_t out_stride_b,
+                      int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                      const int32_t* host_seq_lens, const DecodeAppend& append, void* stream) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -2608,6 +2675,14 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
   }
   if (host_seq_lens != nullptr && !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) {
     return fail(NIE_EINVAL, "host seq_lens do not match max_seq_len / total_seq_len");
+  }
+  if (append.k_new != nullptr || append.v_new != nullptr) {
+    if (!append.k_new || !append.v_new) return fail(NIE_EINVAL, "null pointer argument");
+    if (append.k_stride < kv_heads * head_dim || append.v_stride < kv_heads * head_dim ||
+        !check_aligned(append.k_new, append.k_stride, head_dim, es) ||
+        !check_aligned(append.v_new, append.v_stride, head_dim, es)) {
+      return fail(NIE_EINVAL, "new K/V rows must be 16-byte aligned (batch, kv_heads, head_dim) rows");
+    }
   }
   const DecodePlan plan = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
   const int64_t tps = plan.tps;
@@ -2641,6 +2716,10 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
   a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + items * q_heads * head_dim : nullptr;
   a.ws_items = have_ws ? items : 0;
+  a.k_new = append.k_new;
+  a.v_new = append.v_new;
+  a.kn_s = append.k_stride;
+  a.vn_s = append.v_stride;
   // The grid is an upper bound on the item count (exact to within `batch`);
   // workgroups past the last real item return immediately.
   DecodeItems work;
@@ -2654,6 +2733,45 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
     else launch_decode<float, 128>(a, plan, work, s, may_split);
   }
   return launched("paged_decode");
+}
+
+}  // namespace
+
+NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* k_cache, const void* v_cache, int64_t num_layers,
+                             int64_t layer_index, int64_t num_blocks, int64_t block_size,
+                             int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                             const int32_t* block_tables, int64_t table_stride,
+                             const int32_t* seq_lens, int64_t batch, int64_t max_seq_len,
+                             int64_t total_seq_len, float scale, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                             int64_t workspace_bytes, const int32_t* host_seq_lens, void* stream) {
+  return paged_decode_call(dtype, q, q_stride_b, q_stride_h, k_cache, v_cache, num_layers, layer_index, num_blocks,
+                           block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
+                           max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, workspace,
+                           workspace_bytes, host_seq_lens, DecodeAppend{}, stream);
+}
+
+NIE_API int nie_paged_decode_append(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                    const void* k_new, int64_t k_new_stride, const void* v_new,
+                                    int64_t v_new_stride, void* k_cache, void* v_cache, int64_t num_layers,
+                                    int64_t layer_index, int64_t num_blocks, int64_t block_size,
+                                    int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                    const int32_t* block_tables, int64_t table_stride,
+                                    const int32_t* seq_lens, int64_t batch, int64_t max_seq_len,
+                                    int64_t total_seq_len, float scale, void* out, int64_t out_stride_b,
+                                    int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                                    const int32_t* host_seq_lens, void* stream) {
+  if (batch > 0 && (!k_new || !v_new)) return fail(NIE_EINVAL, "null pointer argument");
+  DecodeAppend append;
+  append.k_new = k_new;
+  append.k_stride = k_new_stride;
+  append.v_new = v_new;
+  append.v_stride = v_new_stride;
+  return paged_decode_call(dtype, q, q_stride_b, q_stride_h, k_cache, v_cache, num_layers, layer_index, num_blocks,
+                           block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
+                           max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, workspace,
+                           workspace_bytes, host_seq_lens, append, stream);
 }
 
 NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query_tokens,

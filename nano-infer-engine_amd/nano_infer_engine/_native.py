@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "nie_argmax_rows",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
+    "nie_paged_decode_append",
     "nie_varlen_prefill_workspace_bytes",
     "nie_varlen_prefill",
 )
@@ -80,6 +81,22 @@ _SIGNATURES = {
         _i32,
         [
             _i32, _ptr, _i64, _i64,          # dtype, q, q strides
+            _ptr, _ptr,                      # caches
+            _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
+            _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
+            _ptr, _i64,                      # block tables, stride
+            _ptr, _i64, _i64, _i64,          # seq_lens, batch, max, total
+            _f32,                            # scale
+            _ptr, _i64, _i64,                # out, strides
+            _ptr, _i64,                      # workspace, bytes
+            _ptr, _ptr,                      # host seq_lens, stream
+        ],
+    ),
+    "nie_paged_decode_append": (
+        _i32,
+        [
+            _i32, _ptr, _i64, _i64,          # dtype, q, q strides
+            _ptr, _i64, _ptr, _i64,          # new K rows, stride, new V rows, stride
             _ptr, _ptr,                      # caches
             _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
             _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
@@ -441,6 +458,7 @@ def paged_decode(
     scale: float,
     out: torch.Tensor | None = None,
     seq_lens_host=None,
+    new_kv: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Decode attention of query (B, Hq, D) over each sequence's first seq_lens[b] tokens.
 
@@ -449,6 +467,11 @@ def paged_decode(
     and sum (they size the launch and must be exact).  The optional
     ``seq_lens_host`` (ints equal to ``seq_lens``) lets the launch be planned
     from the exact lengths.
+
+    ``new_kv=(keys, values)``, each (B, Hkv, D): the same launch first
+    writes row b at position seq_lens[b] - 1 (the slot its block table
+    gives), as the decode step of ``GroupedQueryAttention.forward`` writes
+    the new token before attending (reference ``layers/attention.py:246-269``).
     """
     num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
     _require_gpu(query, block_tables, seq_lens)
@@ -477,6 +500,25 @@ def paged_decode(
     )
     stream = _stream(query.device)
     workspace = _decode_workspace(query.device, stream, ws_bytes)
+    if new_kv is not None:
+        keys, values = _check_new_rows(new_kv, batch, kv_heads, head_dim, query.dtype, query.device)
+        rc = lib.nie_paged_decode_append(
+            dtype_code(query.dtype),
+            query.data_ptr(), query.stride(0), query.stride(1),
+            keys.data_ptr(), keys.stride(0), values.data_ptr(), values.stride(0),
+            k_cache.data_ptr(), v_cache.data_ptr(),
+            num_layers, layer_index, num_blocks, block_size,
+            q_heads, kv_heads, head_dim,
+            block_tables.data_ptr(), block_tables.shape[1],
+            seq_lens.data_ptr(), batch, max_seq_len, total_seq_len,
+            float(scale),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            workspace.data_ptr(), workspace.numel(),
+            _array_ptr(host_lens),
+            stream,
+        )
+        _check(rc, "nie_paged_decode_append")
+        return out
     rc = lib.nie_paged_decode(
         dtype_code(query.dtype),
         query.data_ptr(), query.stride(0), query.stride(1),
@@ -493,6 +535,16 @@ def paged_decode(
     )
     _check(rc, "nie_paged_decode")
     return out
+
+
+def _check_new_rows(new_kv, batch: int, kv_heads: int, head_dim: int, dtype, device):
+    """The (keys, values) rows of a fused decode step: (batch, kv_heads, head_dim), 16-byte aligned."""
+    keys, values = new_kv
+    for t in (keys, values):
+        if (t.dtype != dtype or t.device != device or t.shape != (batch, kv_heads, head_dim) or t.stride(2) != 1
+                or t.stride(1) != head_dim or t.data_ptr() % 16 or (t.stride(0) * t.element_size()) % 16):
+            raise ValueError("new keys/values must be aligned (batch, kv_heads, head_dim) rows matching the query")
+    return keys, values
 
 
 def varlen_prefill(
@@ -649,7 +701,7 @@ class PreparedRopeAppend:
 class PreparedDecode:
     """``paged_decode`` for one batch of sequences (tables, lengths), any layer."""
 
-    __slots__ = ("_fn", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep")
+    __slots__ = ("_fn", "_fn_append", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep", "_kv_shape")
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, total_seq_len: int, q_heads: int, scale: float,
@@ -671,9 +723,11 @@ class PreparedDecode:
         stream = _stream(k_cache.device)
         workspace = _decode_workspace(k_cache.device, stream, ws_bytes)
         self._fn = lib.nie_paged_decode
+        self._fn_append = lib.nie_paged_decode_append
         self._dtype = k_cache.dtype
         self._device = k_cache.device
         self._shape = (batch, q_heads, head_dim)
+        self._kv_shape = (batch, kv_heads, head_dim)
         self._keep = (block_tables, seq_lens, workspace, host_lens)
         self._pre = (code,)
         self._mid = (k_cache.data_ptr(), v_cache.data_ptr(), num_layers)
@@ -695,6 +749,26 @@ class PreparedDecode:
                       stream)
         if rc:
             _check(rc, "nie_paged_decode")
+        return out
+
+    def append_decode(self, query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, layer_index: int,
+                      out: torch.Tensor) -> torch.Tensor:
+        """Writes keys/values row b at position seq_lens[b] - 1, then decodes, in one launch."""
+        for t in (query, out):
+            if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
+                    or t.data_ptr() % 16):
+                raise ValueError("query/out must be aligned (batch, q_heads, head_dim) tensors matching the batch")
+        _check_new_rows((keys, values), *self._kv_shape, self._dtype, self._device)
+        kptr, vptr, num_layers = self._mid
+        (num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch, max_len, total_len,
+         scale, (ws, ws_bytes, hlens, stream)) = self._post
+        rc = self._fn_append(self._pre[0], query.data_ptr(), query.stride(0), query.stride(1), keys.data_ptr(),
+                             keys.stride(0), values.data_ptr(), values.stride(0), kptr, vptr, num_layers, layer_index,
+                             num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch,
+                             max_len, total_len, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes,
+                             hlens, stream)
+        if rc:
+            _check(rc, "nie_paged_decode_append")
         return out
 
 

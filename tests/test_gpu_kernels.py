@@ -313,6 +313,85 @@ def test_decode_workspace_reuse_across_calls():
         assert err <= 2e-2
 
 
+def _append_decode_pair(wl, dtype, host_plan, layer=0, table_edit=None):
+    """Fused append + decode against nie_kv_append then nie_paged_decode on the
+    same inputs: caches and outputs must be bit-identical, and the output
+    within tolerance of the oracle (which writes the rows, then attends).
+
+    The pool gets `layer` extra leading layers of other values, so the
+    fused write is checked at a layer offset; table_edit(table_array) may
+    alter the device tables (both paths see the same ones).
+    """
+    kc, vc = wl.pool(dtype)
+    if layer:
+        kc = torch.cat([torch.randn((layer,) + kc.shape[1:]).to(dtype), kc])
+        vc = torch.cat([torch.randn((layer,) + vc.shape[1:]).to(dtype), vc])
+    q, k_new, v_new = wl.new_tokens(dtype)
+    table_arr = wl.table_array()
+    if table_edit is not None:
+        table_edit(table_arr)
+    pos = np.asarray(wl.seq_lens) - 1
+    slots = table_arr[np.arange(len(pos)), pos // wl.block_size].astype(np.int64) * wl.block_size + pos % wl.block_size
+    tables = torch.from_numpy(table_arr).to(DEV)
+    lens = torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)
+    host = list(wl.seq_lens) if host_plan else None
+    args = (max(wl.seq_lens), sum(wl.seq_lens), wl.head_dim**-0.5)
+    dq, dkn, dvn = q.to(DEV), k_new.to(DEV), v_new.to(DEV)
+
+    k1, v1 = kc.to(DEV), vc.to(DEV)
+    _native.kv_append(k1, v1, layer, dkn, dvn, torch.from_numpy(slots).to(DEV))
+    out1 = _native.paged_decode(dq, k1, v1, layer, tables, lens, *args, seq_lens_host=host)
+    k2, v2 = kc.to(DEV), vc.to(DEV)
+    out2 = _native.paged_decode(dq, k2, v2, layer, tables, lens, *args, seq_lens_host=host, new_kv=(dkn, dvn))
+    torch.cuda.synchronize()
+    assert torch.equal(k1.cpu(), k2.cpu()) and torch.equal(v1.cpu(), v2.cpu()), "fused write differs"
+    assert torch.equal(out1.cpu(), out2.cpu()), "fused output differs"
+    return out2.cpu(), kc, vc, q, k_new, v_new
+
+
+@pytest.mark.parametrize(
+    "q_heads,kv_heads,head_dim,block_size",
+    [(32, 8, 64, 16), (4, 2, 64, 2), (16, 2, 64, 4), (16, 1, 64, 32), (32, 8, 128, 16), (8, 8, 128, 3)],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("host_plan", [False, True])
+def test_decode_append_matches_append_then_decode(q_heads, kv_heads, head_dim, block_size, dtype, host_plan):
+    """The new token lands on every row of a 16-key tile (contexts 0, 4, 15,
+    16, 70, 300, 1000) and in single- and multi-split sequences."""
+    _log(f"decode_append hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} host_plan={host_plan}")
+    wl = workloads.ragged([0, 4, 15, 16, 70, 300, 1000], [1] * 7, seed=13, pool_factor=1.5, q_heads=q_heads,
+                          kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
+    got, kc, vc, q, k_new, v_new = _append_decode_pair(wl, dtype, host_plan, layer=1)
+    ref_k, ref_v = kc.clone(), vc.clone()
+    for b, (table, ctx) in enumerate(zip(wl.tables, wl.context_lens)):
+        reference_ops.write_tokens(ref_k, ref_v, 1, table, wl.block_size, ctx, k_new[b : b + 1], v_new[b : b + 1])
+    want = reference_ops.batched_paged_attention_reference(
+        q, ref_k, ref_v, tuple(tuple(t) for t in wl.tables), tuple(wl.seq_lens), 1)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("host_plan", [False, True])
+def test_decode_append_ragged_lognormal_bf16(host_plan):
+    """The 16-sequence lognormal decode step (many splits per sequence)."""
+    _log(f"decode_append ragged host_plan={host_plan}")
+    wl = workloads.decode_ragged()
+    _append_decode_pair(wl, torch.bfloat16, host_plan)
+
+
+def test_decode_append_skips_out_of_pool_table_entry():
+    """A newest-token table entry outside the pool: no write (as kv_append
+    skips an out-of-range slot), and the same output as the separate calls."""
+    _log("decode_append out-of-pool entry")
+    wl = workloads.ragged([40, 100, 7], [1, 1, 1], seed=17, q_heads=32, kv_heads=8)
+
+    def edit(arr):
+        arr[1, 100 // wl.block_size] = wl.num_blocks + 3
+
+    _append_decode_pair(wl, torch.bfloat16, True, table_edit=edit)
+
+
 def _prefill_case(wl, dtype, host_plan=True):
     """The kernel's output and the oracle's.  host_plan: pass host copies of
     the lengths (exact launch plan) or not (plan from upper bounds)."""
