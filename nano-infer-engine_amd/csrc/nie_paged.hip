@@ -161,11 +161,17 @@ __device__ __forceinline__ float sum_over_groups(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Maximum of two scores.  Scores are never NaN where it matters (masked keys
+// are -inf; a NaN input propagates, as through the reference's softmax), so
+// the IEEE-754 2019 maximum serves, which gfx950 runs as v_maximum3_f32
+// without the operand canonicalization fmaxf needs in IEEE mode.
+__device__ __forceinline__ float score_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ float max_over_groups(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = score_max(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return score_max(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
@@ -382,9 +388,9 @@ struct SoftmaxState {
 // rescaled to the new running max.
 template <int D>
 __device__ __forceinline__ void softmax_tile(SoftmaxState<D>& st, v4f& s) {
-  float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  float tmax = score_max(score_max(s[0], s[1]), score_max(s[2], s[3]));
   tmax = max_over_groups(tmax);
-  const float m_new = fmaxf(st.m, tmax);
+  const float m_new = score_max(st.m, tmax);
   // A row with nothing unmasked so far keeps m = -inf; use 0 as the
   // reference point so the exponentials below are exact zeros, not NaN.
   const float nref = (m_new == kNegInf) ? 0.f : -m_new * kLog2e;
@@ -415,8 +421,8 @@ __device__ __forceinline__ void softmax_tiles(SoftmaxState<D> (&st)[kBlocks], v4
   bool moved = false;
 #pragma unroll
   for (int nb = 0; nb < kBlocks; ++nb) {
-    const float tmax = max_over_groups(fmaxf(fmaxf(s[nb][0], s[nb][1]), fmaxf(s[nb][2], s[nb][3])));
-    m_new[nb] = fmaxf(st[nb].m, tmax);
+    const float tmax = max_over_groups(score_max(score_max(s[nb][0], s[nb][1]), score_max(s[nb][2], s[nb][3])));
+    m_new[nb] = score_max(st[nb].m, tmax);
     nref[nb] = (m_new[nb] == kNegInf) ? 0.f : -m_new[nb] * kLog2e;
     tsum[nb] = 0.f;
 #pragma unroll
@@ -1450,6 +1456,28 @@ __device__ __forceinline__ PrefillItem prefill_locate(const PrefillArgs& a, int6
   return it;
 }
 
+// Work items of a prefill call planned from host metadata, passed by value
+// as a kernel argument: item i (one workgroup per KV head) is piece
+// item_piece[i] (key tiles [piece*S, (piece+1)*S), S = tiles_per_split) of
+// query tile item_tile[i], whose request, rows and context are listed per
+// tile.  Without the table each workgroup locates its item from the device
+// copies of cu_seqlens / context_lens, one memory round trip more.
+constexpr int kMaxSchedTiles = 64;
+constexpr int kMaxSchedItems = 512;
+
+struct PrefillSchedule {
+  int32_t count = 0;  // items; 0: located on the device
+  uint8_t item_tile[kMaxSchedItems];
+  uint8_t item_piece[kMaxSchedItems];
+  int32_t first_item[kMaxSchedTiles];  // the tile's first item (its partials' first workspace slot)
+  int32_t nsplit[kMaxSchedTiles];      // the tile's items; 1: the rows are written out
+  int32_t req[kMaxSchedTiles];         // request of the tile
+  int32_t q_begin[kMaxSchedTiles];     // the request's first packed query row
+  int32_t q_len[kMaxSchedTiles];       // the request's query tokens
+  int32_t ctx[kMaxSchedTiles];         // the request's cached tokens
+  int32_t t0[kMaxSchedTiles];          // the tile's first query token within the request
+};
+
 // Key steps of kPrefillStepTiles 16-key tiles (64 keys) stream through an LDS
 // ring of prefill_stages() steps.
 constexpr int kPrefillStepTiles = 4;
@@ -1495,13 +1523,15 @@ __device__ __forceinline__ void softmax_step(SoftmaxState<D> (&st)[kBlocks], v4f
   for (int nb = 0; nb < kBlocks; ++nb) {
     float tm[kSub];
 #pragma unroll
-    for (int t = 0; t < kSub; ++t) tm[t] = fmaxf(fmaxf(s[nb][t][0], s[nb][t][1]), fmaxf(s[nb][t][2], s[nb][t][3]));
+    for (int t = 0; t < kSub; ++t) {
+      tm[t] = score_max(score_max(s[nb][t][0], s[nb][t][1]), score_max(s[nb][t][2], s[nb][t][3]));
+    }
 #pragma unroll
     for (int w = 1; w < kSub; w <<= 1) {
 #pragma unroll
-      for (int t = 0; t + w < kSub; t += 2 * w) tm[t] = fmaxf(tm[t], tm[t + w]);
+      for (int t = 0; t + w < kSub; t += 2 * w) tm[t] = score_max(tm[t], tm[t + w]);
     }
-    m_new[nb] = fmaxf(st[nb].m, max_over_groups(tm[0]));
+    m_new[nb] = score_max(st[nb].m, max_over_groups(tm[0]));
     grow |= m_new[nb] != kNegInf && (st[nb].m == kNegInf || (m_new[nb] - st[nb].m) * c > kRescaleLog2);
   }
   if (__ballot(grow)) {
@@ -1577,7 +1607,7 @@ __device__ __forceinline__ void ring_read_tr_n(v2u (&r)[N], const uint32_t (&add
 // applied inside the exponential (bf16 only).
 template <typename T, int D, bool kUniform, int kRowBlocks, bool kPow2Scale>
 __global__ __launch_bounds__(kPrefillWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
-void varlen_prefill_kernel(PrefillArgs a) {
+void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, 1>;
   constexpr int kSub = kPrefillStepTiles;
@@ -1596,31 +1626,54 @@ void varlen_prefill_kernel(PrefillArgs a) {
   const int row = lane & 15;
   const int tpt = a.tokens_per_tile;
   const int S = a.tiles_per_split;
-
-  const PrefillItem pit = prefill_locate(a, (int64_t)blockIdx.x);
-  if (pit.r < 0) return;  // uniform over the workgroup
-  const int64_t r = pit.r, local = pit.local, first_r = pit.first;
   const int h = (int)blockIdx.y;
-  const int64_t q_begin = pit.q_begin;
-  const int q_len = pit.q_len;
-  const int ctx = pit.ctx;
-  // (query tile, split) of this item; the loop is wave-uniform
-  int qt = 0, split = (int)local, nsplit = 0;
-  for (;;) {
-    nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
-    if (split < nsplit) break;
-    split -= nsplit;
-    ++qt;
+
+  // This workgroup's item: request r, query tile from token t0, key tiles
+  // [tile_begin, tile_cap), and the workspace slot of its partial (-1: the
+  // item covers its query tile's keys and writes the rows out).
+  int64_t r, q_begin, slot;
+  int q_len, ctx, t0, tile_begin, tile_cap;
+  if (sc.count > 0) {
+    if ((int)blockIdx.x >= sc.count) return;  // uniform over the workgroup
+    const int k = sc.item_tile[blockIdx.x];
+    const int piece = sc.item_piece[blockIdx.x];
+    r = sc.req[k];
+    q_begin = sc.q_begin[k];
+    q_len = sc.q_len[k];
+    ctx = sc.ctx[k];
+    t0 = sc.t0[k];
+    tile_begin = piece * S;
+    slot = sc.nsplit[k] == 1 ? -1 : (int64_t)sc.first_item[k] + piece;
+  } else {
+    const PrefillItem pit = prefill_locate(a, (int64_t)blockIdx.x);
+    if (pit.r < 0) return;  // uniform over the workgroup
+    // (query tile, split) of this item; the loop is wave-uniform
+    int qt = 0, split = (int)pit.local, nsplit = 0;
+    for (;;) {
+      nsplit = (prefill_key_tiles(pit.ctx, pit.q_len, tpt, qt) + S - 1) / S;
+      if (split < nsplit) break;
+      split -= nsplit;
+      ++qt;
+    }
+    r = pit.r;
+    q_begin = pit.q_begin;
+    q_len = pit.q_len;
+    ctx = pit.ctx;
+    t0 = qt * tpt;
+    tile_begin = split * S;
+    slot = nsplit == 1 ? -1 : pit.first + pit.local;
   }
-  qt = __builtin_amdgcn_readfirstlane(qt);
-  split = __builtin_amdgcn_readfirstlane(split);
-  nsplit = __builtin_amdgcn_readfirstlane(nsplit);
-  const int64_t item = first_r + local;
-  const int t0 = qt * tpt;
+  r = uniform64(r);
+  q_begin = uniform64(q_begin);
+  slot = uniform64(slot);
+  q_len = __builtin_amdgcn_readfirstlane(q_len);
+  ctx = __builtin_amdgcn_readfirstlane(ctx);
+  t0 = __builtin_amdgcn_readfirstlane(t0);
+  tile_begin = __builtin_amdgcn_readfirstlane(tile_begin);
+  tile_cap = tile_begin + S;
   const int t_end = min(t0 + tpt, q_len);
   const int key_end = ctx + t_end;
-  const int tile_begin = split * S;
-  const int tile_end = min(tile_begin + S, (key_end + kTileKeys - 1) / kTileKeys);
+  const int tile_end = min(tile_cap, (key_end + kTileKeys - 1) / kTileKeys);
   const int last = min(tile_end * kTileKeys, key_end) - 1;  // last key this item reads
   const int last_key0 = (last / kTileKeys) * kTileKeys;     // first key of the tile holding it
   const int32_t* table = a.tables + r * a.table_stride;
@@ -1873,7 +1926,7 @@ void varlen_prefill_kernel(PrefillArgs a) {
     const int tq = t0 + (wave * kRowBlocks + nb) * tpb + row / a.group;
     if (tq >= t_end) continue;
     const int qh = h * a.group + row % a.group;
-    if (nsplit == 1) {
+    if (slot < 0) {
       const float inv = 1.f / lsum;
       T* dst = reinterpret_cast<T*>(a.out) + (q_begin + tq) * a.o_st + qh * a.o_sh + 4 * g;
 #pragma unroll
@@ -1881,9 +1934,9 @@ void varlen_prefill_kernel(PrefillArgs a) {
         store4<T>(dst + 16 * c, st[nb].o[c][0] * inv, st[nb].o[c][1] * inv, st[nb].o[c][2] * inv,
                   st[nb].o[c][3] * inv);
       }
-    } else if (a.ws_o != nullptr && item < a.ws_items) {
-      const int64_t slot = (item * a.geom.kv_heads + h) * kRows + (wave * kRowBlocks + nb) * 16 + row;
-      float* dst = a.ws_o + slot * D + 4 * g;
+    } else if (a.ws_o != nullptr && slot < a.ws_items) {
+      const int64_t wrow = (slot * a.geom.kv_heads + h) * kRows + (wave * kRowBlocks + nb) * 16 + row;
+      float* dst = a.ws_o + wrow * D + 4 * g;
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
         *reinterpret_cast<float4*>(dst + 16 * c) =
@@ -1891,7 +1944,7 @@ void varlen_prefill_kernel(PrefillArgs a) {
       }
       // the merge expects the maximum of the scaled scores
       const float m = kPow2Scale ? st[nb].m * a.scale : st[nb].m;
-      if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + slot * 2) = make_float2(m, lsum);
+      if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + wrow * 2) = make_float2(m, lsum);
     }
   }
 }
@@ -2140,6 +2193,43 @@ void fill_merge_jobs(const PrefillPlan& p, int64_t num_seqs, const int64_t* host
     }
   }
   jobs->count = n;
+}
+
+// The item table of a host-planned call (see PrefillSchedule), in the order
+// of the device-side enumeration: requests in order, query tiles in order,
+// pieces in order, so item indices, workspace slots and merge jobs are the
+// same either way.  False when the call has more query tiles or items than
+// the table holds (the workgroups then locate their items).
+bool build_prefill_schedule(const PrefillPlan& p, int64_t num_seqs, const int64_t* host_cu,
+                            const int32_t* host_ctx, PrefillSchedule* sc) {
+  sc->count = 0;
+  const int64_t tpt = p.tokens_per_tile;
+  int64_t k = 0, items = 0;
+  for (int64_t r = 0; r < num_seqs; ++r) {
+    const int64_t n = host_cu[r + 1] - host_cu[r];
+    for (int64_t qt = 0; qt < cdiv(n, tpt); ++qt) {
+      const int64_t nsplit = cdiv(host_key_tiles(host_ctx[r], n, tpt, qt), p.tps);
+      if (k == kMaxSchedTiles || items + nsplit > kMaxSchedItems || nsplit > 255 || host_cu[r] > 0x7fffffffLL ||
+          n > 0x7fffffffLL) {
+        return false;
+      }
+      sc->first_item[k] = (int32_t)items;
+      sc->nsplit[k] = (int32_t)nsplit;
+      sc->req[k] = (int32_t)r;
+      sc->q_begin[k] = (int32_t)host_cu[r];
+      sc->q_len[k] = (int32_t)n;
+      sc->ctx[k] = host_ctx[r];
+      sc->t0[k] = (int32_t)(qt * tpt);
+      for (int64_t j = 0; j < nsplit; ++j, ++items) {
+        sc->item_tile[items] = (uint8_t)k;
+        sc->item_piece[items] = (uint8_t)j;
+      }
+      ++k;
+    }
+  }
+  if (items != p.items) return false;  // the plan counts the same items
+  sc->count = (int32_t)items;
+  return true;
 }
 
 // Checks host copies of cu_seqlens / context_lens against the call's sizes.
@@ -2399,12 +2489,14 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& 
 }
 
 template <typename T, int D, int NB, bool P2>
-void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, hipStream_t stream) {
+void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc, hipStream_t stream) {
   const dim3 grid((unsigned)p.items, (unsigned)a.geom.kv_heads);
   if (uniform_tiles(a.geom)) {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a,
+                       sc);
   } else {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a,
+                       sc);
   }
 }
 
@@ -2415,13 +2507,13 @@ bool is_pow2_scale(float scale) {
 }
 
 template <typename T, int D, int NB>
-void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const PrefillMergeJobs& jobs, hipStream_t stream,
-                       bool merge) {
+void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc,
+                       const PrefillMergeJobs& jobs, hipStream_t stream, bool merge) {
   if constexpr (Elt<T>::kIsBf16) {
-    if (is_pow2_scale(a.scale)) launch_prefill_kernel<T, D, NB, true>(a, p, stream);
-    else launch_prefill_kernel<T, D, NB, false>(a, p, stream);
+    if (is_pow2_scale(a.scale)) launch_prefill_kernel<T, D, NB, true>(a, p, sc, stream);
+    else launch_prefill_kernel<T, D, NB, false>(a, p, sc, stream);
   } else {
-    launch_prefill_kernel<T, D, NB, false>(a, p, stream);
+    launch_prefill_kernel<T, D, NB, false>(a, p, sc, stream);
   }
   if (merge) {
     const unsigned tiles = (unsigned)(jobs.count > 0 ? jobs.count : p.qtiles);
@@ -2431,10 +2523,10 @@ void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const Prefill
 }
 
 template <typename T, int D>
-void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, const PrefillMergeJobs& jobs, hipStream_t stream,
-                    bool merge) {
-  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, jobs, stream, merge);
-  else launch_prefill_nb<T, D, 2>(a, p, jobs, stream, merge);
+void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc,
+                    const PrefillMergeJobs& jobs, hipStream_t stream, bool merge) {
+  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, sc, jobs, stream, merge);
+  else launch_prefill_nb<T, D, 2>(a, p, sc, jobs, stream, merge);
 }
 
 int check_aligned(const void* p, int64_t stride_a, int64_t stride_b, int64_t es) {
@@ -2872,13 +2964,15 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   PrefillMergeJobs jobs;
   jobs.count = 0;
   if (may_split) fill_merge_jobs(plan, num_seqs, host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr, &jobs);
+  PrefillSchedule sched;
+  if (host) build_prefill_schedule(plan, num_seqs, host_cu_seqlens, host_context_lens, &sched);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, jobs, s, may_split);
-    else launch_prefill<bf16_t, 128>(a, plan, jobs, s, may_split);
+    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, sched, jobs, s, may_split);
+    else launch_prefill<bf16_t, 128>(a, plan, sched, jobs, s, may_split);
   } else {
-    if (head_dim == 64) launch_prefill<float, 64>(a, plan, jobs, s, may_split);
-    else launch_prefill<float, 128>(a, plan, jobs, s, may_split);
+    if (head_dim == 64) launch_prefill<float, 64>(a, plan, sched, jobs, s, may_split);
+    else launch_prefill<float, 128>(a, plan, sched, jobs, s, may_split);
   }
   return launched("varlen_prefill");
 }
