@@ -1711,45 +1711,48 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   TableCache tc;
   if constexpr (kUniform) tc.load(table, tlen, (tile_begin * kTileKeys) >> a.geom.bs_shift);
 
-  // This wave's DMA ops of the step starting at key0: op = wave + i*kWaves,
-  // tile t = op / (2*kOps), then K ops and V ops of that tile.  Tiles past
-  // the item's last key are redirected to the tile that holds it, and rows
-  // past it to it (no lane reads a slot the sequence does not own; those
-  // keys are masked to p = 0).
+  // This wave's DMA ops of the step starting at key0: the K ops then the V
+  // ops of the step's tile `wave` (op = wave*kOwnOps + i, the tile's LDS
+  // position), so one table lookup serves all of them.  A tile past the
+  // item's last key is redirected to the tile that holds it, and rows past
+  // it to it (no lane reads a slot the sequence does not own; those keys are
+  // masked to p = 0).
+  static_assert(kOwnOps == 2 * GT::kOps, "one tile's K and V ops per wave");
   // Per-lane element offsets of this wave's ops inside a tile (the same for
   // every tile): the lane's row and its swizzled 16-byte chunk.
   int op_row[kOwnOps], op_row_off[kOwnOps], op_chunk_off[kOwnOps];
 #pragma unroll
   for (int i = 0; i < kOwnOps; ++i) {
-    const int kop = ((wave + i * kPrefillWaves) % (2 * GT::kOps)) % GT::kOps;
-    const int rr = kop * GT::kRowsPerOp + lane / GT::kChunks;
+    const int rr = (i % GT::kOps) * GT::kRowsPerOp + lane / GT::kChunks;
     op_row[i] = rr;
     op_row_off[i] = rr * a.geom.row_elems32;
     op_chunk_off[i] = ((lane % GT::kChunks) ^ GT::swz(rr)) * kEltPerChunk;
   }
   auto issue = [&](int slot, int key0) {
-    unsigned char* base = &ring[slot][0];
+    unsigned char* base = &ring[slot][0] + wave * kOwnOps * kWave * 16;
+    const int tkey0 = min(key0 + wave * kTileKeys, last_key0);
+    if constexpr (kUniform) {
+      // the tile lies in one block: one wave-uniform table lookup, then the
+      // lane's row (clamped to the item's last key) and chunk
+      const int lb = min(tkey0 >> a.geom.bs_shift, tlen - 1);
+      int phys = tc.template lookup<false>(table, tlen, lb);
+      phys = phys < 0 ? 0 : (phys >= a.geom.num_blocks ? a.geom.num_blocks - 1 : phys);
+      const int64_t tile = a.geom.layer_offset +
+                           ((int64_t)phys * a.geom.block_size + (tkey0 & (a.geom.block_size - 1))) *
+                               a.geom.row_elems;
+      const T* kt = kc + tile;
+      const T* vt = vc + tile;
+      const int row_cap = (last - tkey0) * a.geom.row_elems32;
 #pragma unroll
-    for (int i = 0; i < kOwnOps; ++i) {
-      const int op = wave + i * kPrefillWaves;
-      const int t = op / (2 * GT::kOps);
-      const int within = op % (2 * GT::kOps);
-      const int tkey0 = min(key0 + t * kTileKeys, last_key0);
-      const T* src_base = within < GT::kOps ? kc : vc;
-      if constexpr (kUniform) {
-        // the tile lies in one block: one wave-uniform table lookup, then the
-        // lane's row (clamped to the item's last key) and chunk
-        const int lb = min(tkey0 >> a.geom.bs_shift, tlen - 1);
-        int phys = tc.template lookup<false>(table, tlen, lb);
-        phys = phys < 0 ? 0 : (phys >= a.geom.num_blocks ? a.geom.num_blocks - 1 : phys);
-        const int64_t tile = a.geom.layer_offset +
-                             ((int64_t)phys * a.geom.block_size + (tkey0 & (a.geom.block_size - 1))) *
-                                 a.geom.row_elems;
-        const int off = min(op_row_off[i], (last - tkey0) * a.geom.row_elems32) + op_chunk_off[i];
-        lds_dma16(src_base + tile + off, base + op * kWave * 16);
-      } else {
+      for (int i = 0; i < kOwnOps; ++i) {
+        const int off = min(op_row_off[i], row_cap) + op_chunk_off[i];
+        lds_dma16((i < GT::kOps ? kt : vt) + off, base + i * kWave * 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kOwnOps; ++i) {
         const int64_t src = token_offset(a.geom, table, tlen, tkey0 + min(op_row[i], last - tkey0)) + op_chunk_off[i];
-        lds_dma16(src_base + src, base + op * kWave * 16);
+        lds_dma16((i < GT::kOps ? kc : vc) + src, base + i * kWave * 16);
       }
     }
   };
