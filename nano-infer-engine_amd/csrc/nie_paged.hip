@@ -1853,13 +1853,12 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     if (!full) {  // causal boundary or item end inside the step
 #pragma unroll
       for (int nb = 0; nb < kRowBlocks; ++nb) {
+        // key key0 + 16t + 4g + i is visible iff 16t + i <= lim
+        const int lim = min(q_pos[nb], last) - (key0 + 4 * g);
 #pragma unroll
         for (int t = 0; t < kSub; ++t) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = key0 + t * kTileKeys + 4 * g + i;
-            p[nb][t][i] = (key <= q_pos[nb] && key <= last) ? p[nb][t][i] : kNegInf;
-          }
+          for (int i = 0; i < 4; ++i) p[nb][t][i] = (t * kTileKeys + i <= lim) ? p[nb][t][i] : kNegInf;
         }
       }
     }
