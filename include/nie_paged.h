@@ -148,6 +148,34 @@ int nie_rope_kv_append(int dtype,
                        void* stream);
 
 /*
+ * RMSNorm of `rows` rows of `cols` elements: out = weight * (h / sqrt(mean(h*h)
+ * + eps)) with h the row in fp32, the product in fp32 and the result rounded
+ * to the storage dtype (weight NULL: no scale).  With residual != NULL the
+ * row is first x + residual, rounded to the storage dtype and also written
+ * to sum_out.  Rows are element strides apart; every row, the weight and
+ * sum_out must be 16-byte aligned, and cols a multiple of 16 bytes' worth of
+ * elements, at most 8192 (bf16) / 4096 (fp32).
+ * Replaces: RmsNorm.forward (src/nano_infer_engine/layers/rms_norm.py:25-31)
+ *           and, with residual, the residual add before the post-attention
+ *           norm (src/nano_infer_engine/layers/decoder.py:50-51, :73-74).
+ */
+int nie_rms_norm(int dtype, const void* x, int64_t x_stride,
+                 const void* residual, int64_t residual_stride,
+                 void* sum_out, int64_t sum_stride,
+                 const void* weight, void* out, int64_t out_stride,
+                 int64_t rows, int64_t cols, float eps, void* stream);
+
+/*
+ * SwiGLU's gated product over n contiguous elements: out = silu(gate) * up,
+ * silu(x) = x / (1 + exp(-x)) in fp32 rounded to the storage dtype, then the
+ * product in fp32 rounded again (torch's two kernels).  n must be a multiple
+ * of 16 bytes' worth of elements; buffers 16-byte aligned.
+ * Replaces: F.silu(self.gate_proj(x)) * self.up_proj(x)
+ *           (src/nano_infer_engine/layers/mlp.py:18-22).
+ */
+int nie_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/*
  * Greedy token selection: out[r] = index of the largest of the cols values
  * of row r (element (r, c) at r * row_stride + c), ties to the lowest index,
  * NaN larger than every number — torch.argmax's result.  out is int64.

@@ -935,6 +935,132 @@ __device__ __forceinline__ void ring_read_vt4(v4s (&a)[4], const uint32_t (&addr
   for (int c = 0; c < 4; ++c) a[c] = __builtin_bit_cast(v4s, r[c]);
 }
 
+// ---------------------------------------------------------------------------
+// Decoder-layer elementwise work on either side of attention
+// ---------------------------------------------------------------------------
+constexpr int kNormThreads = 256;
+constexpr int kNormVecsPerThread = 4;  // cols <= 256 x 4 x (16 bytes / element size)
+
+// Element e of a 16-byte vector of T as float.
+template <typename T>
+__device__ __forceinline__ float vec_elt(const v4u& w, int e) {
+  if constexpr (Elt<T>::kIsBf16) {
+    return bf16_bits_to_f32((w[e / 2] >> (16 * (e % 2))) & 0xffffu);
+  } else {
+    return __uint_as_float(w[e]);
+  }
+}
+
+// RMSNorm of one row per workgroup, in the arithmetic of the reference's
+// RmsNorm.forward (layers/rms_norm.py:25-31): h = fp32(x),
+// h / sqrt(mean(h * h) + eps), times fp32(weight), cast to the storage dtype
+// (round to nearest even).  Only the order of the sum of squares differs from
+// torch's reduction.  With `res`, the row is first x + res rounded to the
+// storage dtype (the decoder's residual add, layers/decoder.py:50-51), which
+// also goes to sum_out.  Each thread keeps its (up to kNormVecsPerThread)
+// 16-byte vectors in registers between the two passes.
+template <typename T>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const void* x, int64_t x_stride, const void* res,
+                                                              int64_t res_stride, void* sum_out,
+                                                              int64_t sum_stride, const void* weight, void* out,
+                                                              int64_t out_stride, int cols, float eps) {
+  constexpr int kPerVec = 16 / Elt<T>::kBytes;
+  const int64_t row = blockIdx.x;
+  const int nvec = cols / kPerVec;
+  const v4u* xr = reinterpret_cast<const v4u*>(reinterpret_cast<const T*>(x) + row * x_stride);
+  v4u v[kNormVecsPerThread];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormVecsPerThread; ++k) {
+    const int j = (int)threadIdx.x + k * kNormThreads;
+    if (j >= nvec) break;
+    v[k] = xr[j];
+    if (res != nullptr) {
+      const v4u r = reinterpret_cast<const v4u*>(reinterpret_cast<const T*>(res) + row * res_stride)[j];
+      v4u sum;
+      if constexpr (Elt<T>::kIsBf16) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          sum[w] = pack_bf16x2(vec_elt<T>(v[k], 2 * w) + vec_elt<T>(r, 2 * w),
+                               vec_elt<T>(v[k], 2 * w + 1) + vec_elt<T>(r, 2 * w + 1));
+        }
+      } else {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) sum[w] = __float_as_uint(vec_elt<T>(v[k], w) + vec_elt<T>(r, w));
+      }
+      v[k] = sum;
+      reinterpret_cast<v4u*>(reinterpret_cast<T*>(sum_out) + row * sum_stride)[j] = sum;
+    }
+#pragma unroll
+    for (int e = 0; e < kPerVec; ++e) {
+      const float h = vec_elt<T>(v[k], e);
+      ss = fmaf(h, h, ss);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  __shared__ float s_ss[kNormThreads / kWave];
+  if (lane_id() == 0) s_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) ss += s_ss[w];
+  const float denom = sqrtf(ss * (1.f / (float)cols) + eps);
+  v4u* orow = reinterpret_cast<v4u*>(reinterpret_cast<T*>(out) + row * out_stride);
+  const v4u* wv = reinterpret_cast<const v4u*>(weight);
+#pragma unroll
+  for (int k = 0; k < kNormVecsPerThread; ++k) {
+    const int j = (int)threadIdx.x + k * kNormThreads;
+    if (j >= nvec) break;
+    const v4u wk = weight != nullptr ? wv[j] : v4u{0u, 0u, 0u, 0u};
+    float y[kPerVec];
+#pragma unroll
+    for (int e = 0; e < kPerVec; ++e) {
+      y[e] = vec_elt<T>(v[k], e) / denom;
+      if (weight != nullptr) y[e] = vec_elt<T>(wk, e) * y[e];
+    }
+    v4u o;
+    if constexpr (Elt<T>::kIsBf16) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) o[w] = pack_bf16x2(y[2 * w], y[2 * w + 1]);
+    } else {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) o[w] = __float_as_uint(y[w]);
+    }
+    orow[j] = o;
+  }
+}
+
+// SwiGLU's product silu(gate) * up (layers/mlp.py:18-22) as torch computes
+// it in two kernels: s = silu(gate) in fp32, x / (1 + exp(-x)), rounded to
+// the storage dtype, then s * up in fp32, rounded again.  One 16-byte vector
+// per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate, const void* up, void* out, int64_t nvec) {
+  constexpr int kPerVec = 16 / Elt<T>::kBytes;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= nvec) return;
+  const v4u g = reinterpret_cast<const v4u*>(gate)[j];
+  const v4u u = reinterpret_cast<const v4u*>(up)[j];
+  float y[kPerVec];
+#pragma unroll
+  for (int e = 0; e < kPerVec; ++e) {
+    const float a = vec_elt<T>(g, e);
+    float sl = a / (1.f + expf(-a));
+    if constexpr (Elt<T>::kIsBf16) sl = bf16_bits_to_f32(f32_to_bf16_bits(sl));
+    y[e] = sl * vec_elt<T>(u, e);
+  }
+  v4u o;
+  if constexpr (Elt<T>::kIsBf16) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = pack_bf16x2(y[2 * w], y[2 * w + 1]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = __float_as_uint(y[w]);
+  }
+  reinterpret_cast<v4u*>(out)[j] = o;
+}
+
 // Merges nsplit split partials of one output row, one wave.  Split s of the
 // row has its unnormalised O row at po + s*po_stride and its (max, sum) pair
 // at ml + s*ml_stride.  The lanes form kSplitsPerPass groups of D/4 lanes; a
@@ -2711,6 +2837,62 @@ NIE_API int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t
                        (hipStream_t)stream, logits, row_stride, cols, out);
   }
   return launched("argmax_rows");
+}
+
+NIE_API int nie_rms_norm(int dtype, const void* x, int64_t x_stride, const void* residual,
+                         int64_t residual_stride, void* sum_out, int64_t sum_stride, const void* weight,
+                         void* out, int64_t out_stride, int64_t rows, int64_t cols, float eps, void* stream) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  const int64_t es = elt_bytes(dtype);
+  const int64_t per_vec = 16 / es;
+  if (rows < 0 || cols <= 0 || cols % per_vec != 0 || cols > kNormThreads * kNormVecsPerThread * per_vec) {
+    return fail(NIE_EUNSUPPORTED, "rms_norm: %lld columns (need a multiple of %lld, at most %lld)", (long long)cols,
+                (long long)per_vec, (long long)(kNormThreads * kNormVecsPerThread * per_vec));
+  }
+  if (rows == 0) return NIE_OK;
+  if (!x || !out || (residual != nullptr && !sum_out)) return fail(NIE_EINVAL, "null pointer argument");
+  if (!check_aligned(x, x_stride, 0, es) || !check_aligned(out, out_stride, 0, es) ||
+      (residual && (!check_aligned(residual, residual_stride, 0, es) || !check_aligned(sum_out, sum_stride, 0, es))) ||
+      (weight && ((uintptr_t)weight % 16))) {
+    return fail(NIE_EINVAL, "rms_norm: rows and weight must be 16-byte aligned");
+  }
+  if (x_stride < cols || out_stride < cols || (residual && (residual_stride < cols || sum_stride < cols))) {
+    return fail(NIE_EINVAL, "rms_norm: row strides shorter than the rows");
+  }
+  if (rows > 0x7fffffffLL) return fail(NIE_EINVAL, "too many rows");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NIE_DTYPE_BF16) {
+    hipLaunchKernelGGL(rms_norm_kernel<bf16_t>, dim3((unsigned)rows), dim3(kNormThreads), 0, s, x, x_stride, residual,
+                       residual_stride, sum_out, sum_stride, weight, out, out_stride, (int)cols, eps);
+  } else {
+    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)rows), dim3(kNormThreads), 0, s, x, x_stride, residual,
+                       residual_stride, sum_out, sum_stride, weight, out, out_stride, (int)cols, eps);
+  }
+  return launched("rms_norm");
+}
+
+NIE_API int nie_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  const int64_t per_vec = 16 / elt_bytes(dtype);
+  if (n < 0 || n % per_vec != 0) return fail(NIE_EUNSUPPORTED, "silu_mul: %lld elements (need a multiple of %lld)",
+                                             (long long)n, (long long)per_vec);
+  if (n == 0) return NIE_OK;
+  if (!gate || !up || !out) return fail(NIE_EINVAL, "null pointer argument");
+  if (((uintptr_t)gate % 16) || ((uintptr_t)up % 16) || ((uintptr_t)out % 16)) {
+    return fail(NIE_EINVAL, "silu_mul: buffers must be 16-byte aligned");
+  }
+  const int64_t nvec = n / per_vec;
+  const int64_t blocks = cdiv(nvec, (int64_t)256);
+  if (blocks > 0x7fffffffLL) return fail(NIE_EINVAL, "silu_mul: too many elements");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NIE_DTYPE_BF16) {
+    hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, out, nvec);
+  } else {
+    hipLaunchKernelGGL(silu_mul_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, out, nvec);
+  }
+  return launched("silu_mul");
 }
 
 NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,

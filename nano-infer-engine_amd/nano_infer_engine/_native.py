@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "nie_kv_copy_blocks",
     "nie_rope_kv_append",
     "nie_argmax_rows",
+    "nie_rms_norm",
+    "nie_silu_mul",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
@@ -76,6 +78,11 @@ _SIGNATURES = {
         ],
     ),
     "nie_argmax_rows": (_i32, [_i32, _ptr, _i64, _i64, _i64, _ptr, _ptr]),
+    "nie_rms_norm": (
+        _i32,
+        [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _f32, _ptr],
+    ),
+    "nie_silu_mul": (_i32, [_i32, _ptr, _ptr, _ptr, _i64, _ptr]),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
@@ -368,6 +375,79 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
                                         logits.stride(0) if rows > 1 else logits.shape[1], out.data_ptr(),
                                         _stream(logits.device))
     _check(rc, "nie_argmax_rows")
+    return out
+
+
+def _norm_rows(t: torch.Tensor, cols: int) -> torch.Tensor:
+    """t as (rows, cols) with unit column stride and 16-byte row strides (a view when possible)."""
+    t2 = t.reshape(-1, cols)
+    if t2.stride(1) != 1 or (t2.shape[0] > 1 and (t2.stride(0) * t2.element_size()) % 16):
+        t2 = t2.contiguous()
+    return t2
+
+
+def rms_norm_supported(x: torch.Tensor) -> bool:
+    """Whether nie_rms_norm / nie_silu_mul take x's dtype and row length."""
+    if x.dtype not in _DTYPE_CODES or x.ndim == 0:
+        return False
+    per_vec = 16 // x.element_size()
+    return x.shape[-1] % per_vec == 0 and 0 < x.shape[-1] <= 1024 * per_vec
+
+
+def silu_mul_supported(x: torch.Tensor) -> bool:
+    """Whether nie_silu_mul takes x's dtype and element count."""
+    return x.dtype in _DTYPE_CODES and x.numel() % (16 // x.element_size()) == 0
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float, residual: torch.Tensor | None = None):
+    """RMSNorm over the last dimension (``layers/rms_norm.py:25-31`` arithmetic, fp32 inside).
+
+    With ``residual`` returns ``(x + residual, norm(x + residual))``, the sum
+    rounded to x's dtype as torch's addition does; otherwise ``norm(x)``.
+    """
+    _require_gpu(x)
+    cols = x.shape[-1]
+    if not rms_norm_supported(x):
+        raise RuntimeError(f"nie_rms_norm does not take {x.dtype} rows of {cols} elements")
+    xs = _aligned(_norm_rows(x, cols))
+    rows = xs.shape[0]
+    out = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+    w = None
+    if weight is not None:
+        if weight.shape != (cols,) or weight.device != x.device or weight.dtype != x.dtype:
+            raise ValueError("weight must be a (cols,) tensor of x's dtype on the device of x")
+        w = _aligned(weight.detach().contiguous())
+    rs = sum_out = None
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != x.dtype or residual.device != x.device:
+            raise ValueError("residual must match x")
+        rs = _aligned(_norm_rows(residual, cols))
+        sum_out = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+    rc = load_library().nie_rms_norm(
+        dtype_code(x.dtype), xs.data_ptr(), xs.stride(0) if rows > 1 else cols,
+        None if rs is None else rs.data_ptr(), 0 if rs is None else (rs.stride(0) if rows > 1 else cols),
+        None if sum_out is None else sum_out.data_ptr(), cols,
+        None if w is None else w.data_ptr(), out.data_ptr(), cols, rows, cols, float(eps), _stream(x.device),
+    )
+    _check(rc, "nie_rms_norm")
+    if sum_out is None:
+        return out.view(x.shape)
+    return sum_out.view(x.shape), out.view(x.shape)
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up with torch's roundings (``layers/mlp.py:18-22``)."""
+    _require_gpu(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype or gate.device != up.device:
+        raise ValueError("gate and up must have the same shape, dtype and device")
+    if not silu_mul_supported(gate):
+        raise RuntimeError(f"nie_silu_mul does not take {gate.dtype} tensors of shape {tuple(gate.shape)}")
+    g = _aligned(gate.contiguous())
+    u = _aligned(up.contiguous())
+    out = torch.empty_like(g)
+    rc = load_library().nie_silu_mul(dtype_code(g.dtype), g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(),
+                                     _stream(g.device))
+    _check(rc, "nie_silu_mul")
     return out
 
 

@@ -20,8 +20,11 @@ class Llama3Decoder(nn.Module):
         self.pre_norm = RmsNorm(hidden_size, eps=norm_eps)
         self.post_norm = RmsNorm(hidden_size, eps=norm_eps)
 
-    def _mlp_residual(self, h):
-        return self.ffn(self.post_norm(h)) + h
+    def _mlp_residual(self, attn, x):
+        # h = attn + x, then ffn(post_norm(h)) + h; the add and the norm are
+        # one kernel on the GPU
+        h, normed = self.post_norm.forward_add(attn, x)
+        return self.ffn(normed) + h
 
     def forward(self, x, k_cache=None, v_cache=None, cache_position=0, attention_mask=None,
                 position_ids=None, *, paged_cache=None, layer_index=None, sequence_id="default",
@@ -31,7 +34,7 @@ class Llama3Decoder(nn.Module):
             paged_cache=paged_cache, layer_index=layer_index, sequence_id=sequence_id,
             sequence_ids=sequence_ids, paged_batch=paged_batch,
         )
-        return self._mlp_residual(attn + x)
+        return self._mlp_residual(attn, x)
 
     def forward_ragged(self, x, *, paged_cache, layer_index, sequence_ids, query_start_loc,
                        context_lengths, paged_batch=None):
@@ -40,9 +43,9 @@ class Llama3Decoder(nn.Module):
             sequence_ids=sequence_ids, query_start_loc=query_start_loc,
             context_lengths=context_lengths, paged_batch=paged_batch,
         )
-        return self._mlp_residual(attn + x)
+        return self._mlp_residual(attn, x)
 
     def forward_tokens(self, x, paged_cache, layer_index, batch):
         """Packed tokens (num_tokens, hidden) of a prebuilt ragged batch."""
         attn = self.attn.forward_tokens(self.pre_norm(x), paged_cache, layer_index, batch)
-        return self._mlp_residual(attn + x)
+        return self._mlp_residual(attn, x)

@@ -3,6 +3,8 @@
 import torch.nn.functional as F
 from torch import nn
 
+from nano_infer_engine import _native
+
 
 class SwiGLUMLP(nn.Module):
     def __init__(self, inner_size: int, hidden_size: int):
@@ -14,4 +16,8 @@ class SwiGLUMLP(nn.Module):
         self.gate_proj = nn.Linear(hidden_size, inner_size, bias=False)
 
     def forward(self, x):
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        gate, up = self.gate_proj(x), self.up_proj(x)
+        if gate.is_cuda and _native.silu_mul_supported(gate):
+            # silu(gate) * up in one HIP kernel (nie_silu_mul), torch's roundings
+            return self.down_proj(_native.silu_mul(gate, up))
+        return self.down_proj(F.silu(gate) * up)

@@ -457,3 +457,67 @@ def test_varlen_prefill_split_keys(q_heads, kv_heads, head_dim, block_size, dtyp
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")
     assert err <= TOL[dtype]
+
+
+def _rms_norm_reference(x, weight, eps):
+    """The reference's RmsNorm.forward arithmetic (layers/rms_norm.py:25-31), fp32 on the CPU."""
+    h = x.float()
+    h = h / torch.sqrt(torch.mean(torch.square(h), dim=-1, keepdim=True) + eps)
+    if weight is not None:
+        h = weight.float() * h
+    return h.to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (16, 2048), (37, 4096), (5, 64), (3, 8)])
+@pytest.mark.parametrize("with_weight", [True, False])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rms_norm_matches_reference_formula(dtype, rows, cols, with_weight, with_residual):
+    """nie_rms_norm against the reference formula in fp32 on the CPU: the
+    residual sum bit for bit; the normalised rows to one storage-dtype
+    rounding (the sum of squares is reduced in another order)."""
+    _log(f"rms_norm {dtype} rows={rows} cols={cols} weight={with_weight} residual={with_residual}")
+    gen = torch.Generator().manual_seed(rows * 1000 + cols)
+    x = (torch.randn((rows, cols), generator=gen) * 3).to(dtype)
+    res = (torch.randn((rows, cols), generator=gen)).to(dtype) if with_residual else None
+    w = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype) if with_weight else None
+    if res is not None:
+        s_got, got = _native.rms_norm(x.to(DEV), None if w is None else w.to(DEV), 1e-5, residual=res.to(DEV))
+        s_want = x + res
+        assert torch.equal(s_got.cpu(), s_want)
+        want = _rms_norm_reference(s_want, w, 1e-5)
+    else:
+        got = _native.rms_norm(x.to(DEV), None if w is None else w.to(DEV), 1e-5)
+        want = _rms_norm_reference(x, w, 1e-5)
+    torch.cuda.synchronize()
+    got = got.cpu().float()
+    want = want.float()
+    rel = 2.0**-7 if dtype == torch.bfloat16 else 1e-5
+    err = ((got - want).abs() / want.abs().clamp_min(1e-3)).max().item()
+    mism = (got != want).float().mean().item()
+    _log(f"  max_rel_err={err:.3e} mismatching={mism:.4f}")
+    assert err <= rel
+    if dtype == torch.bfloat16:
+        assert mism < 0.01
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_silu_mul_matches_reference_formula(dtype):
+    """nie_silu_mul against F.silu(gate) * up computed in fp32 on the CPU with
+    torch's roundings (silu rounded to the storage dtype, then the product)."""
+    _log(f"silu_mul {dtype}")
+    gen = torch.Generator().manual_seed(5)
+    g = (torch.randn((16, 8192), generator=gen) * 4).to(dtype)
+    u = torch.randn((16, 8192), generator=gen).to(dtype)
+    got = _native.silu_mul(g.to(DEV), u.to(DEV))
+    torch.cuda.synchronize()
+    want = (torch.nn.functional.silu(g.float()).to(dtype).float() * u.float()).to(dtype)
+    got = got.cpu().float()
+    want = want.float()
+    rel = 2.0**-7 if dtype == torch.bfloat16 else 1e-6
+    err = ((got - want).abs() / want.abs().clamp_min(1e-3)).max().item()
+    mism = (got != want).float().mean().item()
+    _log(f"  max_rel_err={err:.3e} mismatching={mism:.5f}")
+    assert err <= rel
+    if dtype == torch.bfloat16:
+        assert mism < 0.001
