@@ -19,7 +19,6 @@ class RequestStatus(str, Enum):
 class PagedRequest:
     sequence_id: str
     prompt: torch.Tensor
-    sequence: torch.Tensor = field(init=False)
     generated_tokens: int = 0
     finished: bool = False
     required_blocks: int = 0
@@ -27,6 +26,31 @@ class PagedRequest:
     prefill_offset: int = 0
     status: RequestStatus = RequestStatus.PENDING
     error: Exception | None = None
+    # the prompt and the tokens generated so far: a joined (1, n) prefix plus
+    # (1, 1) token views not yet joined (see `sequence`)
+    _joined: torch.Tensor | None = field(init=False, default=None, repr=False, compare=False)
+    _pending: list = field(init=False, default_factory=list, repr=False, compare=False)
 
     def __post_init__(self) -> None:
-        self.sequence = self.prompt
+        self._joined = self.prompt
+
+    @property
+    def sequence(self) -> torch.Tensor:
+        """The prompt followed by the generated tokens, (1, length).
+
+        Tokens appended by the scheduler are joined when this is read, in one
+        concatenation, instead of one device copy per token and step.
+        """
+        if self._pending:
+            self._joined = torch.cat((self._joined, *self._pending), dim=1)
+            self._pending = []
+        return self._joined
+
+    @sequence.setter
+    def sequence(self, value: torch.Tensor) -> None:
+        self._joined = value
+        self._pending = []
+
+    def append_token(self, token: torch.Tensor) -> None:
+        """Appends a generated token, a (1, 1) tensor (kept as given until `sequence` is read)."""
+        self._pending.append(token)

@@ -320,7 +320,7 @@ class ContinuousBatchingScheduler:
         events = tuple(TokenEvent(r.sequence_id, token_ids[i]) for i, r in enumerate(self.active_requests))
         for i, request in enumerate(self.active_requests):
             request.generated_tokens += 1
-            request.sequence = torch.cat((request.sequence, next_tokens[i : i + 1]), dim=1)
+            request.append_token(next_tokens[i : i + 1])
         return next_tokens, token_ids, events
 
     def _retire(self, token_ids: list[int], completed: list[PagedRequest]) -> list[int]:

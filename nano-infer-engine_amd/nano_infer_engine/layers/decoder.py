@@ -49,3 +49,20 @@ class Llama3Decoder(nn.Module):
         """Packed tokens (num_tokens, hidden) of a prebuilt ragged batch."""
         attn = self.attn.forward_tokens(self.pre_norm(x), paged_cache, layer_index, batch)
         return self._mlp_residual(attn, x)
+
+    def forward_tokens_unsummed(self, x, paged_cache, layer_index, batch):
+        """forward_tokens with the block's last residual add left to the caller.
+
+        ``x`` is the block input, or a pair ``(a, b)`` standing for ``a + b``
+        (the previous block's unsummed output): the add then happens inside
+        this block's pre-attention norm (one kernel on the GPU).  Returns
+        ``(ffn_out, h)``, whose sum ``ffn_out + h`` is the block's output
+        (reference ``layers/decoder.py:50-51``).
+        """
+        if isinstance(x, tuple):
+            x, normed = self.pre_norm.forward_add(*x)
+        else:
+            normed = self.pre_norm(x)
+        attn = self.attn.forward_tokens(normed, paged_cache, layer_index, batch)
+        h, normed = self.post_norm.forward_add(attn, x)
+        return self.ffn(normed), h

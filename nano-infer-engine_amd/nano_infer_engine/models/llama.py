@@ -134,11 +134,16 @@ class Llama3_2(nn.Module):
         and the LM head.
         """
         x = self.embed(input_ids)
+        # each block's output stays an unsummed pair (ffn_out, h); the next
+        # norm adds it (one kernel for the add and the norm on the GPU)
         for layer_index, decoder in enumerate(self.decoders):
-            x = decoder.forward_tokens(x, cache, layer_index, batch)
+            x = decoder.forward_tokens_unsummed(x, cache, layer_index, batch)
+        if not isinstance(x, tuple):  # no layers
+            x = (x, torch.zeros_like(x))
+        ffn_out, h = x
         if logits_rows is not None:
-            x = x[logits_rows]
-        return self.lm_head(self.final_rms(x))
+            ffn_out, h = ffn_out[logits_rows], h[logits_rows]
+        return self.lm_head(self.final_rms.forward_add(ffn_out, h)[1])
 
     def _new_cache_for(self, batch_size: int, seq_len: int, device: torch.device) -> tuple[PagedKVCache, tuple[str, ...]]:
         block_size = 16
