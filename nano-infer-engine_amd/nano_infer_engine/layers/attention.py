@@ -19,6 +19,7 @@ Dense (contiguous-cache) attention is not part of this build.
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from nano_infer_engine.layers.rope import Rope
@@ -47,6 +48,29 @@ class GroupedQueryAttention(nn.Module):
         self.v_proj = nn.Linear(hidden_size, kv_head_num * self.head_dim, bias=False)
         self.o_proj = nn.Linear(hidden_size, hidden_size, bias=False)
         self.rope = Rope(self.head_dim) if rope is None else rope
+        # [q; k; v] weight rows for one projection GEMM on the GPU, rebuilt
+        # whenever one of the three weights is replaced or modified
+        self._qkv_weight: torch.Tensor | None = None
+        self._qkv_key: tuple | None = None
+
+    def _project_qkv(self, x: torch.Tensor):
+        """q, k, v = q_proj(x), k_proj(x), v_proj(x) (``layers/attention.py:227-238``, ``:359-361``).
+
+        On the GPU without autograd this is one GEMM over the concatenated
+        weights; q, k and v are then column slices of its output.  A captured
+        decode graph keeps the concatenation it was captured with (weights
+        changed afterwards need a new capture, as any captured weight would).
+        """
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        if not x.is_cuda or (torch.is_grad_enabled() and any(w.requires_grad for w in ws)):
+            return self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        if key != self._qkv_key:
+            with torch.no_grad():
+                self._qkv_weight = torch.cat(ws, dim=0)
+            self._qkv_key = key
+        qkv = F.linear(x, self._qkv_weight)
+        return qkv.split((ws[0].shape[0], ws[1].shape[0], ws[2].shape[0]), dim=-1)
 
     # ------------------------------------------------------------------
     def forward_tokens(
@@ -58,9 +82,10 @@ class GroupedQueryAttention(nn.Module):
     ) -> torch.Tensor:
         """Attention for packed tokens x (num_tokens, hidden) described by ``batch``."""
         tokens = x.shape[0]
-        q = self.q_proj(x).view(tokens, self.q_head_num, self.head_dim)
-        k = self.k_proj(x).view(tokens, self.kv_head_num, self.head_dim)
-        v = self.v_proj(x).view(tokens, self.kv_head_num, self.head_dim)
+        q, k, v = self._project_qkv(x)
+        q = q.view(tokens, self.q_head_num, self.head_dim)
+        k = k.view(tokens, self.kv_head_num, self.head_dim)
+        v = v.view(tokens, self.kv_head_num, self.head_dim)
         context = attention_core(q, k, v, paged_cache, layer_index, batch, self.head_dim**-0.5, self.rope)
         return self.o_proj(context.view(tokens, self.hidden_size))
 

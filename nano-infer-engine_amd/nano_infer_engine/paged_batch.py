@@ -207,7 +207,10 @@ def attention_core(
 
 
 def _rows(t: torch.Tensor) -> torch.Tensor:
-    """``t`` if it is contiguous with a 16-byte aligned start, else an aligned copy."""
-    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+    """``t`` if its last dimension is contiguous and its start and other strides
+    are 16-byte multiples (a column slice of a fused projection qualifies),
+    else an aligned contiguous copy."""
+    es = t.element_size()
+    if t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((st * es) % 16 == 0 for st in t.stride()[:-1]):
         return t
     return t.clone(memory_format=torch.contiguous_format)
