@@ -166,14 +166,17 @@ int nie_rms_norm(int dtype, const void* x, int64_t x_stride,
                  int64_t rows, int64_t cols, float eps, void* stream);
 
 /*
- * SwiGLU's gated product over n contiguous elements: out = silu(gate) * up,
+ * SwiGLU's gated product over rows x cols elements: out = silu(gate) * up,
  * silu(x) = x / (1 + exp(-x)) in fp32 rounded to the storage dtype, then the
- * product in fp32 rounded again (torch's two kernels).  n must be a multiple
- * of 16 bytes' worth of elements; buffers 16-byte aligned.
+ * product in fp32 rounded again (torch's two kernels).  Row r of each
+ * operand starts at r * stride elements (gate and up may be the two halves
+ * of one fused gate/up projection's output); rows 16-byte aligned and cols a
+ * multiple of 16 bytes' worth of elements.
  * Replaces: F.silu(self.gate_proj(x)) * self.up_proj(x)
  *           (src/nano_infer_engine/layers/mlp.py:18-22).
  */
-int nie_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream);
+int nie_silu_mul(int dtype, const void* gate, int64_t gate_stride, const void* up, int64_t up_stride,
+                 void* out, int64_t out_stride, int64_t rows, int64_t cols, void* stream);
 
 /*
  * Greedy token selection: out[r] = index of the largest of the cols values

@@ -1033,15 +1033,20 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const void* x, i
 
 // SwiGLU's product silu(gate) * up (layers/mlp.py:18-22) as torch computes
 // it in two kernels: s = silu(gate) in fp32, x / (1 + exp(-x)), rounded to
-// the storage dtype, then s * up in fp32, rounded again.  One 16-byte vector
-// per thread.
+// the storage dtype, then s * up in fp32, rounded again.  Rows of `cols`
+// elements at element strides (gate and up may be the two halves of one
+// fused projection's output); one 16-byte vector per thread.
 template <typename T>
-__global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate, const void* up, void* out, int64_t nvec) {
+__global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate, int64_t gate_stride, const void* up,
+                                                       int64_t up_stride, void* out, int64_t out_stride,
+                                                       int64_t vecs_per_row, int64_t nvec) {
   constexpr int kPerVec = 16 / Elt<T>::kBytes;
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= nvec) return;
-  const v4u g = reinterpret_cast<const v4u*>(gate)[j];
-  const v4u u = reinterpret_cast<const v4u*>(up)[j];
+  const int64_t r = j / vecs_per_row;
+  const int64_t c = (j - r * vecs_per_row) * kPerVec;
+  const v4u g = *reinterpret_cast<const v4u*>(reinterpret_cast<const T*>(gate) + r * gate_stride + c);
+  const v4u u = *reinterpret_cast<const v4u*>(reinterpret_cast<const T*>(up) + r * up_stride + c);
   float y[kPerVec];
 #pragma unroll
   for (int e = 0; e < kPerVec; ++e) {
@@ -1058,7 +1063,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate, const v
 #pragma unroll
     for (int w = 0; w < 4; ++w) o[w] = __float_as_uint(y[w]);
   }
-  reinterpret_cast<v4u*>(out)[j] = o;
+  *reinterpret_cast<v4u*>(reinterpret_cast<T*>(out) + r * out_stride + c) = o;
 }
 
 // Merges nsplit split partials of one output row, one wave.  Split s of the
@@ -2872,25 +2877,36 @@ NIE_API int nie_rms_norm(int dtype, const void* x, int64_t x_stride, const void*
   return launched("rms_norm");
 }
 
-NIE_API int nie_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream) {
+NIE_API int nie_silu_mul(int dtype, const void* gate, int64_t gate_stride, const void* up, int64_t up_stride,
+                         void* out, int64_t out_stride, int64_t rows, int64_t cols, void* stream) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
-  const int64_t per_vec = 16 / elt_bytes(dtype);
-  if (n < 0 || n % per_vec != 0) return fail(NIE_EUNSUPPORTED, "silu_mul: %lld elements (need a multiple of %lld)",
-                                             (long long)n, (long long)per_vec);
-  if (n == 0) return NIE_OK;
-  if (!gate || !up || !out) return fail(NIE_EINVAL, "null pointer argument");
-  if (((uintptr_t)gate % 16) || ((uintptr_t)up % 16) || ((uintptr_t)out % 16)) {
-    return fail(NIE_EINVAL, "silu_mul: buffers must be 16-byte aligned");
+  const int64_t es = elt_bytes(dtype);
+  const int64_t per_vec = 16 / es;
+  if (rows < 0 || cols <= 0 || cols % per_vec != 0) {
+    return fail(NIE_EUNSUPPORTED, "silu_mul: rows of %lld elements (need a multiple of %lld)", (long long)cols,
+                (long long)per_vec);
   }
-  const int64_t nvec = n / per_vec;
+  if (rows == 0) return NIE_OK;
+  if (!gate || !up || !out) return fail(NIE_EINVAL, "null pointer argument");
+  if (!check_aligned(gate, gate_stride, 0, es) || !check_aligned(up, up_stride, 0, es) ||
+      !check_aligned(out, out_stride, 0, es)) {
+    return fail(NIE_EINVAL, "silu_mul: rows must be 16-byte aligned");
+  }
+  if ((rows > 1 && (gate_stride < cols || up_stride < cols || out_stride < cols))) {
+    return fail(NIE_EINVAL, "silu_mul: row strides shorter than the rows");
+  }
+  const int64_t vecs_per_row = cols / per_vec;
+  const int64_t nvec = rows * vecs_per_row;
   const int64_t blocks = cdiv(nvec, (int64_t)256);
   if (blocks > 0x7fffffffLL) return fail(NIE_EINVAL, "silu_mul: too many elements");
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, out, nvec);
+    hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, s, gate, gate_stride, up,
+                       up_stride, out, out_stride, vecs_per_row, nvec);
   } else {
-    hipLaunchKernelGGL(silu_mul_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, out, nvec);
+    hipLaunchKernelGGL(silu_mul_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, gate, gate_stride, up,
+                       up_stride, out, out_stride, vecs_per_row, nvec);
   }
   return launched("silu_mul");
 }

@@ -82,7 +82,7 @@ _SIGNATURES = {
         _i32,
         [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _f32, _ptr],
     ),
-    "nie_silu_mul": (_i32, [_i32, _ptr, _ptr, _ptr, _i64, _ptr]),
+    "nie_silu_mul": (_i32, [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
@@ -395,8 +395,8 @@ def rms_norm_supported(x: torch.Tensor) -> bool:
 
 
 def silu_mul_supported(x: torch.Tensor) -> bool:
-    """Whether nie_silu_mul takes x's dtype and element count."""
-    return x.dtype in _DTYPE_CODES and x.numel() % (16 // x.element_size()) == 0
+    """Whether nie_silu_mul takes x's dtype and row length."""
+    return x.dtype in _DTYPE_CODES and x.ndim > 0 and x.shape[-1] % (16 // x.element_size()) == 0
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float, residual: torch.Tensor | None = None):
@@ -436,19 +436,26 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float, residual:
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
-    """silu(gate) * up with torch's roundings (``layers/mlp.py:18-22``)."""
+    """silu(gate) * up with torch's roundings (``layers/mlp.py:18-22``).
+
+    gate and up may be row-strided views (the halves of a fused gate/up
+    projection's output); the result is contiguous.
+    """
     _require_gpu(gate, up)
     if gate.shape != up.shape or gate.dtype != up.dtype or gate.device != up.device:
         raise ValueError("gate and up must have the same shape, dtype and device")
     if not silu_mul_supported(gate):
         raise RuntimeError(f"nie_silu_mul does not take {gate.dtype} tensors of shape {tuple(gate.shape)}")
-    g = _aligned(gate.contiguous())
-    u = _aligned(up.contiguous())
-    out = torch.empty_like(g)
-    rc = load_library().nie_silu_mul(dtype_code(g.dtype), g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(),
-                                     _stream(g.device))
+    cols = gate.shape[-1]
+    g = _aligned(_norm_rows(gate, cols))
+    u = _aligned(_norm_rows(up, cols))
+    rows = g.shape[0]
+    out = torch.empty((rows, cols), dtype=gate.dtype, device=gate.device)
+    rc = load_library().nie_silu_mul(dtype_code(g.dtype), g.data_ptr(), g.stride(0) if rows > 1 else cols,
+                                     u.data_ptr(), u.stride(0) if rows > 1 else cols, out.data_ptr(), cols, rows,
+                                     cols, _stream(g.device))
     _check(rc, "nie_silu_mul")
-    return out
+    return out.view(gate.shape)
 
 
 def kv_gather(

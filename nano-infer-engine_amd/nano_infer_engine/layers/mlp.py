@@ -1,5 +1,6 @@
 """SwiGLU feed-forward block (``layers/mlp.py:18-22`` of the reference)."""
 
+import torch
 import torch.nn.functional as F
 from torch import nn
 
@@ -14,10 +15,24 @@ class SwiGLUMLP(nn.Module):
         self.down_proj = nn.Linear(inner_size, hidden_size, bias=False)
         self.up_proj = nn.Linear(hidden_size, inner_size, bias=False)
         self.gate_proj = nn.Linear(hidden_size, inner_size, bias=False)
+        # [gate; up] weight rows for one projection GEMM on the GPU, rebuilt
+        # whenever either weight is replaced or modified
+        self._gate_up_weight: torch.Tensor | None = None
+        self._gate_up_key: tuple | None = None
 
     def forward(self, x):
-        gate, up = self.gate_proj(x), self.up_proj(x)
-        if gate.is_cuda and _native.silu_mul_supported(gate):
-            # silu(gate) * up in one HIP kernel (nie_silu_mul), torch's roundings
-            return self.down_proj(_native.silu_mul(gate, up))
-        return self.down_proj(F.silu(gate) * up)
+        ws = (self.gate_proj.weight, self.up_proj.weight)
+        if x.is_cuda and not (torch.is_grad_enabled() and any(w.requires_grad for w in ws)):
+            # one GEMM over the concatenated weights (a captured decode graph
+            # keeps the concatenation it was captured with), then
+            # silu(gate) * up in one HIP kernel over the two halves
+            key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+            if key != self._gate_up_key:
+                with torch.no_grad():
+                    self._gate_up_weight = torch.cat(ws, dim=0)
+                self._gate_up_key = key
+            gate, up = F.linear(x, self._gate_up_weight).split((ws[0].shape[0], ws[1].shape[0]), dim=-1)
+            if _native.silu_mul_supported(gate):
+                return self.down_proj(_native.silu_mul(gate, up))
+            return self.down_proj(F.silu(gate) * up)
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))

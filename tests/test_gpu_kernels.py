@@ -502,14 +502,22 @@ def test_rms_norm_matches_reference_formula(dtype, rows, cols, with_weight, with
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_silu_mul_matches_reference_formula(dtype):
+@pytest.mark.parametrize("halves", [False, True])
+def test_silu_mul_matches_reference_formula(dtype, halves):
     """nie_silu_mul against F.silu(gate) * up computed in fp32 on the CPU with
-    torch's roundings (silu rounded to the storage dtype, then the product)."""
-    _log(f"silu_mul {dtype}")
+    torch's roundings (silu rounded to the storage dtype, then the product);
+    halves: gate and up are the two column halves of one (16, 16384) tensor,
+    as a fused gate/up projection produces them."""
+    _log(f"silu_mul {dtype} halves={halves}")
     gen = torch.Generator().manual_seed(5)
     g = (torch.randn((16, 8192), generator=gen) * 4).to(dtype)
     u = torch.randn((16, 8192), generator=gen).to(dtype)
-    got = _native.silu_mul(g.to(DEV), u.to(DEV))
+    if halves:
+        gu = torch.cat((g, u), dim=1).to(DEV)
+        dg, du = gu.split((8192, 8192), dim=1)
+    else:
+        dg, du = g.to(DEV), u.to(DEV)
+    got = _native.silu_mul(dg, du)
     torch.cuda.synchronize()
     want = (torch.nn.functional.silu(g.float()).to(dtype).float() * u.float()).to(dtype)
     got = got.cpu().float()
