@@ -262,16 +262,23 @@ int nie_paged_decode(int dtype,
  * that slot (the block of a sequence's newest token is its own).  A table
  * entry outside [0, num_blocks) skips the write, as an out-of-range slot
  * skips nie_kv_append.  Workspace: nie_paged_decode_workspace_bytes.
+ * With cos_table / sin_table ((table_rows, head_dim / 2) in the storage
+ * dtype; NULL: none), q and the new K rows are first rotated at position
+ * seq_lens[b] - 1 exactly as nie_rope_kv_append rotates them (q is not
+ * written back), so the call equals nie_rope_kv_append then
+ * nie_paged_decode on a decode-only batch.
  * Replaces: the decode step of GroupedQueryAttention.forward's paged branch
  *           (src/nano_infer_engine/layers/attention.py:246-269): one
  *           PagedKVCache.write per sequence at its cached length
  *           (paged_cache.py:264-322), then batched_paged_attention_reference
- *           with lengths + 1.
+ *           with lengths + 1; with the tables also the RoPE of q and k before
+ *           it (attention.py:238-239, layers/rope.py:171-200).
  */
 int nie_paged_decode_append(int dtype,
                             const void* q, int64_t q_stride_b, int64_t q_stride_h,
                             const void* k_new, int64_t k_new_stride,
                             const void* v_new, int64_t v_new_stride,
+                            const void* cos_table, const void* sin_table, int64_t table_rows,
                             void* k_cache, void* v_cache,
                             int64_t num_layers, int64_t layer_index,
                             int64_t num_blocks, int64_t block_size,

@@ -805,6 +805,11 @@ struct DecodeArgs {
   const void* k_new = nullptr;
   const void* v_new = nullptr;
   int64_t kn_s = 0, vn_s = 0;
+  // RoPE of q and of the new K rows at position seq_len - 1 (fused append
+  // only): cos / sin tables (rope_rows, head_dim / 2); nullptr: none
+  const void* rope_cos = nullptr;
+  const void* rope_sin = nullptr;
+  int64_t rope_rows = 0;
 };
 
 // Work items of a decode call planned from host copies of the lengths,
@@ -1066,6 +1071,40 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate, int64_t
   *reinterpret_cast<v4u*>(reinterpret_cast<T*>(out) + r * out_stride + c) = o;
 }
 
+// Floats -> one 16-byte vector of T (round to nearest even for bf16).
+template <typename T>
+__device__ __forceinline__ v4u pack_vec(const float (&y)[16 / Elt<T>::kBytes]) {
+  v4u o;
+  if constexpr (Elt<T>::kIsBf16) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = pack_bf16x2(y[2 * w], y[2 * w + 1]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = __float_as_uint(y[w]);
+  }
+  return o;
+}
+
+// RoPE of 16-byte vectors: lo holds dims i..i+E-1 of the first half of a
+// head, hi the same dims of the second half, c / s the cos / sin table
+// entries of dims i.. at the token's position.  The arithmetic is
+// rope_kv_append_kernel's (every product and sum rounded to T on its own):
+// lo' = lo*c - hi*s, hi' = hi*c + lo*s.
+template <typename T>
+__device__ __forceinline__ void rope_vec(v4u& lo, v4u& hi, const v4u& c, const v4u& s) {
+  constexpr int kE = 16 / Elt<T>::kBytes;
+  float nlo[kE], nhi[kE];
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    const float x1 = vec_elt<T>(lo, e), x2 = vec_elt<T>(hi, e);
+    const float cc = vec_elt<T>(c, e), ss = vec_elt<T>(s, e);
+    nlo[e] = sub_t<T>(mul_t<T>(x1, cc), mul_t<T>(x2, ss));
+    nhi[e] = add_t<T>(mul_t<T>(x2, cc), mul_t<T>(x1, ss));
+  }
+  lo = pack_vec<T>(nlo);
+  hi = pack_vec<T>(nhi);
+}
+
 // Merges nsplit split partials of one output row, one wave.  Split s of the
 // row has its unnormalised O row at po + s*po_stride and its (max, sum) pair
 // at ml + s*ml_stride.  The lanes form kSplitsPerPass groups of D/4 lanes; a
@@ -1232,6 +1271,28 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   }
   bool carry = false;  // set at the last tile: the chunk goes to new_dst
   T* new_dst = nullptr;
+  // RoPE (with the fused append): this lane's cos / sin vectors for the
+  // first-half dims of its q vectors, and for its new K chunk's dims
+  const bool rope = a.rope_cos != nullptr && a.k_new != nullptr;
+  constexpr int kQHalf = F::kVec / 2;
+  v4u q_cos[kQHalf], q_sin[kQHalf], k_cos = v4u{0u, 0u, 0u, 0u}, k_sin = v4u{0u, 0u, 0u, 0u};
+  if (rope) {
+    int64_t pos = seq_len - 1;
+    pos = pos >= a.rope_rows ? a.rope_rows - 1 : pos;
+    const T* crow = reinterpret_cast<const T*>(a.rope_cos) + pos * (D / 2);
+    const T* srow = reinterpret_cast<const T*>(a.rope_sin) + pos * (D / 2);
+#pragma unroll
+    for (int j = 0; j < kQHalf; ++j) {
+      const int d0 = (64 * j + 16 * (lane >> 4)) / Elt<T>::kBytes;  // first dim of q vector j
+      q_cos[j] = *reinterpret_cast<const v4u*>(crow + d0);
+      q_sin[j] = *reinterpret_cast<const v4u*>(srow + d0);
+    }
+    if (carrier && carries_k) {
+      const int d0 = (new_c % (kHeadChunks / 2)) * kEltPerChunk;
+      k_cos = *reinterpret_cast<const v4u*>(crow + d0);
+      k_sin = *reinterpret_cast<const v4u*>(srow + d0);
+    }
+  }
 
   TableCache tc;
   if constexpr (kUniform) tc.load(table, tlen, key_begin >> a.geom.bs_shift);
@@ -1330,6 +1391,31 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   constexpr int kAhead = kStages - 1;
 #pragma unroll
   for (int j = 0; j < kAhead; ++j) issue(j, min(key_begin + j * kTileKeys, last_key0));
+  if (rope) {
+    // rotate q (vector j pairs with vector j + kVec/2: dims i and i + D/2)
+    // while the first tiles are in flight
+    if (row_valid) {
+#pragma unroll
+      for (int j = 0; j < kQHalf; ++j) {
+        v4u lo = __builtin_bit_cast(v4u, qf.v[j]), hi = __builtin_bit_cast(v4u, qf.v[j + kQHalf]);
+        rope_vec<T>(lo, hi, q_cos[j], q_sin[j]);
+        qf.v[j] = __builtin_bit_cast(uint4, lo);
+        qf.v[j + kQHalf] = __builtin_bit_cast(uint4, hi);
+      }
+    }
+    if (appender) {
+      // K chunk c pairs with chunk c + kHeadChunks/2 (lane xor kHeadChunks/2)
+      v4u other;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) other[w] = (uint32_t)__shfl_xor((int)new_chunk[w], kHeadChunks / 2);
+      if (carrier && carries_k) {
+        const bool first_half = new_c < kHeadChunks / 2;
+        v4u lo = first_half ? new_chunk : other, hi = first_half ? other : new_chunk;
+        rope_vec<T>(lo, hi, k_cos, k_sin);
+        new_chunk = first_half ? lo : hi;
+      }
+    }
+  }
   for (int t = 0; t < ntiles; t += kStages) {
 #pragma unroll
     for (int j = 0; j < kStages; ++j) {
@@ -1364,11 +1450,17 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
           new_dst = cache + a.geom.layer_offset + ((int64_t)phys * a.geom.block_size + off) * a.geom.row_elems +
                     h * D + new_c * kEltPerChunk;
           carry = true;
-          const uint32_t patch = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)GT::kBytes) +
-                                 (uint32_t)GT::chunk_offset(pos - key_begin - tt * kTileKeys,
-                                                            wave * kHeadChunks + new_c);
-          // the wait + barrier above ordered the tile's DMA before this write
-          asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(patch), "v"(new_chunk) : "memory");
+          // The rows after the new token's were read from its slot too (reads
+          // past the split's last key clamp to it; those keys are masked,
+          // but their V rows still meet p = 0 in the P.V MFMAs, so they must
+          // hold the new row, not the slot's old content).  The wait +
+          // barrier above ordered the tile's DMA before these writes.
+          const uint32_t base = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)GT::kBytes);
+          for (int rr = pos - key_begin - tt * kTileKeys; rr < kTileKeys; ++rr) {
+            const uint32_t patch = base + (uint32_t)GT::chunk_offset(rr, wave * kHeadChunks + new_c);
+            asm volatile("ds_write_b128 %0, %1" : : "v"(patch), "v"(new_chunk) : "memory");
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -2932,6 +3024,9 @@ struct DecodeAppend {
   int64_t k_stride = 0;
   const void* v_new = nullptr;
   int64_t v_stride = 0;
+  const void* cos_table = nullptr;  // RoPE tables (table_rows, head_dim / 2); nullptr: no RoPE
+  const void* sin_table = nullptr;
+  int64_t table_rows = 0;
 };
 
 int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
@@ -2975,6 +3070,14 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
         !check_aligned(append.v_new, append.v_stride, head_dim, es)) {
       return fail(NIE_EINVAL, "new K/V rows must be 16-byte aligned (batch, kv_heads, head_dim) rows");
     }
+    if (append.cos_table != nullptr || append.sin_table != nullptr) {
+      if (!append.cos_table || !append.sin_table || append.table_rows <= 0) {
+        return fail(NIE_EINVAL, "RoPE needs both tables and at least one row");
+      }
+      if (((uintptr_t)append.cos_table % 16) || ((uintptr_t)append.sin_table % 16)) {
+        return fail(NIE_EINVAL, "RoPE tables must be 16-byte aligned");
+      }
+    }
   }
   const DecodePlan plan = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
   const int64_t tps = plan.tps;
@@ -3012,6 +3115,9 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   a.v_new = append.v_new;
   a.kn_s = append.k_stride;
   a.vn_s = append.v_stride;
+  a.rope_cos = append.cos_table;
+  a.rope_sin = append.sin_table;
+  a.rope_rows = append.table_rows;
   // The grid is an upper bound on the item count (exact to within `batch`);
   // workgroups past the last real item return immediately.
   DecodeItems work;
@@ -3046,7 +3152,8 @@ NIE_API int nie_paged_decode(int dtype, const void* q, int64_t q_stride_b, int64
 
 NIE_API int nie_paged_decode_append(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
                                     const void* k_new, int64_t k_new_stride, const void* v_new,
-                                    int64_t v_new_stride, void* k_cache, void* v_cache, int64_t num_layers,
+                                    int64_t v_new_stride, const void* cos_table, const void* sin_table,
+                                    int64_t table_rows, void* k_cache, void* v_cache, int64_t num_layers,
                                     int64_t layer_index, int64_t num_blocks, int64_t block_size,
                                     int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                                     const int32_t* block_tables, int64_t table_stride,
@@ -3060,6 +3167,9 @@ NIE_API int nie_paged_decode_append(int dtype, const void* q, int64_t q_stride_b
   append.k_stride = k_new_stride;
   append.v_new = v_new;
   append.v_stride = v_new_stride;
+  append.cos_table = cos_table;
+  append.sin_table = sin_table;
+  append.table_rows = table_rows;
   return paged_decode_call(dtype, q, q_stride_b, q_stride_h, k_cache, v_cache, num_layers, layer_index, num_blocks,
                            block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
                            max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, workspace,

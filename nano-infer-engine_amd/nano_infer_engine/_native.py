@@ -104,6 +104,7 @@ _SIGNATURES = {
         [
             _i32, _ptr, _i64, _i64,          # dtype, q, q strides
             _ptr, _i64, _ptr, _i64,          # new K rows, stride, new V rows, stride
+            _ptr, _ptr, _i64,                # RoPE cos / sin tables, rows
             _ptr, _ptr,                      # caches
             _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
             _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
@@ -546,6 +547,7 @@ def paged_decode(
     out: torch.Tensor | None = None,
     seq_lens_host=None,
     new_kv: tuple[torch.Tensor, torch.Tensor] | None = None,
+    rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Decode attention of query (B, Hq, D) over each sequence's first seq_lens[b] tokens.
 
@@ -559,6 +561,9 @@ def paged_decode(
     writes row b at position seq_lens[b] - 1 (the slot its block table
     gives), as the decode step of ``GroupedQueryAttention.forward`` writes
     the new token before attending (reference ``layers/attention.py:246-269``).
+    ``rope_tables=(cos, sin)``, each (rows, D/2) in the storage dtype (with
+    ``new_kv`` only): q and the new K rows are first rotated at that position
+    as ``rope_kv_append`` rotates them; q itself is not modified.
     """
     num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
     _require_gpu(query, block_tables, seq_lens)
@@ -587,12 +592,16 @@ def paged_decode(
     )
     stream = _stream(query.device)
     workspace = _decode_workspace(query.device, stream, ws_bytes)
+    if rope_tables is not None and new_kv is None:
+        raise ValueError("rope_tables applies to the fused append (new_kv)")
     if new_kv is not None:
         keys, values = _check_new_rows(new_kv, batch, kv_heads, head_dim, query.dtype, query.device)
+        cos, sin, rows = _check_rope_tables(rope_tables, head_dim, query.dtype, query.device)
         rc = lib.nie_paged_decode_append(
             dtype_code(query.dtype),
             query.data_ptr(), query.stride(0), query.stride(1),
             keys.data_ptr(), keys.stride(0), values.data_ptr(), values.stride(0),
+            cos, sin, rows,
             k_cache.data_ptr(), v_cache.data_ptr(),
             num_layers, layer_index, num_blocks, block_size,
             q_heads, kv_heads, head_dim,
@@ -622,6 +631,20 @@ def paged_decode(
     )
     _check(rc, "nie_paged_decode")
     return out
+
+
+def _check_rope_tables(rope_tables, head_dim: int, dtype, device):
+    """(cos pointer, sin pointer, rows) of optional RoPE tables, (rows, head_dim/2) each; (None, None, 0) without."""
+    if rope_tables is None:
+        return None, None, 0
+    cos, sin = rope_tables
+    for t in (cos, sin):
+        if (t.dtype != dtype or t.device != device or t.ndim != 2 or t.shape[1] != head_dim // 2
+                or not t.is_contiguous() or t.data_ptr() % 16 or t.shape[0] == 0):
+            raise ValueError("RoPE tables must be contiguous, aligned (rows, head_dim / 2) tensors of the query dtype")
+    if cos.shape != sin.shape:
+        raise ValueError("RoPE cos and sin tables must have the same shape")
+    return cos.data_ptr(), sin.data_ptr(), cos.shape[0]
 
 
 def _check_new_rows(new_kv, batch: int, kv_heads: int, head_dim: int, dtype, device):
@@ -839,18 +862,24 @@ class PreparedDecode:
         return out
 
     def append_decode(self, query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, layer_index: int,
-                      out: torch.Tensor) -> torch.Tensor:
-        """Writes keys/values row b at position seq_lens[b] - 1, then decodes, in one launch."""
+                      out: torch.Tensor, rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None) -> torch.Tensor:
+        """Writes keys/values row b at position seq_lens[b] - 1, then decodes, in one launch.
+
+        With ``rope_tables=(cos, sin)`` q and the new keys are rotated at that
+        position first (``rope_kv_append``'s arithmetic; q is not modified).
+        """
         for t in (query, out):
             if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
                     or t.data_ptr() % 16):
                 raise ValueError("query/out must be aligned (batch, q_heads, head_dim) tensors matching the batch")
         _check_new_rows((keys, values), *self._kv_shape, self._dtype, self._device)
+        cos, sin, rows = _check_rope_tables(rope_tables, self._kv_shape[2], self._dtype, self._device)
         kptr, vptr, num_layers = self._mid
         (num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch, max_len, total_len,
          scale, (ws, ws_bytes, hlens, stream)) = self._post
         rc = self._fn_append(self._pre[0], query.data_ptr(), query.stride(0), query.stride(1), keys.data_ptr(),
-                             keys.stride(0), values.data_ptr(), values.stride(0), kptr, vptr, num_layers, layer_index,
+                             keys.stride(0), values.data_ptr(), values.stride(0), cos, sin, rows, kptr, vptr,
+                             num_layers, layer_index,
                              num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch,
                              max_len, total_len, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes,
                              hlens, stream)

@@ -76,8 +76,11 @@ class DecodeGraphRunner:
         ints = torch.zeros(b * width + 2 * b, dtype=torch.int32, device=self.device)
         longs = torch.zeros(3 * b + 1, dtype=torch.int64, device=self.device)
         ids = torch.zeros(b, dtype=torch.int64, device=self.device)
-        # capture-time contents: every slot -1 (the K/V writes are skipped),
-        # length-1 sequences over block 0, position 0
+        # capture-time contents: length-1 sequences at position 0 whose
+        # table entries lie outside the pool and whose slots are -1, so the
+        # K/V writes of the warm-up and capture runs are skipped (the fused
+        # decode derives its slot from the table; reads clamp into the pool)
+        ints[: b * width] = cache.keys.shape[1]
         ints[b * width :] = 1
         ints[b * width : b * width + b] = 0
         longs[:b] = -1

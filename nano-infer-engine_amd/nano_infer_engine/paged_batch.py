@@ -73,7 +73,7 @@ class RaggedBatch:
         return max(c + n for c, n in zip(self.context_lens, self.query_lens))
 
     def launchers(self, cache: PagedKVCache, q_heads: int, scale: float, rope):
-        """(rope + append, prefill or None, decode or None) launches of this batch on ``cache``.
+        """(rope + append, prefill or None, decode or None, (cos, sin)) of this batch on ``cache``.
 
         Built once and reused by every layer: the cache pointers, metadata,
         sin/cos tables, launch plan, workspace and stream are resolved here,
@@ -103,7 +103,7 @@ class RaggedBatch:
                 cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], self.decode_bound,
                 rows * self.decode_bound, q_heads, scale,
             )
-        found = (append, prefill, decode)
+        found = (append, prefill, decode, (cos, sin))
         self._launch[key] = found
         return found
 
@@ -194,8 +194,13 @@ def attention_core(
     place; every new token then attends to its sequence's cached prefix and,
     causally, to the new tokens before it (``layers/attention.py:378-411``).
     """
-    append, prefill, decode = batch.launchers(cache, q.shape[1], scale, rope)
+    append, prefill, decode, rope_tables = batch.launchers(cache, q.shape[1], scale, rope)
     q = _rows(q)
+    if prefill is None and decode is not None:
+        # decode rows only: RoPE, the append and attention in one launch
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        decode.append_decode(q, _rows(k), _rows(v), layer_index, out, rope_tables=rope_tables)
+        return out
     append(q, k, v, layer_index)
     out = torch.empty_like(q)
     split = batch.first_decode_token

@@ -313,16 +313,26 @@ def test_decode_workspace_reuse_across_calls():
         assert err <= 2e-2
 
 
-def _append_decode_pair(wl, dtype, host_plan, layer=0, table_edit=None):
+def _same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Bitwise equality (NaN slots compare equal to themselves)."""
+    ints = {torch.bfloat16: torch.int16, torch.float32: torch.int32}[a.dtype]
+    return a.dtype == b.dtype and torch.equal(a.cpu().view(ints), b.cpu().view(ints))
+
+
+def _append_decode_pair(wl, dtype, host_plan, layer=0, table_edit=None, rope=False, pool_edit=None):
     """Fused append + decode against nie_kv_append then nie_paged_decode on the
     same inputs: caches and outputs must be bit-identical, and the output
     within tolerance of the oracle (which writes the rows, then attends).
 
     The pool gets `layer` extra leading layers of other values, so the
     fused write is checked at a layer offset; table_edit(table_array) may
-    alter the device tables (both paths see the same ones).
+    alter the device tables (both paths see the same ones).  rope: the fused
+    call also rotates q and the new keys, against nie_rope_kv_append then
+    nie_paged_decode.  pool_edit(kc, vc) may alter the pool first.
     """
     kc, vc = wl.pool(dtype)
+    if pool_edit is not None:
+        pool_edit(kc, vc)
     if layer:
         kc = torch.cat([torch.randn((layer,) + kc.shape[1:]).to(dtype), kc])
         vc = torch.cat([torch.randn((layer,) + vc.shape[1:]).to(dtype), vc])
@@ -339,19 +349,34 @@ def _append_decode_pair(wl, dtype, host_plan, layer=0, table_edit=None):
     dq, dkn, dvn = q.to(DEV), k_new.to(DEV), v_new.to(DEV)
 
     k1, v1 = kc.to(DEV), vc.to(DEV)
-    _native.kv_append(k1, v1, layer, dkn, dvn, torch.from_numpy(slots).to(DEV))
-    out1 = _native.paged_decode(dq, k1, v1, layer, tables, lens, *args, seq_lens_host=host)
+    tables_rope = None
+    if rope:
+        from nano_infer_engine.layers.rope import RopeScale
+
+        tables_rope = RopeScale(wl.head_dim).tables(DEV, dtype, max(wl.seq_lens))
+        q1 = dq.clone()
+        positions = torch.from_numpy(pos.astype(np.int64)).to(DEV)
+        _native.rope_kv_append(k1, v1, layer, q1, dkn, dvn, positions, torch.from_numpy(slots).to(DEV),
+                               *tables_rope)
+    else:
+        q1 = dq
+        _native.kv_append(k1, v1, layer, dkn, dvn, torch.from_numpy(slots).to(DEV))
+    out1 = _native.paged_decode(q1, k1, v1, layer, tables, lens, *args, seq_lens_host=host)
     k2, v2 = kc.to(DEV), vc.to(DEV)
-    out2 = _native.paged_decode(dq, k2, v2, layer, tables, lens, *args, seq_lens_host=host, new_kv=(dkn, dvn))
+    q2 = dq.clone()
+    out2 = _native.paged_decode(q2, k2, v2, layer, tables, lens, *args, seq_lens_host=host, new_kv=(dkn, dvn),
+                                rope_tables=tables_rope)
     torch.cuda.synchronize()
-    assert torch.equal(k1.cpu(), k2.cpu()) and torch.equal(v1.cpu(), v2.cpu()), "fused write differs"
-    assert torch.equal(out1.cpu(), out2.cpu()), "fused output differs"
+    assert torch.equal(q2, dq), "the fused call must not modify q"
+    assert _same_bits(k1, k2) and _same_bits(v1, v2), "fused write differs"
+    assert _same_bits(out1, out2), "fused output differs"
     return out2.cpu(), kc, vc, q, k_new, v_new
 
 
 @pytest.mark.parametrize(
     "q_heads,kv_heads,head_dim,block_size",
-    [(32, 8, 64, 16), (4, 2, 64, 2), (16, 2, 64, 4), (16, 1, 64, 32), (32, 8, 128, 16), (8, 8, 128, 3)],
+    [(32, 8, 64, 16), (4, 2, 64, 16), (4, 2, 64, 2), (16, 2, 64, 4), (16, 1, 64, 32), (32, 8, 128, 16),
+     (8, 8, 128, 3)],
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("host_plan", [False, True])
@@ -378,6 +403,42 @@ def test_decode_append_ragged_lognormal_bf16(host_plan):
     _log(f"decode_append ragged host_plan={host_plan}")
     wl = workloads.decode_ragged()
     _append_decode_pair(wl, torch.bfloat16, host_plan)
+
+
+@pytest.mark.parametrize(
+    "q_heads,kv_heads,head_dim,block_size",
+    [(32, 8, 64, 16), (4, 2, 64, 16), (16, 2, 64, 4), (32, 8, 128, 16), (8, 8, 128, 3)],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("host_plan", [False, True])
+def test_decode_rope_append_matches_rope_append_then_decode(q_heads, kv_heads, head_dim, block_size, dtype,
+                                                           host_plan):
+    """Fused RoPE + append + decode == nie_rope_kv_append then nie_paged_decode,
+    caches and outputs bit for bit, q left unrotated."""
+    _log(f"decode_rope_append hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} "
+         f"host_plan={host_plan}")
+    wl = workloads.ragged([0, 4, 15, 16, 70, 300, 1000], [1] * 7, seed=19, pool_factor=1.5, q_heads=q_heads,
+                          kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
+    _append_decode_pair(wl, dtype, host_plan, layer=1, rope=True)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_decode_append_ignores_stale_slot_content(rope):
+    """NaN in the new token's slot and in every later slot of its block (what
+    an unwritten pool may hold): the fused call's reads of those slots are
+    replaced by the new row, so the output is finite and bit-identical to the
+    separate calls, which write the slot first."""
+    _log(f"decode_append stale slots rope={rope}")
+    wl = workloads.ragged([40, 100, 7, 3000], [1, 1, 1, 1], seed=23, q_heads=32, kv_heads=8)
+
+    def poison(kc, vc):
+        for table, n in zip(wl.tables, wl.seq_lens):
+            block = table[(n - 1) // wl.block_size]
+            kc[0, block, (n - 1) % wl.block_size :] = float("nan")
+            vc[0, block, (n - 1) % wl.block_size :] = float("nan")
+
+    got = _append_decode_pair(wl, torch.bfloat16, False, rope=rope, pool_edit=poison)[0]
+    assert torch.isfinite(got.float()).all()
 
 
 def test_decode_append_skips_out_of_pool_table_entry():
