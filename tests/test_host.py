@@ -327,3 +327,88 @@ def test_library_prefill_plan_from_host_lengths():
     # lengths that do not match the sizes of the call
     assert query([0, 128, 256, 384, 500], [0, 384, 1024, 4000], 512, 128, 4128) == 0
     assert query([0, 128, 256, 384, 512], [0, 384, 1024, 4001], 512, 128, 4128) == 0
+
+
+def test_decoder_kernel_support_checks():
+    """The shapes the RMSNorm / SiLU-product kernels take (16-byte rows, at most
+    1024 vectors per norm row), decided on the host before any launch."""
+    bf = torch.empty((16, 2048), dtype=torch.bfloat16)
+    assert _native.rms_norm_supported(bf) and _native.silu_mul_supported(bf)
+    assert _native.rms_norm_supported(torch.empty((3, 8192), dtype=torch.bfloat16))
+    assert not _native.rms_norm_supported(torch.empty((3, 8200), dtype=torch.bfloat16))  # > 1024 vectors
+    assert not _native.rms_norm_supported(torch.empty((3, 12), dtype=torch.bfloat16))  # not whole vectors
+    assert _native.silu_mul_supported(torch.empty((3, 16384), dtype=torch.float32))
+    assert not _native.silu_mul_supported(torch.empty((3, 6), dtype=torch.float32))
+    assert not _native.rms_norm_supported(torch.empty((3, 64), dtype=torch.float16))
+
+
+def test_rope_table_validation():
+    """RoPE tables for the fused decode: (rows, head_dim / 2), the query dtype,
+    contiguous, the same shape; None means no rotation."""
+    cpu = torch.device("cpu")
+    assert _native._check_rope_tables(None, 64, torch.bfloat16, cpu) == (None, None, 0)
+    cos = torch.zeros((10, 32), dtype=torch.bfloat16)
+    sin = torch.zeros((10, 32), dtype=torch.bfloat16)
+    _, _, rows = _native._check_rope_tables((cos, sin), 64, torch.bfloat16, cpu)
+    assert rows == 10
+    for bad in [(cos, sin[:5]), (cos.float(), sin), (cos[:, :16], sin[:, :16]), (cos.t(), sin.t())]:
+        with pytest.raises(ValueError):
+            _native._check_rope_tables(bad, 64, torch.bfloat16, cpu)
+
+
+def test_request_joins_generated_tokens_when_read():
+    """PagedRequest.sequence: the prompt followed by the appended tokens, joined
+    once when read; assigning replaces it."""
+    from nano_infer_engine.generation.request import PagedRequest
+
+    prompt = torch.tensor([[5, 6, 7]])
+    r = PagedRequest("s", prompt)
+    assert r.sequence is prompt
+    step = torch.tensor([[1], [2]])
+    r.append_token(step[1:2])
+    r.append_token(torch.tensor([[9]]))
+    assert r.sequence.tolist() == [[5, 6, 7, 2, 9]]
+    assert r.sequence.tolist() == [[5, 6, 7, 2, 9]]  # joined once, stable
+    r.append_token(torch.tensor([[4]]))
+    assert r.sequence.tolist() == [[5, 6, 7, 2, 9, 4]]
+    r.sequence = prompt
+    assert r.sequence is prompt
+
+
+def test_rms_norm_forward_add_on_cpu_is_add_then_norm():
+    """RmsNorm.forward_add: (x + residual, norm(x + residual)), the reference's
+    residual add then norm (layers/decoder.py:50-51), on the CPU path."""
+    from nano_infer_engine.layers.rms_norm import RmsNorm
+
+    torch.manual_seed(0)
+    norm = RmsNorm(64, eps=1e-5)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(64))
+    x, r = torch.randn(5, 64).bfloat16(), torch.randn(5, 64).bfloat16()
+    norm = norm.bfloat16()
+    h, n = norm.forward_add(x, r)
+    assert torch.equal(h, x + r)
+    assert torch.equal(n, norm(x + r))
+
+
+def test_unsummed_residual_chain_equals_summed_on_cpu():
+    """Decoder blocks passing their output as an unsummed (ffn_out, h) pair to
+    the next norm give the same values as summing first (CPU path)."""
+    from nano_infer_engine.layers.decoder import Llama3Decoder
+
+    torch.manual_seed(1)
+    blocks = [Llama3Decoder(1e-5, 4, 2, 64, 128) for _ in range(2)]
+
+    def fake_attention(normed, *args):  # deterministic stand-in for the paged attention
+        return torch.tanh(normed)
+
+    for b in blocks:
+        b.attn.forward_tokens = fake_attention
+    x = torch.randn(3, 64)
+    summed = x
+    for b in blocks:
+        summed = b.forward_tokens(summed, None, 0, None)
+    pair = x
+    for b in blocks:
+        pair = b.forward_tokens_unsummed(pair, None, 0, None)
+    assert torch.equal(summed, pair[0] + pair[1])
