@@ -412,3 +412,34 @@ def test_unsummed_residual_chain_equals_summed_on_cpu():
     for b in blocks:
         pair = b.forward_tokens_unsummed(pair, None, 0, None)
     assert torch.equal(summed, pair[0] + pair[1])
+
+
+def test_library_rejects_bad_decoder_and_fused_arguments():
+    """The new entry points validate before any launch: unsupported dtype or
+    row length, null pointers and misaligned rows return an error status (and
+    an empty batch returns 0), so no kernel sees a bad shape."""
+    lib = _native.load_library()
+    buf = torch.zeros(4096, dtype=torch.uint8)
+    p = buf.data_ptr() + (-buf.data_ptr()) % 16  # a 16-byte aligned host address (never dereferenced)
+    # nie_rms_norm(dtype, x, x_stride, res, res_stride, sum, sum_stride, w, out, out_stride, rows, cols, eps, stream)
+    assert lib.nie_rms_norm(7, p, 64, None, 0, None, 0, None, p, 64, 4, 64, 1e-5, None) < 0  # dtype
+    assert lib.nie_rms_norm(1, p, 64, None, 0, None, 0, None, p, 64, 4, 12, 1e-5, None) < 0  # 12 columns
+    assert lib.nie_rms_norm(1, p, 9000, None, 0, None, 0, None, p, 9000, 4, 9000, 1e-5, None) < 0  # too long
+    assert lib.nie_rms_norm(1, None, 64, None, 0, None, 0, None, p, 64, 4, 64, 1e-5, None) < 0  # null x
+    assert lib.nie_rms_norm(1, p, 64, p, 64, None, 0, None, p, 64, 4, 64, 1e-5, None) < 0  # residual, no sum
+    assert lib.nie_rms_norm(1, p + 2, 64, None, 0, None, 0, None, p, 64, 4, 64, 1e-5, None) < 0  # misaligned
+    assert lib.nie_rms_norm(1, p, 32, None, 0, None, 0, None, p, 64, 4, 64, 1e-5, None) < 0  # stride < cols
+    assert lib.nie_rms_norm(1, p, 64, None, 0, None, 0, None, p, 64, 0, 64, 1e-5, None) == 0  # no rows
+    # nie_silu_mul(dtype, gate, gate_stride, up, up_stride, out, out_stride, rows, cols, stream)
+    assert lib.nie_silu_mul(1, p, 64, p, 64, p, 64, 4, 12, None) < 0  # 12 columns
+    assert lib.nie_silu_mul(1, None, 64, p, 64, p, 64, 4, 64, None) < 0  # null gate
+    assert lib.nie_silu_mul(1, p + 2, 64, p, 64, p, 64, 4, 64, None) < 0  # misaligned
+    assert lib.nie_silu_mul(1, p, 64, p, 64, p, 64, 0, 64, None) == 0  # no rows
+    # nie_paged_decode_append with a batch but no new rows, or one RoPE table only
+    args = dict(q=p, k_cache=p, v_cache=p, tables=p, lens=p, out=p)
+    base = [1, args["q"], 32 * 64, 64]
+    rest = [args["k_cache"], args["v_cache"], 1, 0, 4, 16, 32, 8, 64, args["tables"], 4, args["lens"], 2, 40, 60,
+            0.125, args["out"], 32 * 64, 64, p, 1 << 20, None, None]
+    assert lib.nie_paged_decode_append(*base, None, 512, p, 512, None, None, 0, *rest) < 0  # no new keys
+    assert lib.nie_paged_decode_append(*base, p, 512, p, 512, p, None, 4, *rest) < 0  # one table
+    assert b"RoPE" in lib.nie_last_error()
