@@ -318,8 +318,10 @@ def run_mixed(args):
         pev.append((e[0], e[1]))
         dev_.append((e[1], e[2]))
     torch.cuda.synchronize()
-    p_us = sum(a.elapsed_time(b) for a, b in pev) / reps * 1e3
-    d_us = sum(a.elapsed_time(b) for a, b in dev_) / reps * 1e3
+    # medians: an event pair also spans the host's launch of the call, so a
+    # host stall (a page fault, the garbage collector) would skew a mean
+    p_us = float(np.median([a.elapsed_time(b) for a, b in pev])) * 1e3
+    d_us = float(np.median([a.elapsed_time(b) for a, b in dev_])) * 1e3
     flops = workloads.prefill_flops(wl.context_lens[:n_pref], wl.query_lens[:n_pref])
     tflops = flops / (p_us * 1e-6) / 1e12
     dbytes = workloads.decode_bytes(seq_lens[n_pref:])

@@ -179,6 +179,28 @@ int nie_silu_mul(int dtype, const void* gate, int64_t gate_stride, const void* u
                  void* out, int64_t out_stride, int64_t rows, int64_t cols, void* stream);
 
 /*
+ * Projection GEMM of a decode step: y[m, j] = sum_i x[m, i] * w[j, i] for
+ * m < rows, with w the (n, k) row-major weight of an nn.Linear (no bias),
+ * bf16 operands, fp32 accumulation and one rounding to bf16.
+ * epilogue NIE_LINEAR_SILU_MUL: w is the (2n, k) [gate; up] weight of a
+ * SwiGLU block and y = silu(gate) * up over the n columns, with gate and up
+ * rounded to bf16 first and nie_silu_mul's arithmetic after.
+ * rows in 1..16, n a multiple of 16, k a multiple of 2048; x rows and w
+ * 16-byte aligned; x_stride / y_stride are element strides between rows.
+ * Other shapes return NIE_EUNSUPPORTED (callers then use a library GEMM).
+ * Replaces, for decode steps: the nn.Linear projections of
+ *           GroupedQueryAttention (q/k/v: src/nano_infer_engine/layers/attention.py:227-232,
+ *           :359-361; o_proj: :271, :414), SwiGLUMLP's gate/up/down
+ *           projections and their gated product
+ *           (src/nano_infer_engine/layers/mlp.py:18-22) and the LM head
+ *           (src/nano_infer_engine/models/llama.py:328, :391).
+ */
+#define NIE_LINEAR_PLAIN 0
+#define NIE_LINEAR_SILU_MUL 1
+int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t rows, const void* w, int64_t n,
+                    int64_t k, int epilogue, void* y, int64_t y_stride, void* stream);
+
+/*
  * Greedy token selection: out[r] = index of the largest of the cols values
  * of row r (element (r, c) at r * row_stride + c), ties to the lowest index,
  * NaN larger than every number — torch.argmax's result.  out is int64.

@@ -35,6 +35,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "nie_paged.h"
 
@@ -1080,6 +1081,232 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate, int64_t
     for (int w = 0; w < 4; ++w) o[w] = __float_as_uint(y[w]);
   }
   *reinterpret_cast<v4u*>(reinterpret_cast<T*>(out) + r * out_stride + c) = o;
+}
+
+// ---------------------------------------------------------------------------
+// Decode-step projections: y = x . W^T over at most 16 rows (bf16)
+// ---------------------------------------------------------------------------
+// A decode step multiplies at most one row per sequence by each weight, so
+// these GEMMs stream their weights once and are HBM-bound: 2*N*K bytes for
+// 2*rows*N*K flops.  The work is tiles of 16 output columns (the SwiGLU
+// epilogue: 16 gate rows and the 16 matching up rows of the weight), each
+// walked in passes of 16 weight rows x 1024 k (32 KiB).  One workgroup per
+// CU streams the passes of its tiles (tile blockIdx.x, then + gridDim.x, ...)
+// through a 4-stage LDS ring, three passes in flight while one is multiplied:
+//  - each wave of eight DMAs 2 of the 16 rows of a pass with global_load_lds_dwordx4
+//    (one op = 1 KiB of one row, contiguous) under the non-temporal policy
+//    (every weight byte is read once);
+//  - a row's 16-byte slot S sits at LDS slot S ^ (row & 15), so the MFMA
+//    operand reads (16 rows, the same k) hit 16 different bank groups;
+//  - wave w multiplies the k eighth w of each pass: per 32-wide chunk one
+//    v_mfma_f32_16x16x32_bf16 with x as the A operand (row l%16, k
+//    8*(l/16)..+7) and the weight rows as B (column l%16, the same k).  A
+//    wave loads its x operands of the whole k into registers once (x is
+//    read by every workgroup: the L2 serves it);
+//  - at a tile's last pass the eight waves' sums meet in LDS and wave 0
+//    writes the tile while the ring keeps streaming.
+// Epilogues: kLinearPlain writes bf16(x . W^T).  kLinearSiluMul alternates
+// gate and up passes over the same k range and writes silu(gate) * up with
+// torch's roundings: gate and up rounded to bf16 (the GEMM outputs), silu in
+// fp32 rounded, the product rounded (layers/mlp.py:18-22 of the reference
+// engine; nie_silu_mul's arithmetic).
+constexpr int kLinearWaves = 8;
+constexpr int kLinearMaxRows = 16;
+constexpr int kLinearPassBytes = 32 * 1024;
+constexpr int kLinearStages = 4;
+constexpr int kLinearPlain = 0;
+constexpr int kLinearSiluMul = 1;
+
+struct LinearArgs {
+  const bf16_t* x;
+  int64_t x_stride;  // elements between rows of x
+  int32_t rows;      // 1..16
+  const bf16_t* w;   // (n, k) row-major; (2n, k) for kLinearSiluMul
+  int64_t n;         // output columns
+  int64_t k;
+  bf16_t* y;
+  int64_t y_stride;
+};
+
+__device__ __forceinline__ bf16x8_t load_bf16x8(const bf16_t* p) {
+  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const v4u*>(p));
+}
+
+// f(integral_constant<int, I>) for I = kBegin .. kEnd - 1.
+template <int kBegin, int kEnd, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (kBegin < kEnd) {
+    f(std::integral_constant<int, kBegin>{});
+    static_for<kBegin + 1, kEnd>(f);
+  }
+}
+
+// kKPasses = k / 1024 (2, 4 or 8); grid.x <= the number of tiles.
+template <int kEpi, int kKPasses>
+__global__ __launch_bounds__(kLinearWaves* kWave) void linear_rows_kernel(LinearArgs a) {
+  constexpr int kSets = kEpi == kLinearSiluMul ? 2 : 1;
+  constexpr int kPasses = kSets * kKPasses;             // passes per tile
+  constexpr int kRowBytes = kLinearPassBytes / 16;      // 2 KiB of each row per pass
+  constexpr int kPassK = kRowBytes / 2;                 // 1024
+  constexpr int kPieces = kRowBytes / (kWave * 16);     // 2 DMA ops per row and pass
+  constexpr int kRowsPerWave = 16 / kLinearWaves;       // 2
+  constexpr int kOps = kRowsPerWave * kPieces;          // DMA ops per wave and pass
+  constexpr int kWaveK = kPassK / kLinearWaves;         // 128
+  constexpr int kChunks = kWaveK / 32;                  // 4 MFMAs per wave and pass
+  // passes per loop trip: stage (q % 4) and pass (q % kPasses) of every step
+  // are then compile-time constants
+  constexpr int kTrip = kPasses > kLinearStages ? kPasses : kLinearStages;
+  static_assert(kTrip % kPasses == 0 && kTrip % kLinearStages == 0, "trip covers whole tiles and ring turns");
+  __shared__ __attribute__((aligned(16))) unsigned char ring[kLinearStages][kLinearPassBytes];
+  __shared__ v4f red[kSets][kLinearWaves][kWave];
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16, g = lane / 16;
+  const int64_t tiles = a.n / 16;
+  const int64_t my_tiles = (tiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
+  const int64_t total = my_tiles * kPasses;  // passes of this workgroup
+  const bool row_ok = c < a.rows;
+  const bf16x8_t zero = __builtin_bit_cast(bf16x8_t, v4u{0u, 0u, 0u, 0u});
+
+  // DMA source of row r = 2*wave + i of tile 0: lane l reads 16-byte slot
+  // l ^ r of each 1 KiB piece, so slot S lands at S ^ r
+  const unsigned char* src[kRowsPerWave];
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave; ++i) {
+    const int r = wave * kRowsPerWave + i;
+    src[i] = reinterpret_cast<const unsigned char*>(a.w + r * a.k) + 16 * (lane ^ r);
+  }
+  const int64_t tile_bytes = 16 * a.k * (int64_t)sizeof(bf16_t);
+  const int64_t set_bytes = a.n * a.k * (int64_t)sizeof(bf16_t);  // gate rows -> up rows
+  // LDS address of this lane's operand slot of chunk j in ring stage 0
+  uint32_t rd[kChunks];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int slot = wave * (kWaveK / 8) + 4 * j + g;
+    rd[j] = lds_off(&ring[0][c * kRowBytes + 16 * (slot ^ c)]);
+  }
+
+  // pass q of the stream (tile blockIdx.x + (q / kPasses) * gridDim.x, pass
+  // kPass = q % kPasses of it) into ring stage q % 4
+  auto issue = [&](int64_t q, auto pass_tag) {
+    constexpr int kPass = decltype(pass_tag)::value % kPasses;
+    constexpr int kStage = decltype(pass_tag)::value % kLinearStages;
+    constexpr int kSet = kSets == 2 ? (kPass & 1) : 0;
+    constexpr int kKp = kSets == 2 ? kPass >> 1 : kPass;
+    const int64_t t = blockIdx.x + (q / kPasses) * gridDim.x;
+    const int64_t off = t * tile_bytes + kSet * set_bytes + kKp * kRowBytes;
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i) {
+      const int r = wave * kRowsPerWave + i;
+#pragma unroll
+      for (int pc = 0; pc < kPieces; ++pc) {
+        lds_dma16<kCacheStream>(src[i] + off + pc * kWave * 16, &ring[kStage][r * kRowBytes + pc * kWave * 16]);
+      }
+    }
+  };
+
+  // this wave's x operands of the whole k (its eighth of every pass): issued
+  // between passes 0 and 1, so the wait for pass 0 covers them
+  bf16x8_t xa[kKPasses][kChunks];
+  issue(0, std::integral_constant<int, 0>{});
+  {
+    const bf16_t* xp = a.x + (int64_t)(row_ok ? c : 0) * a.x_stride + wave * kWaveK + 8 * g;
+#pragma unroll
+    for (int kp = 0; kp < kKPasses; ++kp) {
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) xa[kp][j] = row_ok ? load_bf16x8(xp + kp * kPassK + 32 * j) : zero;
+    }
+  }
+  issue(1, std::integral_constant<int, 1>{});
+  if (total > 2) issue(2, std::integral_constant<int, 2>{});
+
+  v4f acc[kSets];
+#pragma unroll
+  for (int s = 0; s < kSets; ++s) acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t q0 = 0; q0 < total; q0 += kTrip) {
+    static_for<0, kTrip>([&](auto u_tag) {
+      constexpr int kU = decltype(u_tag)::value;
+      constexpr int kStage = kU % kLinearStages;
+      constexpr int kPass = kU % kPasses;
+      constexpr int kSet = kSets == 2 ? (kPass & 1) : 0;
+      constexpr int kKp = kSets == 2 ? kPass >> 1 : kPass;
+      const int64_t q = q0 + kU;
+      if (q >= total) return;  // uniform: the last trip may end early, at a tile boundary
+      // passes q+1 and q+2 (when they exist) may still be in flight
+      const int64_t after = total - 1 - q;
+      if (after >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kOps));
+      else if (after == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kOps));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      // every wave has its rows of pass q, and is done with stage (q - 1) % 4.
+      // A bare s_barrier: __syncthreads() would first wait for every DMA in
+      // flight, the next passes' included.
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (q + kLinearStages - 1 < total) issue(q + kLinearStages - 1, std::integral_constant<int, kU + kLinearStages - 1>{});
+      uint32_t addr[kChunks];
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) addr[j] = rd[j] + kStage * kLinearPassBytes;
+      uint4 wv[kChunks];
+      ring_read_k<kChunks>(wv, addr);
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) {
+        acc[kSet] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[kKp][j], __builtin_bit_cast(bf16x8_t, wv[j]),
+                                                            acc[kSet], 0, 0, 0);
+      }
+      if constexpr (kPass == kPasses - 1) {
+        // the tile's sums meet in LDS; wave 0 writes them.  The next write of
+        // red comes at least one pass (one barrier) later.  Inline-asm LDS
+        // ops and an explicit lgkmcnt wait: compiler-visible LDS accesses
+        // would first wait for the DMA still in flight.
+        // The accumulators come straight from the MFMAs: a DS instruction
+        // reading an MFMA result needs wait states after it (11 for the
+        // 8-pass 16x16x32), which the compiler does not insert ahead of
+        // inline asm, so the asm carries 16 of its own.
+#pragma unroll
+        for (int s = 0; s < kSets; ++s) {
+          const v4u v = __builtin_bit_cast(v4u, acc[s]);
+          asm volatile("s_nop 7\n\ts_nop 7\n\tds_write_b128 %0, %1" ::"v"(lds_off(&red[s][wave][lane])), "v"(v)
+                       : "memory");
+          acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (wave == 0) {
+          v4f sum[kSets];
+#pragma unroll
+          for (int s = 0; s < kSets; ++s) {
+            uint32_t raddr[kLinearWaves];
+#pragma unroll
+            for (int w = 0; w < kLinearWaves; ++w) raddr[w] = lds_off(&red[s][w][lane]);
+            uint4 part[kLinearWaves];
+            ring_read_k<kLinearWaves>(part, raddr);
+            sum[s] = __builtin_bit_cast(v4f, part[0]);
+#pragma unroll
+            for (int w = 1; w < kLinearWaves; ++w) sum[s] += __builtin_bit_cast(v4f, part[w]);
+          }
+          // lane l holds rows 4g..4g+3 of column col
+          const int64_t col = (blockIdx.x + (q / kPasses) * gridDim.x) * 16 + c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            if (m >= a.rows) break;
+            float v;
+            if constexpr (kEpi == kLinearSiluMul) {
+              const float gate = round_to_bf16(sum[0][r]);
+              const float up = round_to_bf16(sum[1][r]);
+              v = round_to_bf16(gate / (1.f + expf(-gate))) * up;
+            } else {
+              v = sum[0][r];
+            }
+            reinterpret_cast<uint16_t*>(a.y)[m * a.y_stride + col] = (uint16_t)f32_to_bf16_bits(v);
+          }
+        }
+      }
+    });
+  }
 }
 
 // Floats -> one 16-byte vector of T (round to nearest even for bf16).
@@ -2978,6 +3205,59 @@ NIE_API int nie_rms_norm(int dtype, const void* x, int64_t x_stride, const void*
                        residual_stride, sum_out, sum_stride, weight, out, out_stride, (int)cols, eps);
   }
   return launched("rms_norm");
+}
+
+NIE_API int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t rows, const void* w, int64_t n,
+                            int64_t k, int epilogue, void* y, int64_t y_stride, void* stream) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  if (dtype != NIE_DTYPE_BF16) return fail(NIE_EUNSUPPORTED, "linear_rows: only bf16 is built");
+  if (epilogue != NIE_LINEAR_PLAIN && epilogue != NIE_LINEAR_SILU_MUL) {
+    return fail(NIE_EINVAL, "linear_rows: unknown epilogue %d", epilogue);
+  }
+  if (rows < 1 || rows > kLinearMaxRows) {
+    return fail(NIE_EUNSUPPORTED, "linear_rows: %lld rows (1..%d are built)", (long long)rows, kLinearMaxRows);
+  }
+  if (n <= 0 || n % 16 != 0 || n / 16 > 0x7fffffffLL) {
+    return fail(NIE_EUNSUPPORTED, "linear_rows: %lld output columns (need a positive multiple of 16)", (long long)n);
+  }
+  if (k != 2048 && k != 4096 && (k != 8192 || epilogue == NIE_LINEAR_SILU_MUL)) {
+    return fail(NIE_EUNSUPPORTED, "linear_rows: inner size %lld (2048, 4096 and, without the SiLU epilogue, 8192 are built)",
+                (long long)k);
+  }
+  if (!x || !w || !y) return fail(NIE_EINVAL, "null pointer argument");
+  if (x_stride < k || y_stride < n) return fail(NIE_EINVAL, "linear_rows: row strides shorter than the rows");
+  if (!check_aligned(x, x_stride, 0, 2) || !check_aligned(w, 0, 0, 2) || ((uintptr_t)y % 2) != 0) {
+    return fail(NIE_EINVAL, "linear_rows: x rows and the weight must be 16-byte aligned");
+  }
+  LinearArgs a;
+  a.x = reinterpret_cast<const bf16_t*>(x);
+  a.x_stride = x_stride;
+  a.rows = (int32_t)rows;
+  a.w = reinterpret_cast<const bf16_t*>(w);
+  a.n = n;
+  a.k = k;
+  a.y = reinterpret_cast<bf16_t*>(y);
+  a.y_stride = y_stride;
+  hipStream_t s = (hipStream_t)stream;
+  // one workgroup per CU (the ring takes 128 KiB of LDS), at most one per tile
+  const int64_t tiles = n / 16;
+  const dim3 grid((unsigned)(tiles < kDecodeCUs ? tiles : kDecodeCUs)), block(kLinearWaves * kWave);
+  const bool silu = epilogue == NIE_LINEAR_SILU_MUL;
+  switch (k) {
+    case 2048:
+      if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 2>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 2>), grid, block, 0, s, a);
+      break;
+    case 4096:
+      if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 4>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 4>), grid, block, 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 8>), grid, block, 0, s, a);
+      break;
+  }
+  return launched("linear_rows_kernel");
 }
 
 NIE_API int nie_silu_mul(int dtype, const void* gate, int64_t gate_stride, const void* up, int64_t up_stride,

@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "nie_argmax_rows",
     "nie_rms_norm",
     "nie_silu_mul",
+    "nie_linear_rows",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
@@ -83,6 +84,7 @@ _SIGNATURES = {
         [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _f32, _ptr],
     ),
     "nie_silu_mul": (_i32, [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr]),
+    "nie_linear_rows": (_i32, [_i32, _ptr, _i64, _i64, _ptr, _i64, _i64, _i32, _ptr, _i64, _ptr]),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
@@ -457,6 +459,51 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
                                      cols, _stream(g.device))
     _check(rc, "nie_silu_mul")
     return out.view(gate.shape)
+
+
+LINEAR_MAX_ROWS = 16
+LINEAR_K_MULTIPLE = 2048
+LINEAR_PLAIN = 0
+LINEAR_SILU_MUL = 1
+
+
+def linear_rows_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether nie_linear_rows takes ``F.linear(x, weight)``: bf16 on the GPU,
+    at most 16 rows, in-features a multiple of 2048, out-features of 16."""
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or weight.ndim != 2 or x.ndim == 0:
+        return False
+    if not x.is_cuda or weight.device != x.device:
+        return False
+    n, k = weight.shape
+    rows = x.numel() // max(x.shape[-1], 1)
+    return (x.shape[-1] == k and 0 < rows <= LINEAR_MAX_ROWS and k % LINEAR_K_MULTIPLE == 0 and n % 16 == 0
+            and n > 0)
+
+
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, silu_mul: bool = False) -> torch.Tensor:
+    """``F.linear(x, weight)`` (no bias) for a decode step's few rows, on nie_linear_rows.
+
+    With ``silu_mul`` the weight is a SwiGLU block's ``[gate; up]`` rows and the
+    result is ``silu(gate) * up`` (``layers/mlp.py:18-22``), half as wide.
+    """
+    _require_gpu(x, weight)
+    if not linear_rows_supported(x, weight):
+        raise RuntimeError(f"nie_linear_rows does not take x {tuple(x.shape)} {x.dtype} with weight "
+                           f"{tuple(weight.shape)} {weight.dtype}")
+    n, k = weight.shape
+    if silu_mul and n % 32 != 0:
+        raise RuntimeError("a [gate; up] weight needs a multiple of 32 rows")
+    n_out = n // 2 if silu_mul else n
+    xs = _aligned(_norm_rows(x, k))
+    w = _aligned(weight.detach() if weight.is_contiguous() else weight.detach().contiguous())
+    rows = xs.shape[0]
+    out = torch.empty((rows, n_out), dtype=x.dtype, device=x.device)
+    rc = load_library().nie_linear_rows(
+        dtype_code(x.dtype), xs.data_ptr(), xs.stride(0) if rows > 1 else k, rows, w.data_ptr(), n_out, k,
+        LINEAR_SILU_MUL if silu_mul else LINEAR_PLAIN, out.data_ptr(), n_out, _stream(x.device),
+    )
+    _check(rc, "nie_linear_rows")
+    return out.view(*x.shape[:-1], n_out)
 
 
 def kv_gather(

@@ -4,7 +4,8 @@ Public surface of ``GroupedQueryAttention`` in ``layers/attention.py:121-414``
 of the reference engine: the constructor, ``forward`` with its paged decode
 branch (``paged_cache=``, ``layer_index=``, ``sequence_id=``,
 ``sequence_ids=``; same checks and messages) and ``forward_ragged``.  The
-projections and output projection stay torch ops; RoPE, the K/V write and
+projections run through :mod:`layers.linear` (the HIP GEMM for a decode
+step's rows, torch's otherwise); RoPE, the K/V write and
 the attention itself go through :data:`attention_core`
 (:func:`paged_batch.attention_core`: one fused RoPE + KV-append launch plus
 the decode / varlen-prefill kernels).
@@ -22,6 +23,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from nano_infer_engine.layers import linear as _linear
 from nano_infer_engine.layers.rope import Rope
 from nano_infer_engine import paged_batch as _paged_batch
 from nano_infer_engine.paged_batch import RaggedBatch, build_ragged_batch
@@ -69,7 +71,7 @@ class GroupedQueryAttention(nn.Module):
             with torch.no_grad():
                 self._qkv_weight = torch.cat(ws, dim=0)
             self._qkv_key = key
-        qkv = F.linear(x, self._qkv_weight)
+        qkv = _linear.linear(x, self._qkv_weight)
         return qkv.split((ws[0].shape[0], ws[1].shape[0], ws[2].shape[0]), dim=-1)
 
     # ------------------------------------------------------------------
@@ -87,7 +89,7 @@ class GroupedQueryAttention(nn.Module):
         k = k.view(tokens, self.kv_head_num, self.head_dim)
         v = v.view(tokens, self.kv_head_num, self.head_dim)
         context = attention_core(q, k, v, paged_cache, layer_index, batch, self.head_dim**-0.5, self.rope)
-        return self.o_proj(context.view(tokens, self.hidden_size))
+        return _linear.apply(self.o_proj, context.view(tokens, self.hidden_size))
 
     def forward(
         self,

@@ -5,6 +5,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from nano_infer_engine import _native
+from nano_infer_engine.layers import linear as _linear
 
 
 class SwiGLUMLP(nn.Module):
@@ -31,8 +32,14 @@ class SwiGLUMLP(nn.Module):
                 with torch.no_grad():
                     self._gate_up_weight = torch.cat(ws, dim=0)
                 self._gate_up_key = key
+            if ws[0].shape == ws[1].shape:
+                # a decode step's rows: both projections and the gated
+                # product in one HIP GEMM
+                h = _linear.silu_mul_linear(x, self._gate_up_weight, ws[0].shape[0])
+                if h is not None:
+                    return _linear.apply(self.down_proj, h)
             gate, up = F.linear(x, self._gate_up_weight).split((ws[0].shape[0], ws[1].shape[0]), dim=-1)
             if _native.silu_mul_supported(gate):
-                return self.down_proj(_native.silu_mul(gate, up))
-            return self.down_proj(F.silu(gate) * up)
+                return _linear.apply(self.down_proj, _native.silu_mul(gate, up))
+            return _linear.apply(self.down_proj, F.silu(gate) * up)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))

@@ -20,6 +20,7 @@ from dataclasses import dataclass, field
 import torch
 from torch import nn
 
+from nano_infer_engine.layers import linear as _linear
 from nano_infer_engine.layers.decoder import Llama3Decoder
 from nano_infer_engine.layers.rms_norm import RmsNorm
 from nano_infer_engine.layers.rope import Rope, RopeScale
@@ -143,7 +144,7 @@ class Llama3_2(nn.Module):
         ffn_out, h = x
         if logits_rows is not None:
             ffn_out, h = ffn_out[logits_rows], h[logits_rows]
-        return self.lm_head(self.final_rms.forward_add(ffn_out, h)[1])
+        return _linear.apply(self.lm_head, self.final_rms.forward_add(ffn_out, h)[1])
 
     def _new_cache_for(self, batch_size: int, seq_len: int, device: torch.device) -> tuple[PagedKVCache, tuple[str, ...]]:
         block_size = 16

@@ -590,3 +590,74 @@ def test_silu_mul_matches_reference_formula(dtype, halves):
     assert err <= rel
     if dtype == torch.bfloat16:
         assert mism < 0.001
+
+
+def _linear_inputs(rows, n, k, seed, x_cols=None):
+    gen = torch.Generator().manual_seed(seed)
+    x_full = torch.randn((rows, x_cols or k), generator=gen).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=gen) / k**0.5).to(torch.bfloat16)
+    return x_full, w
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16])
+@pytest.mark.parametrize("n,k", [(3072, 2048), (2048, 8192), (32768, 2048)])
+def test_linear_rows_matches_float64_product(rows, n, k):
+    """nie_linear_rows against x . W^T in float64 on the CPU, rounded to bf16:
+    every output within half a bf16 ulp of the exact product (plus the fp32
+    accumulation's error), at most 1% of outputs one ulp away from torch's own
+    bf16 GEMM on the GPU.  (32768, 2048) takes the two-tile launch; x is a
+    column slice of a wider tensor (row stride > k)."""
+    _log(f"linear_rows rows={rows} n={n} k={k}")
+    x_full, w = _linear_inputs(rows, n, k, seed=rows * 7 + n, x_cols=k + 64)
+    x = x_full[:, 32:32 + k]
+    dx, dw = x_full.to(DEV)[:, 32:32 + k], w.to(DEV)
+    got = _native.linear_rows(dx, dw)
+    lib = torch.nn.functional.linear(dx, dw)
+    torch.cuda.synchronize()
+    exact = x.double() @ w.double().T
+    got = got.cpu().double()
+    err = ((got - exact).abs() - exact.abs() * 2.0**-8).max().item()
+    ulp_diff = (got != lib.cpu().double()).double().mean().item()
+    _log(f"  excess over half an ulp={err:.3e} differs from torch's GEMM={ulp_diff:.5f}")
+    assert err <= 1e-5
+    assert ulp_diff < 0.01
+
+
+@pytest.mark.parametrize("rows", [3, 16])
+def test_linear_rows_silu_mul_matches_reference_formula(rows):
+    """The SwiGLU epilogue: gate and up from float64 products rounded to bf16,
+    then silu rounded and the product rounded (nie_silu_mul's arithmetic),
+    against nie_linear_rows with the fused [gate; up] weight; outputs whose
+    gate or up landed on the other side of a rounding boundary are the only
+    ones allowed to differ (< 1%).  One ulp on gate and on up, carried through
+    silu's rounding and the product's, stays within 6 bf16 ulps, so the
+    bound is 2^-5 relative (8 ulps); a wrong operand or index gives O(1)."""
+    inner, k = 8192, 2048
+    _log(f"linear_rows silu_mul rows={rows}")
+    x, w = _linear_inputs(rows, 2 * inner, k, seed=11 + rows)
+    w = (w.float() * 3).to(torch.bfloat16)  # gate values of a few units, where silu bends
+    got = _native.linear_rows(x.to(DEV), w.to(DEV), silu_mul=True)
+    torch.cuda.synchronize()
+    prod = x.double() @ w.double().T
+    gate = prod[:, :inner].to(torch.bfloat16).float()
+    up = prod[:, inner:].to(torch.bfloat16).float()
+    want = (torch.nn.functional.silu(gate).to(torch.bfloat16).float() * up).to(torch.bfloat16).float()
+    got = got.cpu().float()
+    assert got.shape == (rows, inner)
+    rel = ((got - want).abs() / want.abs().clamp_min(1e-3)).max().item()
+    mism = (got != want).float().mean().item()
+    _log(f"  max_rel_err={rel:.3e} mismatching={mism:.5f}")
+    assert rel <= 2.0**-5
+    assert mism < 0.01
+
+
+def test_linear_rows_rejects_unsupported_shapes_on_the_gpu():
+    """17 rows or an in-size that is not a multiple of 2048 raise before any
+    launch (callers keep torch's GEMM for them)."""
+    x = torch.zeros((17, 2048), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((64, 2048), dtype=torch.bfloat16, device=DEV)
+    assert not _native.linear_rows_supported(x, w)
+    with pytest.raises(RuntimeError, match="nie_linear_rows"):
+        _native.linear_rows(x, w)
+    assert not _native.linear_rows_supported(x[:4, :1024], w[:, :1024])
+    assert _native.linear_rows_supported(x[:16], w)

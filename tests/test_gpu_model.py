@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import nano_infer_engine.layers.attention as attention_module
+import nano_infer_engine.layers.linear as linear_module
 from nano_infer_engine.generation import (
     ContinuousBatchingScheduler,
     GenerationConfig,
@@ -50,6 +51,30 @@ def oracle_attention():
         yield
     finally:
         attention_module.attention_core = saved
+
+
+@contextlib.contextmanager
+def reference_path():
+    """The reference's algorithms end to end: the reference attention and
+    torch's GEMM for every projection (no nie_linear_rows)."""
+    saved = linear_module.USE_NATIVE
+    linear_module.USE_NATIVE = False
+    try:
+        with oracle_attention():
+            yield
+    finally:
+        linear_module.USE_NATIVE = saved
+
+
+@contextlib.contextmanager
+def torch_gemm():
+    """The projections on torch's GEMM, attention on the HIP kernels."""
+    saved = linear_module.USE_NATIVE
+    linear_module.USE_NATIVE = False
+    try:
+        yield
+    finally:
+        linear_module.USE_NATIVE = saved
 
 
 def _model(dtype=torch.float32, hidden=256, q_heads=4, kv_heads=2, layers=2, vocab=64, max_seq_len=64, seed=0):
@@ -361,7 +386,9 @@ def test_greedy_tokens_identical_to_oracle_attention_fp32():
 
 def test_bf16_teacher_forced_matches_oracle_attention():
     """bf16 Llama-shaped heads (32 q / 8 kv, head_dim 64): logits of a prefill
-    and 24 teacher-forced decode steps, HIP vs the reference algorithm.
+    and 24 teacher-forced decode steps, HIP (attention kernels and the decode
+    steps' projection GEMMs) vs the reference algorithm (reference attention,
+    torch's GEMMs).
 
     The two differ by bf16 rounding order only: max abs logit error <= 5e-2.
     The top-1 token must match on every row whose reference top-2 margin is
@@ -388,7 +415,7 @@ def test_bf16_teacher_forced_matches_oracle_attention():
 
     with torch.inference_mode():
         hip = run()
-        with oracle_attention():
+        with reference_path():
             ref = run()
     err = (hip - ref).abs().max().item()
     top2 = ref.topk(2, dim=-1).values
@@ -400,3 +427,44 @@ def test_bf16_teacher_forced_matches_oracle_attention():
     assert torch.equal(hip.argmax(-1)[decisive], ref.argmax(-1)[decisive])
     picked = ref.gather(1, hip.argmax(-1, keepdim=True)).squeeze(1)
     assert bool((top2[:, 0] - picked <= 2 * err).all())
+
+
+def test_bf16_batched_decode_projections_match_torch_gemm():
+    """16 sequences through two Llama-3.2-1B-shaped blocks (hidden 2048, 32 q /
+    8 kv heads, SwiGLU 4096, vocab 32768, bf16): prefill, then 6 decode steps
+    of 16 rows each, whose projections, gated product and LM head run on
+    nie_linear_rows, against the same steps on torch's GEMM (the attention
+    kernels the same in both).  The two differ by accumulation order only:
+    max abs logit error <= 5e-2, top-1 identical on rows whose margin exceeds
+    twice that error (the majority)."""
+    _log("bf16 batched decode projections")
+    model = _model(dtype=torch.bfloat16, hidden=2048, q_heads=32, kv_heads=8, layers=2, vocab=32768,
+                   max_seq_len=128)
+    for p in model.parameters():
+        if p.ndim > 1:
+            torch.nn.init.normal_(p, 0.0, 0.02)
+    gen = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, 32768, (16, 24), generator=gen).to(DEV)
+    follow = torch.randint(0, 32768, (16, 6), generator=gen).to(DEV)
+
+    ids = tuple(f"seq-{i}" for i in range(16))
+
+    def run():
+        cache = _cache_for(model, 16 * 3, block_size=16)
+        rows = [model(prompt, kv_cache=cache, sequence_ids=ids)[:, -1]]
+        for t in range(follow.shape[1]):
+            rows.append(model(follow[:, t:t + 1], kv_cache=cache, sequence_ids=ids)[:, -1])
+        return torch.cat(rows).float()
+
+    with torch.inference_mode():
+        hip = run()
+        with torch_gemm():
+            ref = run()
+    err = (hip[16:] - ref[16:]).abs().max().item()
+    assert torch.equal(hip[:16], ref[:16])  # the prefill rows take torch's GEMM in both runs
+    top2 = ref.topk(2, dim=-1).values
+    decisive = (top2[:, 0] - top2[:, 1]) > 2 * err
+    _log(f"  decode logits max_abs_err={err:.3e} decisive rows={int(decisive.sum())}/{len(ref)}")
+    assert 0 < err <= 5e-2
+    assert decisive.float().mean().item() >= 0.5
+    assert torch.equal(hip.argmax(-1)[decisive], ref.argmax(-1)[decisive])

@@ -342,6 +342,20 @@ def test_decoder_kernel_support_checks():
     assert not _native.rms_norm_supported(torch.empty((3, 64), dtype=torch.float16))
 
 
+def test_linear_rows_support_checks():
+    """The projections nie_linear_rows takes (bf16 GPU tensors, at most 16 rows,
+    in-features a multiple of 2048, out-features a multiple of 16); CPU tensors
+    and other shapes stay with torch's GEMM."""
+    x = torch.empty((16, 2048), dtype=torch.bfloat16)
+    w = torch.empty((3072, 2048), dtype=torch.bfloat16)
+    assert not _native.linear_rows_supported(x, w)  # CPU tensors
+    meta = torch.device("meta")
+    xm, wm = x.to(meta), w.to(meta)
+    assert not _native.linear_rows_supported(xm, wm)  # not a GPU device
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        _native.linear_rows(x, w)
+
+
 def test_rope_table_validation():
     """RoPE tables for the fused decode: (rows, head_dim / 2), the query dtype,
     contiguous, the same shape; None means no rotation."""
@@ -435,6 +449,19 @@ def test_library_rejects_bad_decoder_and_fused_arguments():
     assert lib.nie_silu_mul(1, None, 64, p, 64, p, 64, 4, 64, None) < 0  # null gate
     assert lib.nie_silu_mul(1, p + 2, 64, p, 64, p, 64, 4, 64, None) < 0  # misaligned
     assert lib.nie_silu_mul(1, p, 64, p, 64, p, 64, 0, 64, None) == 0  # no rows
+    # nie_linear_rows(dtype, x, x_stride, rows, w, n, k, epilogue, y, y_stride, stream)
+    assert lib.nie_linear_rows(0, p, 2048, 4, p, 64, 2048, 0, p, 64, None) == -2  # fp32 is not built
+    assert lib.nie_linear_rows(1, p, 2048, 17, p, 64, 2048, 0, p, 64, None) == -2  # 17 rows
+    assert lib.nie_linear_rows(1, p, 2048, 0, p, 64, 2048, 0, p, 64, None) == -2  # no rows
+    assert lib.nie_linear_rows(1, p, 1024, 4, p, 64, 1024, 0, p, 64, None) == -2  # k not a multiple of 2048
+    assert lib.nie_linear_rows(1, p, 2048, 4, p, 40, 2048, 0, p, 40, None) == -2  # n not a multiple of 16
+    assert lib.nie_linear_rows(1, p, 2048, 4, p, 64, 2048, 2, p, 64, None) == -1  # unknown epilogue
+    assert lib.nie_linear_rows(1, None, 2048, 4, p, 64, 2048, 0, p, 64, None) == -1  # null x
+    assert lib.nie_linear_rows(1, p + 2, 2048, 4, p, 64, 2048, 0, p, 64, None) == -1  # misaligned x
+    assert lib.nie_linear_rows(1, p, 2052, 4, p, 64, 2048, 0, p, 64, None) == -1  # x rows misaligned
+    assert lib.nie_linear_rows(1, p, 1024, 4, p, 64, 2048, 0, p, 64, None) == -1  # x stride < k
+    assert lib.nie_linear_rows(1, p, 2048, 4, p, 64, 2048, 0, p, 32, None) == -1  # y stride < n
+    assert b"linear_rows" in lib.nie_last_error()
     # nie_paged_decode_append with a batch but no new rows, or one RoPE table only
     args = dict(q=p, k_cache=p, v_cache=p, tables=p, lens=p, out=p)
     base = [1, args["q"], 32 * 64, 64]
