@@ -1206,20 +1206,32 @@ __global__ __launch_bounds__(kLinearWaves* kWave) void linear_rows_kernel(Linear
     }
   };
 
-  // this wave's x operands of the whole k (its eighth of every pass): issued
-  // between passes 0 and 1, so the wait for pass 0 covers them
+  // this wave's x operands of the whole k (its eighth of every pass).  The
+  // loop uses them from its first step, so the compiler waits for them (and
+  // for every load issued before that wait) ahead of the loop.  A workgroup
+  // of one two-pass tile issues them between passes 0 and 1 (that wait is
+  // then the one for pass 0 anyway); a longer stream settles them first, so
+  // the ring starts full after one L2 round trip instead of draining.
   bf16x8_t xa[kKPasses][kChunks];
-  issue(0, std::integral_constant<int, 0>{});
-  {
+  auto load_x = [&]() {
     const bf16_t* xp = a.x + (int64_t)(row_ok ? c : 0) * a.x_stride + wave * kWaveK + 8 * g;
 #pragma unroll
     for (int kp = 0; kp < kKPasses; ++kp) {
 #pragma unroll
       for (int j = 0; j < kChunks; ++j) xa[kp][j] = row_ok ? load_bf16x8(xp + kp * kPassK + 32 * j) : zero;
     }
+  };
+  if (total > 2) {
+    load_x();
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    issue(2, std::integral_constant<int, 2>{});
+  } else {
+    issue(0, std::integral_constant<int, 0>{});
+    load_x();
+    issue(1, std::integral_constant<int, 1>{});
   }
-  issue(1, std::integral_constant<int, 1>{});
-  if (total > 2) issue(2, std::integral_constant<int, 2>{});
 
   v4f acc[kSets];
 #pragma unroll
