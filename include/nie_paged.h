@@ -201,6 +201,27 @@ int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t rows, co
                     int64_t k, int epilogue, void* y, int64_t y_stride, void* stream);
 
 /*
+ * nie_linear_rows with the RMSNorm that precedes the projection folded into
+ * its x operand: h = x (+ residual, rounded to bf16), then
+ * y = epilogue(norm(h) . w^T) with norm(h) = norm_weight * (h / sqrt(mean(h*h)
+ * + eps)) rounded to bf16 — nie_rms_norm's arithmetic (only the order of
+ * the sum of squares differs).  With residual and sum_out, h is also written
+ * to sum_out (rows of k elements, sum_stride apart).  k must be 2048;
+ * norm_weight (k elements) is required; residual and sum_out may be NULL
+ * (sum_out needs residual).  Other arguments as nie_linear_rows.
+ * Replaces, for decode steps: RmsNorm.forward (src/nano_infer_engine/layers/rms_norm.py:25-31)
+ *           with the residual add before it (src/nano_infer_engine/layers/decoder.py:50-51)
+ *           followed by the q/k/v, gate/up or LM-head projection
+ *           (src/nano_infer_engine/layers/attention.py:227-232,
+ *           src/nano_infer_engine/layers/mlp.py:18-22,
+ *           src/nano_infer_engine/models/llama.py:328).
+ */
+int nie_rms_norm_linear_rows(int dtype, const void* x, int64_t x_stride, const void* residual,
+                             int64_t residual_stride, void* sum_out, int64_t sum_stride,
+                             const void* norm_weight, float eps, int64_t rows, const void* w, int64_t n,
+                             int64_t k, int epilogue, void* y, int64_t y_stride, void* stream);
+
+/*
  * Greedy token selection: out[r] = index of the largest of the cols values
  * of row r (element (r, c) at r * row_stride + c), ties to the lowest index,
  * NaN larger than every number — torch.argmax's result.  out is int64.

@@ -1116,6 +1116,9 @@ constexpr int kLinearPassBytes = 32 * 1024;
 constexpr int kLinearStages = 4;
 constexpr int kLinearPlain = 0;
 constexpr int kLinearSiluMul = 1;
+constexpr int kLinearNoNorm = 0;
+constexpr int kLinearNorm = 1;
+constexpr int kLinearNormRes = 2;
 
 struct LinearArgs {
   const bf16_t* x;
@@ -1126,6 +1129,15 @@ struct LinearArgs {
   int64_t k;
   bf16_t* y;
   int64_t y_stride;
+  // RMSNorm folded into the x operand (the kNorm kernels): x is replaced by
+  // norm_w * (h / sqrt(mean(h*h) + eps)), h = x + res (res may be null),
+  // and workgroup 0 writes h to sum_out when both are given
+  const bf16_t* res;
+  int64_t res_stride;
+  bf16_t* sum_out;
+  int64_t sum_stride;
+  const bf16_t* norm_w;
+  float eps;
 };
 
 __device__ __forceinline__ bf16x8_t load_bf16x8(const bf16_t* p) {
@@ -1141,8 +1153,9 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// kKPasses = k / 1024 (2, 4 or 8); grid.x <= the number of tiles.
-template <int kEpi, int kKPasses>
+// kKPasses = k / 1024 (2, 4 or 8; 2 with a norm); grid.x <= the number of tiles.
+// kNorm: kLinearNoNorm, kLinearNorm (RMSNorm of x) or kLinearNormRes (of x + res).
+template <int kEpi, int kKPasses, int kNorm>
 __global__ __launch_bounds__(kLinearWaves* kWave) void linear_rows_kernel(LinearArgs a) {
   constexpr int kSets = kEpi == kLinearSiluMul ? 2 : 1;
   constexpr int kPasses = kSets * kKPasses;             // passes per tile
@@ -1157,8 +1170,16 @@ __global__ __launch_bounds__(kLinearWaves* kWave) void linear_rows_kernel(Linear
   // are then compile-time constants
   constexpr int kTrip = kPasses > kLinearStages ? kPasses : kLinearStages;
   static_assert(kTrip % kPasses == 0 && kTrip % kLinearStages == 0, "trip covers whole tiles and ring turns");
+  static_assert(kNorm == kLinearNoNorm || kKPasses == 2, "the folded RMSNorm is built for k = 2048");
   __shared__ __attribute__((aligned(16))) unsigned char ring[kLinearStages][kLinearPassBytes];
   __shared__ v4f red[kSets][kLinearWaves][kWave];
+  // the folded norm's row totals; its per-vector partial sums of squares
+  // (16 rows x k/8 vectors, 16 KiB) use ring stage 3, which the first pass
+  // to fill it (pass 3, issued after the prologue's last barrier) finds free
+  __shared__ float norm_ss[16];
+  constexpr int kNormVecs = kKPasses * kPassK / 8;
+  static_assert(kNorm == kLinearNoNorm || 16 * kNormVecs * 4 <= kLinearPassBytes, "partials fit a ring stage");
+  float* const norm_part = reinterpret_cast<float*>(&ring[kLinearStages - 1][0]);
 
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
@@ -1221,7 +1242,112 @@ __global__ __launch_bounds__(kLinearWaves* kWave) void linear_rows_kernel(Linear
       for (int j = 0; j < kChunks; ++j) xa[kp][j] = row_ok ? load_bf16x8(xp + kp * kPassK + 32 * j) : zero;
     }
   };
-  if (total > 2) {
+  if constexpr (kNorm != kLinearNoNorm) {
+    // RMSNorm of the rows in the arithmetic of rms_norm_kernel (h = x + res
+    // rounded to bf16, fp32 sum of squares, y = w * (h / sqrt(mean + eps))
+    // rounded once; only the order of the sum of squares differs).  The
+    // loads are unconditional (a row past `rows` reads row 0; its values are
+    // zeroed at the end) and settled by one wait before the first passes'
+    // DMA goes out: conditional loads and loads still pending behind the DMA
+    // would each make the compiler wait for every load in flight.  The
+    // arithmetic then overlaps the DMA.
+    constexpr bool kRes = kNorm == kLinearNormRes;
+    const int64_t kofs = wave * kWaveK + 8 * g;
+    const int64_t row = row_ok ? c : 0;
+    v4u hv[kKPasses][kChunks], nw[kKPasses][kChunks], rv[kRes ? kKPasses : 1][kChunks];
+#pragma unroll
+    for (int kp = 0; kp < kKPasses; ++kp) {
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) {
+        const int64_t col = kofs + kp * kPassK + 32 * j;
+        hv[kp][j] = *reinterpret_cast<const v4u*>(a.x + row * a.x_stride + col);
+        nw[kp][j] = *reinterpret_cast<const v4u*>(a.norm_w + col);
+        if constexpr (kRes) rv[kp][j] = *reinterpret_cast<const v4u*>(a.res + row * a.res_stride + col);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    if (total > 2) issue(2, std::integral_constant<int, 2>{});
+    // The sum of squares in rms_norm_kernel's order at k = 2048 (256 threads,
+    // one 16-byte vector each): an fma chain over the vector's 8 elements, an
+    // xor butterfly over each 64 vectors, the four sums added in order.  The
+    // norm is then bit-identical to nie_rms_norm's.
+#pragma unroll
+    for (int kp = 0; kp < kKPasses; ++kp) {
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) {
+        if constexpr (kRes) {
+          v4u sum;
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) {
+            sum[w2] = pack_bf16x2(vec_elt<bf16_t>(hv[kp][j], 2 * w2) + vec_elt<bf16_t>(rv[kp][j], 2 * w2),
+                                  vec_elt<bf16_t>(hv[kp][j], 2 * w2 + 1) + vec_elt<bf16_t>(rv[kp][j], 2 * w2 + 1));
+          }
+          hv[kp][j] = sum;
+        }
+        float ssv = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float h = vec_elt<bf16_t>(hv[kp][j], e);
+          ssv = fmaf(h, h, ssv);
+        }
+        // vector index of (row c, column kofs + kp*1024 + 32 j)
+        const int v = (int)((kofs + kp * kPassK + 32 * j) / 8);
+        asm volatile("s_nop 1\n\tds_write_b32 %0, %1" ::"v"(lds_off(&norm_part[c * kNormVecs + v])), "v"(ssv)
+                     : "memory");
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // wave w reduces rows 2w and 2w + 1: lane l takes vectors 64 q + l
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = 2 * wave + rr;
+      uint32_t addr[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) addr[q] = lds_off(&norm_part[r * kNormVecs + 64 * q + lane]);
+      uint32_t pv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) asm volatile("ds_read_b32 %0, %1" : "=v"(pv[q]) : "v"(addr[q]));
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(pv[0]), "+v"(pv[1]), "+v"(pv[2]), "+v"(pv[3]));
+      float row_ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float t = __uint_as_float(pv[q]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+        row_ss += t;
+      }
+      if (lane == 0) {
+        asm volatile("s_nop 1\n\tds_write_b32 %0, %1" ::"v"(lds_off(&norm_ss[r])), "v"(row_ss) : "memory");
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t total_bits;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(total_bits) : "v"(lds_off(&norm_ss[c])));
+    const float denom = sqrtf(__uint_as_float(total_bits) * (1.f / (float)(kKPasses * kPassK)) + a.eps);
+    const bool write_sum = kRes && blockIdx.x == 0 && a.sum_out != nullptr && row_ok;
+#pragma unroll
+    for (int kp = 0; kp < kKPasses; ++kp) {
+#pragma unroll
+      for (int j = 0; j < kChunks; ++j) {
+        if (write_sum) {
+          *reinterpret_cast<v4u*>(a.sum_out + (int64_t)c * a.sum_stride + kofs + kp * kPassK + 32 * j) = hv[kp][j];
+        }
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = vec_elt<bf16_t>(nw[kp][j], e) * (vec_elt<bf16_t>(hv[kp][j], e) / denom);
+        v4u o;
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2) o[w2] = row_ok ? pack_bf16x2(y[2 * w2], y[2 * w2 + 1]) : 0u;
+        xa[kp][j] = __builtin_bit_cast(bf16x8_t, o);
+      }
+    }
+  } else if (total > 2) {
     load_x();
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     issue(0, std::integral_constant<int, 0>{});
@@ -3219,8 +3345,10 @@ NIE_API int nie_rms_norm(int dtype, const void* x, int64_t x_stride, const void*
   return launched("rms_norm");
 }
 
-NIE_API int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t rows, const void* w, int64_t n,
-                            int64_t k, int epilogue, void* y, int64_t y_stride, void* stream) {
+namespace {
+
+int check_linear(int dtype, const void* x, int64_t x_stride, int64_t rows, const void* w, int64_t n, int64_t k,
+                 int epilogue, void* y, int64_t y_stride) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
   if (dtype != NIE_DTYPE_BF16) return fail(NIE_EUNSUPPORTED, "linear_rows: only bf16 is built");
@@ -3242,6 +3370,11 @@ NIE_API int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t 
   if (!check_aligned(x, x_stride, 0, 2) || !check_aligned(w, 0, 0, 2) || ((uintptr_t)y % 2) != 0) {
     return fail(NIE_EINVAL, "linear_rows: x rows and the weight must be 16-byte aligned");
   }
+  return NIE_OK;
+}
+
+LinearArgs linear_args(const void* x, int64_t x_stride, int64_t rows, const void* w, int64_t n, int64_t k, void* y,
+                       int64_t y_stride) {
   LinearArgs a;
   a.x = reinterpret_cast<const bf16_t*>(x);
   a.x_stride = x_stride;
@@ -3251,25 +3384,80 @@ NIE_API int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t 
   a.k = k;
   a.y = reinterpret_cast<bf16_t*>(y);
   a.y_stride = y_stride;
-  hipStream_t s = (hipStream_t)stream;
+  a.res = nullptr;
+  a.res_stride = 0;
+  a.sum_out = nullptr;
+  a.sum_stride = 0;
+  a.norm_w = nullptr;
+  a.eps = 0.f;
+  return a;
+}
+
+template <bool kNorm>
+int launch_linear(const LinearArgs& a, int epilogue, hipStream_t s) {
   // one workgroup per CU (the ring takes 128 KiB of LDS), at most one per tile
-  const int64_t tiles = n / 16;
+  const int64_t tiles = a.n / 16;
   const dim3 grid((unsigned)(tiles < kDecodeCUs ? tiles : kDecodeCUs)), block(kLinearWaves * kWave);
   const bool silu = epilogue == NIE_LINEAR_SILU_MUL;
-  switch (k) {
-    case 2048:
-      if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 2>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 2>), grid, block, 0, s, a);
-      break;
-    case 4096:
-      if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 4>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 4>), grid, block, 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 8>), grid, block, 0, s, a);
-      break;
+  if constexpr (kNorm) {
+    if (a.res != nullptr) {
+      if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 2, kLinearNormRes>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 2, kLinearNormRes>), grid, block, 0, s, a);
+    } else {
+      if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 2, kLinearNorm>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 2, kLinearNorm>), grid, block, 0, s, a);
+    }
+  } else {
+    switch (a.k) {
+      case 2048:
+        if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 2, kLinearNoNorm>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 2, kLinearNoNorm>), grid, block, 0, s, a);
+        break;
+      case 4096:
+        if (silu) hipLaunchKernelGGL((linear_rows_kernel<kLinearSiluMul, 4, kLinearNoNorm>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 4, kLinearNoNorm>), grid, block, 0, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL((linear_rows_kernel<kLinearPlain, 8, kLinearNoNorm>), grid, block, 0, s, a);
+        break;
+    }
   }
   return launched("linear_rows_kernel");
+}
+
+}  // namespace
+
+NIE_API int nie_linear_rows(int dtype, const void* x, int64_t x_stride, int64_t rows, const void* w, int64_t n,
+                            int64_t k, int epilogue, void* y, int64_t y_stride, void* stream) {
+  const int rc = check_linear(dtype, x, x_stride, rows, w, n, k, epilogue, y, y_stride);
+  if (rc) return rc;
+  return launch_linear<false>(linear_args(x, x_stride, rows, w, n, k, y, y_stride), epilogue, (hipStream_t)stream);
+}
+
+NIE_API int nie_rms_norm_linear_rows(int dtype, const void* x, int64_t x_stride, const void* residual,
+                                     int64_t residual_stride, void* sum_out, int64_t sum_stride,
+                                     const void* norm_weight, float eps, int64_t rows, const void* w, int64_t n,
+                                     int64_t k, int epilogue, void* y, int64_t y_stride, void* stream) {
+  const int rc = check_linear(dtype, x, x_stride, rows, w, n, k, epilogue, y, y_stride);
+  if (rc) return rc;
+  if (k != 2048) return fail(NIE_EUNSUPPORTED, "rms_norm_linear_rows: inner size %lld (2048 is built)", (long long)k);
+  if (!norm_weight) return fail(NIE_EINVAL, "rms_norm_linear_rows: null norm weight");
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(NIE_EINVAL, "rms_norm_linear_rows: eps must be finite and >= 0");
+  if (!check_aligned(norm_weight, 0, 0, 2)) return fail(NIE_EINVAL, "rms_norm_linear_rows: misaligned norm weight");
+  if (residual != nullptr && (residual_stride < k || !check_aligned(residual, residual_stride, 0, 2))) {
+    return fail(NIE_EINVAL, "rms_norm_linear_rows: residual rows shorter than k or misaligned");
+  }
+  if (sum_out != nullptr && (residual == nullptr || sum_stride < k || !check_aligned(sum_out, sum_stride, 0, 2))) {
+    return fail(NIE_EINVAL, "rms_norm_linear_rows: sum_out needs a residual and aligned rows of k elements");
+  }
+  LinearArgs a = linear_args(x, x_stride, rows, w, n, k, y, y_stride);
+  a.res = reinterpret_cast<const bf16_t*>(residual);
+  a.res_stride = residual_stride;
+  a.sum_out = reinterpret_cast<bf16_t*>(sum_out);
+  a.sum_stride = sum_stride;
+  a.norm_w = reinterpret_cast<const bf16_t*>(norm_weight);
+  a.eps = eps;
+  return launch_linear<true>(a, epilogue, (hipStream_t)stream);
 }
 
 NIE_API int nie_silu_mul(int dtype, const void* gate, int64_t gate_stride, const void* up, int64_t up_stride,

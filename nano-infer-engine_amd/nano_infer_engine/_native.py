@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "nie_rms_norm",
     "nie_silu_mul",
     "nie_linear_rows",
+    "nie_rms_norm_linear_rows",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
@@ -85,6 +86,10 @@ _SIGNATURES = {
     ),
     "nie_silu_mul": (_i32, [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr]),
     "nie_linear_rows": (_i32, [_i32, _ptr, _i64, _i64, _ptr, _i64, _i64, _i32, _ptr, _i64, _ptr]),
+    "nie_rms_norm_linear_rows": (
+        _i32,
+        [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _f32, _i64, _ptr, _i64, _i64, _i32, _ptr, _i64, _ptr],
+    ),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
@@ -504,6 +509,54 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, silu_mul: bool = False) -
     )
     _check(rc, "nie_linear_rows")
     return out.view(*x.shape[:-1], n_out)
+
+
+RMS_NORM_LINEAR_K = 2048
+
+
+def rms_norm_linear_rows(
+    x: torch.Tensor,
+    residual: torch.Tensor | None,
+    norm_weight: torch.Tensor,
+    eps: float,
+    weight: torch.Tensor,
+    silu_mul: bool = False,
+    want_sum: bool = True,
+) -> tuple[torch.Tensor | None, torch.Tensor]:
+    """``RmsNorm(x + residual)`` then ``F.linear(., weight)`` in one launch (nie_rms_norm_linear_rows).
+
+    Returns ``(x + residual, y)`` (the sum is None without a residual or with
+    ``want_sum=False``); ``silu_mul`` as for :func:`linear_rows`.  The norm's
+    arithmetic is ``rms_norm``'s (``layers/rms_norm.py:25-31``).
+    """
+    _require_gpu(x, weight, norm_weight)
+    if not linear_rows_supported(x, weight) or weight.shape[1] != RMS_NORM_LINEAR_K:
+        raise RuntimeError(f"nie_rms_norm_linear_rows does not take x {tuple(x.shape)} {x.dtype} with weight "
+                           f"{tuple(weight.shape)} {weight.dtype}")
+    n, k = weight.shape
+    if norm_weight.shape != (k,) or norm_weight.dtype != x.dtype or norm_weight.device != x.device:
+        raise ValueError("norm_weight must be a (k,) tensor of x's dtype on the device of x")
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
+                                 or residual.device != x.device):
+        raise ValueError("residual must match x")
+    if silu_mul and n % 32 != 0:
+        raise RuntimeError("a [gate; up] weight needs a multiple of 32 rows")
+    n_out = n // 2 if silu_mul else n
+    xs = _aligned(_norm_rows(x, k))
+    rows = xs.shape[0]
+    rs = None if residual is None else _aligned(_norm_rows(residual, k))
+    nw = _aligned(norm_weight.detach().contiguous())
+    w = _aligned(weight.detach() if weight.is_contiguous() else weight.detach().contiguous())
+    out = torch.empty((rows, n_out), dtype=x.dtype, device=x.device)
+    sum_out = torch.empty((rows, k), dtype=x.dtype, device=x.device) if (want_sum and rs is not None) else None
+    rc = load_library().nie_rms_norm_linear_rows(
+        dtype_code(x.dtype), xs.data_ptr(), xs.stride(0) if rows > 1 else k,
+        None if rs is None else rs.data_ptr(), 0 if rs is None else (rs.stride(0) if rows > 1 else k),
+        None if sum_out is None else sum_out.data_ptr(), k, nw.data_ptr(), float(eps), rows, w.data_ptr(), n_out, k,
+        LINEAR_SILU_MUL if silu_mul else LINEAR_PLAIN, out.data_ptr(), n_out, _stream(x.device),
+    )
+    _check(rc, "nie_rms_norm_linear_rows")
+    return (None if sum_out is None else sum_out.view(x.shape)), out.view(*x.shape[:-1], n_out)
 
 
 def kv_gather(

@@ -66,13 +66,34 @@ class GroupedQueryAttention(nn.Module):
         ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
         if not x.is_cuda or (torch.is_grad_enabled() and any(w.requires_grad for w in ws)):
             return self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        qkv = _linear.linear(x, self._stacked_qkv_weight())
+        return qkv.split((ws[0].shape[0], ws[1].shape[0], ws[2].shape[0]), dim=-1)
+
+    def _stacked_qkv_weight(self) -> torch.Tensor:
+        """[q; k; v] weight rows, rebuilt whenever one of them changes."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
         key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
         if key != self._qkv_key:
             with torch.no_grad():
                 self._qkv_weight = torch.cat(ws, dim=0)
             self._qkv_key = key
-        qkv = _linear.linear(x, self._qkv_weight)
-        return qkv.split((ws[0].shape[0], ws[1].shape[0], ws[2].shape[0]), dim=-1)
+        return self._qkv_weight
+
+    def project_qkv_normed(self, x: torch.Tensor, residual: torch.Tensor | None, norm: nn.Module):
+        """``h = x + residual`` (``x`` without one), then q, k, v of ``norm(h)``:
+        the pre-attention norm folded into the projection GEMM (one launch for
+        a decode step's rows).  Returns ``(h, q, k, v)``, or None when the HIP
+        path does not take the shapes (callers then norm and project apart)."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        if (not x.is_cuda or any(p.bias is not None for p in (self.q_proj, self.k_proj, self.v_proj))
+                or (torch.is_grad_enabled() and any(w.requires_grad for w in ws))):
+            return None
+        r = _linear.rms_norm_linear(x, residual, norm, self._stacked_qkv_weight())
+        if r is None:
+            return None
+        h, qkv = r
+        q, k, v = qkv.split((ws[0].shape[0], ws[1].shape[0], ws[2].shape[0]), dim=-1)
+        return (x if h is None else h), q, k, v
 
     # ------------------------------------------------------------------
     def forward_tokens(
@@ -81,10 +102,15 @@ class GroupedQueryAttention(nn.Module):
         paged_cache: PagedKVCache,
         layer_index: int,
         batch: RaggedBatch,
+        *,
+        qkv: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     ) -> torch.Tensor:
-        """Attention for packed tokens x (num_tokens, hidden) described by ``batch``."""
-        tokens = x.shape[0]
-        q, k, v = self._project_qkv(x)
+        """Attention for packed tokens x (num_tokens, hidden) described by ``batch``.
+
+        ``qkv``: the tokens' projections, already computed (``x`` is then unused).
+        """
+        q, k, v = self._project_qkv(x) if qkv is None else qkv
+        tokens = q.shape[0]
         q = q.view(tokens, self.q_head_num, self.head_dim)
         k = k.view(tokens, self.kv_head_num, self.head_dim)
         v = v.view(tokens, self.kv_head_num, self.head_dim)

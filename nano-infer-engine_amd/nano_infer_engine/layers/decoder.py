@@ -59,10 +59,21 @@ class Llama3Decoder(nn.Module):
         ``(ffn_out, h)``, whose sum ``ffn_out + h`` is the block's output
         (reference ``layers/decoder.py:50-51``).
         """
-        if isinstance(x, tuple):
-            x, normed = self.pre_norm.forward_add(*x)
+        a, b = x if isinstance(x, tuple) else (x, None)
+        # a decode step's rows: each norm (with the residual add before it)
+        # runs inside the projection GEMM that consumes it
+        fused = self.attn.project_qkv_normed(a, b, self.pre_norm)
+        if fused is not None:
+            x, q, k, v = fused
+            attn = self.attn.forward_tokens(None, paged_cache, layer_index, batch, qkv=(q, k, v))
         else:
-            normed = self.pre_norm(x)
-        attn = self.attn.forward_tokens(normed, paged_cache, layer_index, batch)
+            if b is not None:
+                x, normed = self.pre_norm.forward_add(a, b)
+            else:
+                x, normed = a, self.pre_norm(a)
+            attn = self.attn.forward_tokens(normed, paged_cache, layer_index, batch)
+        out = self.ffn.forward_normed(attn, x, self.post_norm)
+        if out is not None:
+            return out
         h, normed = self.post_norm.forward_add(attn, x)
         return self.ffn(normed), h

@@ -56,3 +56,33 @@ def silu_mul_linear(x: torch.Tensor, gate_up_weight: torch.Tensor, inner: int) -
     if gate_up_weight.shape[0] != 2 * inner or not _native_ok(x, gate_up_weight) or inner % 16:
         return None
     return _native.linear_rows(x, gate_up_weight, silu_mul=True)
+
+
+def rms_norm_linear(x: torch.Tensor, residual: torch.Tensor | None, norm: nn.Module, weight: torch.Tensor,
+                    silu_mul: bool = False, want_sum: bool = True):
+    """``(x + residual, linear(norm(x + residual), weight))`` in one launch
+    (``silu_mul``: the SwiGLU product of a stacked ``[gate; up]`` weight), or
+    None when the HIP path does not take the shapes.  ``norm`` is an
+    ``RmsNorm`` with a weight; the sum is None without a residual.
+
+    Not while a HIP graph is being captured: the folded norm saves a launch,
+    but each of the GEMM's workgroups reads x and the residual again (128 KiB
+    each), which costs more GPU time than the separate norm kernel once
+    launches are replayed from a graph (8273 against 7812 output tok/s on the
+    serving workload); launched one by one (eager steps: 5410 against 4296)
+    the saved launch wins."""
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    nw = getattr(norm, "weight", None)
+    if nw is None or nw.shape != (x.shape[-1],) or nw.dtype != x.dtype or nw.device != x.device:
+        return None
+    if weight.ndim != 2 or weight.shape[1] != _native.RMS_NORM_LINEAR_K or not _native_ok(x, weight):
+        return None
+    if torch.is_grad_enabled() and nw.requires_grad:
+        return None
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
+                                 or residual.device != x.device):
+        return None
+    if silu_mul and weight.shape[0] % 32:
+        return None
+    return _native.rms_norm_linear_rows(x, residual, nw, norm.eps, weight, silu_mul=silu_mul, want_sum=want_sum)

@@ -21,17 +21,38 @@ class SwiGLUMLP(nn.Module):
         self._gate_up_weight: torch.Tensor | None = None
         self._gate_up_key: tuple | None = None
 
+    def _stacked_gate_up_weight(self) -> torch.Tensor:
+        ws = (self.gate_proj.weight, self.up_proj.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        if key != self._gate_up_key:
+            with torch.no_grad():
+                self._gate_up_weight = torch.cat(ws, dim=0)
+            self._gate_up_key = key
+        return self._gate_up_weight
+
+    def forward_normed(self, x, residual, norm):
+        """``(self(norm(h)), h)`` for ``h = x + residual``, with the residual add
+        and the norm folded into the gate/up GEMM and its SwiGLU epilogue (one
+        launch for a decode step's rows), or None when the HIP path does not
+        take the shapes."""
+        ws = (self.gate_proj.weight, self.up_proj.weight)
+        if (not x.is_cuda or ws[0].shape != ws[1].shape
+                or any(p.bias is not None for p in (self.gate_proj, self.up_proj))
+                or (torch.is_grad_enabled() and any(w.requires_grad for w in ws))):
+            return None
+        r = _linear.rms_norm_linear(x, residual, norm, self._stacked_gate_up_weight(), silu_mul=True)
+        if r is None:
+            return None
+        h, act = r
+        return _linear.apply(self.down_proj, act), h
+
     def forward(self, x):
         ws = (self.gate_proj.weight, self.up_proj.weight)
         if x.is_cuda and not (torch.is_grad_enabled() and any(w.requires_grad for w in ws)):
             # one GEMM over the concatenated weights (a captured decode graph
             # keeps the concatenation it was captured with), then
             # silu(gate) * up in one HIP kernel over the two halves
-            key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
-            if key != self._gate_up_key:
-                with torch.no_grad():
-                    self._gate_up_weight = torch.cat(ws, dim=0)
-                self._gate_up_key = key
+            self._stacked_gate_up_weight()
             if ws[0].shape == ws[1].shape:
                 # a decode step's rows: both projections and the gated
                 # product in one HIP GEMM

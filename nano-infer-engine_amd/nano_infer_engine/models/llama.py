@@ -144,6 +144,12 @@ class Llama3_2(nn.Module):
         ffn_out, h = x
         if logits_rows is not None:
             ffn_out, h = ffn_out[logits_rows], h[logits_rows]
+        if self.lm_head.bias is None:
+            # a decode step's rows: the final norm and its residual add inside
+            # the LM-head GEMM
+            r = _linear.rms_norm_linear(ffn_out, h, self.final_rms, self.lm_head.weight, want_sum=False)
+            if r is not None:
+                return r[1]
         return _linear.apply(self.lm_head, self.final_rms.forward_add(ffn_out, h)[1])
 
     def _new_cache_for(self, batch_size: int, seq_len: int, device: torch.device) -> tuple[PagedKVCache, tuple[str, ...]]:

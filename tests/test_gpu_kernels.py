@@ -661,3 +661,62 @@ def test_linear_rows_rejects_unsupported_shapes_on_the_gpu():
         _native.linear_rows(x, w)
     assert not _native.linear_rows_supported(x[:4, :1024], w[:, :1024])
     assert _native.linear_rows_supported(x[:16], w)
+
+
+@pytest.mark.parametrize("rows", [1, 7, 16])
+@pytest.mark.parametrize("with_residual", [False, True])
+@pytest.mark.parametrize("silu", [False, True])
+def test_rms_norm_linear_rows_matches_norm_then_product(rows, with_residual, silu):
+    """nie_rms_norm_linear_rows, each stage against its own bar:
+    - the residual sum bit for bit (x + residual in bf16);
+    - the folded norm's operand (read back exactly through an identity
+      weight) bit for bit equal to nie_rms_norm's output (the kernel reduces
+      the sum of squares in rms_norm_kernel's order), and against the
+      reference norm formula in fp32 as nie_rms_norm is held: within one
+      bf16 ulp, < 1% of elements off;
+    - the product against float64 over that operand: half an ulp for the
+      plain epilogue, the SwiGLU epilogue as for nie_linear_rows."""
+    k, n = 2048, (2 * 4096 if silu else 3072)
+    _log(f"rms_norm_linear_rows rows={rows} residual={with_residual} silu={silu}")
+    gen = torch.Generator().manual_seed(rows * 100 + with_residual * 10 + silu)
+    x = torch.randn((rows, k), generator=gen).to(torch.bfloat16)
+    res = torch.randn((rows, k), generator=gen).to(torch.bfloat16) if with_residual else None
+    nw = (1 + 0.1 * torch.randn(k, generator=gen)).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=gen) * (3 if silu else 1) / k**0.5).to(torch.bfloat16)
+    dx, dnw = x.to(DEV), nw.to(DEV)
+    dres = None if res is None else res.to(DEV)
+    s_got, got = _native.rms_norm_linear_rows(dx, dres, dnw, 1e-5, w.to(DEV), silu_mul=silu)
+    _, xn_k = _native.rms_norm_linear_rows(dx, dres, dnw, 1e-5, torch.eye(k, dtype=torch.bfloat16, device=DEV),
+                                           want_sum=False)
+    torch.cuda.synchronize()
+    h = x + res if res is not None else x
+    if res is not None:
+        assert torch.equal(s_got.cpu(), h)
+    else:
+        assert s_got is None
+    if dres is not None:
+        _, sep_norm = _native.rms_norm(dx, dnw, 1e-5, residual=dres)
+    else:
+        sep_norm = _native.rms_norm(dx, dnw, 1e-5)
+    torch.cuda.synchronize()
+    xn_k = xn_k.cpu()
+    assert torch.equal(xn_k, sep_norm.cpu())
+    xn = _rms_norm_reference(h, nw, 1e-5).float()
+    n_rel = ((xn_k.float() - xn).abs() / xn.abs().clamp_min(1e-3)).max().item()
+    n_mism = (xn_k.float() != xn).float().mean().item()
+    _log(f"  norm operand: max_rel_err={n_rel:.3e} mismatching={n_mism:.5f}")
+    assert n_rel <= 2.0**-7 and n_mism < 0.01
+    prod = xn_k.double() @ w.double().T
+    got = got.cpu().float()
+    if silu:
+        gate = prod[:, : n // 2].to(torch.bfloat16).float()
+        up = prod[:, n // 2:].to(torch.bfloat16).float()
+        want = (torch.nn.functional.silu(gate).to(torch.bfloat16).float() * up).to(torch.bfloat16).float()
+        rel = ((got - want).abs() / want.abs().clamp_min(1e-3)).max().item()
+        mism = (got != want).float().mean().item()
+        _log(f"  product: max_rel_err={rel:.3e} mismatching={mism:.5f}")
+        assert rel <= 2.0**-5 and mism < 0.01
+    else:
+        err = ((got.double() - prod).abs() - prod.abs() * 2.0**-8).max().item()
+        _log(f"  product: excess over half an ulp={err:.3e}")
+        assert err <= 1e-5

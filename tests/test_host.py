@@ -462,6 +462,19 @@ def test_library_rejects_bad_decoder_and_fused_arguments():
     assert lib.nie_linear_rows(1, p, 1024, 4, p, 64, 2048, 0, p, 64, None) == -1  # x stride < k
     assert lib.nie_linear_rows(1, p, 2048, 4, p, 64, 2048, 0, p, 32, None) == -1  # y stride < n
     assert b"linear_rows" in lib.nie_last_error()
+    # nie_rms_norm_linear_rows(dtype, x, xs, res, rs, sum, ss, norm_w, eps, rows, w, n, k, epi, y, ys, stream)
+    assert lib.nie_rms_norm_linear_rows(1, p, 4096, None, 0, None, 0, p, 1e-5, 4, p, 64, 4096, 0, p, 64, None) == -2
+    assert lib.nie_rms_norm_linear_rows(1, p, 2048, None, 0, None, 0, None, 1e-5, 4, p, 64, 2048, 0, p, 64,
+                                        None) == -1  # no norm weight
+    assert lib.nie_rms_norm_linear_rows(1, p, 2048, None, 0, p, 2048, p, 1e-5, 4, p, 64, 2048, 0, p, 64,
+                                        None) == -1  # sum_out without a residual
+    assert lib.nie_rms_norm_linear_rows(1, p, 2048, p, 1024, None, 0, p, 1e-5, 4, p, 64, 2048, 0, p, 64,
+                                        None) == -1  # residual rows shorter than k
+    assert lib.nie_rms_norm_linear_rows(1, p, 2048, None, 0, None, 0, p, -1.0, 4, p, 64, 2048, 0, p, 64,
+                                        None) == -1  # negative eps
+    assert lib.nie_rms_norm_linear_rows(1, p, 2048, None, 0, None, 0, p + 2, 1e-5, 4, p, 64, 2048, 0, p, 64,
+                                        None) == -1  # misaligned norm weight
+    assert b"rms_norm_linear_rows" in lib.nie_last_error()
     # nie_paged_decode_append with a batch but no new rows, or one RoPE table only
     args = dict(q=p, k_cache=p, v_cache=p, tables=p, lens=p, out=p)
     base = [1, args["q"], 32 * 64, 64]
