@@ -50,6 +50,8 @@ def parse_args():
     p.add_argument("--e2e-ref-steps", type=int, default=3,
                    help="scheduler steps timed with the reference attention algorithm")
     p.add_argument("--mixed-only", action="store_true", help="run only the mixed chunked-prefill figure")
+    p.add_argument("--linear-only", action="store_true",
+                   help="run only the decode-step projection GEMM figure (nie_linear_rows vs torch's GEMM)")
     p.add_argument("--stress-only", action="store_true",
                    help="run only the 16x29600 decode figure (for per-workload profiles)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -448,6 +450,70 @@ def run_e2e(args):
     }
 
 
+def run_linear(args):
+    """Decode-step projections of the Llama-3.2-1B shape at 16 rows, bf16:
+    nie_linear_rows against torch's GEMM (F.linear, hipBLASLt), each timed
+    over 20 calls replayed from a captured HIP graph (launch overhead out),
+    the calls rotating over weight copies that together exceed the 256 MB
+    last-level cache.  Bytes = the weight (2 n k); the gate/up row is the
+    fused SwiGLU epilogue against F.linear + nie_silu_mul."""
+    import torch
+    import torch.nn.functional as F
+
+    from nano_infer_engine import _native
+
+    device = torch.device("cuda:0")
+    shapes = [("q/k/v", 3072, 2048, False), ("o_proj", 2048, 2048, False),
+              ("gate/up + SiLU", 16384, 2048, True), ("down", 2048, 8192, False),
+              ("LM head", 128256, 2048, False)]
+    calls = 20
+    out = {}
+    for name, n, k, glu in shapes:
+        copies = max(2, min(calls, int(1.5e9 // (n * k * 2))))
+        gen = torch.Generator(device=device).manual_seed(n)
+        ws = [torch.randn((n, k), generator=gen, device=device).to(torch.bfloat16) for _ in range(copies)]
+        x = torch.randn((16, k), generator=gen, device=device).to(torch.bfloat16)
+
+        def ours(i):
+            return _native.linear_rows(x, ws[i % copies], silu_mul=glu)
+
+        def lib(i):
+            y = F.linear(x, ws[i % copies])
+            if glu:
+                g, u = y.split((n // 2, n // 2), dim=-1)
+                return _native.silu_mul(g, u)
+            return y
+
+        res = {}
+        for tag, fn in (("nie_linear_rows", ours), ("torch", lib)):
+            for i in range(3):
+                fn(i)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(calls):
+                    fn(i)
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 5
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            res[tag] = e0.elapsed_time(e1) * 1e3 / (reps * calls)
+            del graph
+        gbs = n * k * 2 / (res["nie_linear_rows"] * 1e-6) / 1e9
+        out[name] = {"n": n, "k": k, "us": round(res["nie_linear_rows"], 2), "GBs": round(gbs, 1),
+                     "frac": round(gbs / 8000.0, 4), "torch_us": round(res["torch"], 2)}
+        log(f"{name:15s} {n}x{k}: nie_linear_rows {res['nie_linear_rows']:.2f} us ({gbs:.0f} GB/s), "
+            f"torch {res['torch']:.2f} us")
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def _measured_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if present."""
     path = os.path.join(REPO, "profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json")
@@ -525,6 +591,12 @@ def main():
 
         _native.load_library()
         print(json.dumps({"mixed_prefill_step": run_mixed(args)}), flush=True)
+        return
+    if args.linear_only:
+        from nano_infer_engine import _native
+
+        _native.load_library()
+        print(json.dumps({"decode_projections": run_linear(args)}), flush=True)
         return
     if args.stress_only:
         from nano_infer_engine import _native

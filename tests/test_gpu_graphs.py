@@ -43,6 +43,12 @@ def test_argmax_rows_matches_torch(dtype):
     got = _native.argmax_rows(logits)
     assert torch.equal(got, logits.argmax(dim=-1))
     aligned = torch.randn((16, 128256), generator=gen, device=DEV).to(dtype)
+    # the vector path loads 8 vectors per thread at once: a tie across those
+    # batches, the row's last element, NaN, an all-equal row
+    aligned[0, 5] = aligned[0, 128000] = 100.0
+    aligned[1, 128255] = 100.0
+    aligned[2, 64000] = float("nan")
+    aligned[3] = 1.0
     assert torch.equal(_native.argmax_rows(aligned), aligned.argmax(dim=-1))
 
 
