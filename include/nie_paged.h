@@ -234,6 +234,20 @@ int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t cols, i
                     int64_t* out, void* stream);
 
 /*
+ * nie_argmax_rows for long rows: one workgroup per piece of 8192 columns of
+ * a row, then a merge of the pieces' (value, index) pairs; the result is
+ * nie_argmax_rows's (the comparison is a strict total order).  workspace:
+ * device memory of nie_argmax_rows_workspace_bytes(rows, cols) bytes,
+ * 16-byte aligned, no initialisation needed; calls that overlap in time need
+ * different workspaces.
+ * Replaces: as nie_argmax_rows (src/nano_infer_engine/generation/scheduler.py:399-401),
+ *           for LM-head rows of 128256 logits.
+ */
+int64_t nie_argmax_rows_workspace_bytes(int64_t rows, int64_t cols);
+int nie_argmax_rows_split(int dtype, const void* logits, int64_t rows, int64_t cols, int64_t row_stride,
+                          int64_t* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Workspace bytes needed by nie_paged_decode for a call with these
  * arguments (same meaning as there; host values), whose sequence lengths
  * have maximum max_seq_len and sum total_seq_len, and the same optional

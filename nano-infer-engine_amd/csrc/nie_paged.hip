@@ -29,6 +29,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -710,20 +711,35 @@ __device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int6
 
 constexpr int kArgmaxThreads = 1024;
 
-// One workgroup per row; each thread scans 16-byte vectors of the row
-// (a scalar tail covers rows whose length or start is not vector aligned),
-// then the workgroup reduces (value, index) through LDS.
+// (value, index) of a piece of a row, for nie_argmax_rows_split's second pass.
+struct ArgmaxPartial {
+  float value;
+  int32_t pad;
+  int64_t index;
+};
+constexpr int64_t kArgmaxPieceCols = 8192;  // one 16-byte bf16 vector per thread
+
+// One workgroup per row (grid.y == 1), or per (row, piece of
+// kArgmaxPieceCols columns) with `partial` set; each thread scans 16-byte
+// vectors of its columns (a scalar tail covers rows whose length or start is
+// not vector aligned), then the workgroup reduces (value, index) through LDS
+// and writes the row's index, or the piece's pair to partial[row * grid.y +
+// piece].
 template <typename T>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const void* logits, int64_t row_stride,
-                                                                     int64_t cols, int64_t* out) {
+                                                                     int64_t cols, int64_t* out,
+                                                                     ArgmaxPartial* partial) {
   constexpr int kPerVec = 16 / Elt<T>::kBytes;
   const int64_t row = blockIdx.x;
   const T* x = reinterpret_cast<const T*>(logits) + row * row_stride;
+  const int64_t c0 = partial != nullptr ? (int64_t)blockIdx.y * kArgmaxPieceCols : 0;
+  const int64_t c1 = partial != nullptr && c0 + kArgmaxPieceCols < cols ? c0 + kArgmaxPieceCols : cols;
   float best = kNegInf;
   int64_t best_i = cols;  // past the end: loses every comparison with a real element
   const bool vec = ((uintptr_t)x % 16) == 0;
+  const int64_t vec_end = vec ? c1 / kPerVec : 0;  // c0 is a multiple of kPerVec
   const int64_t nvec = vec ? cols / kPerVec : 0;
-  for (int64_t j = threadIdx.x; j < nvec; j += kArgmaxThreads) {
+  for (int64_t j = c0 / kPerVec + threadIdx.x; j < vec_end; j += kArgmaxThreads) {
     const uint4 w = reinterpret_cast<const uint4*>(x)[j];
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -741,7 +757,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const void*
       }
     }
   }
-  for (int64_t i = nvec * kPerVec + threadIdx.x; i < cols; i += kArgmaxThreads) {
+  for (int64_t i = (nvec * kPerVec > c0 ? nvec * kPerVec : c0) + threadIdx.x; i < c1; i += kArgmaxThreads) {
     const float v = load_elt<T>(x, i);
     if (argmax_better(v, i, best, best_i)) {
       best = v;
@@ -773,8 +789,39 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const void*
         best_i = s_idx[w];
       }
     }
-    out[row] = best_i;
+    if (partial != nullptr) {
+      partial[row * gridDim.y + blockIdx.y] = ArgmaxPartial{best, 0, best_i};
+    } else {
+      out[row] = best_i;
+    }
   }
+}
+
+// Second pass of nie_argmax_rows_split: one wave per row over its pieces'
+// pairs (argmax_better is a strict total order, so the pieces' order of
+// combination does not change the result).
+__global__ __launch_bounds__(kWave) void argmax_merge_kernel(const ArgmaxPartial* partial, int64_t pieces,
+                                                             int64_t* out) {
+  const int64_t row = blockIdx.x;
+  float best = kNegInf;
+  int64_t best_i = INT64_MAX;
+  for (int64_t p = lane_id(); p < pieces; p += kWave) {
+    const ArgmaxPartial q = partial[row * pieces + p];
+    if (argmax_better(q.value, q.index, best, best_i)) {
+      best = q.value;
+      best_i = q.index;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v = __shfl_xor(best, off);
+    const int64_t i = __shfl_xor(best_i, off);
+    if (argmax_better(v, i, best, best_i)) {
+      best = v;
+      best_i = i;
+    }
+  }
+  if (lane_id() == 0) out[row] = best_i;
 }
 
 // ---------------------------------------------------------------------------
@@ -3304,12 +3351,45 @@ NIE_API int nie_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t
   if (rows > 0x7fffffffLL) return fail(NIE_EINVAL, "too many rows");
   if (dtype == NIE_DTYPE_BF16) {
     hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, dim3((unsigned)rows), dim3(kArgmaxThreads), 0,
-                       (hipStream_t)stream, logits, row_stride, cols, out);
+                       (hipStream_t)stream, logits, row_stride, cols, out, nullptr);
   } else {
     hipLaunchKernelGGL(argmax_rows_kernel<float>, dim3((unsigned)rows), dim3(kArgmaxThreads), 0,
-                       (hipStream_t)stream, logits, row_stride, cols, out);
+                       (hipStream_t)stream, logits, row_stride, cols, out, nullptr);
   }
   return launched("argmax_rows");
+}
+
+NIE_API int64_t nie_argmax_rows_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return rows * cdiv(cols, kArgmaxPieceCols) * (int64_t)sizeof(ArgmaxPartial);
+}
+
+NIE_API int nie_argmax_rows_split(int dtype, const void* logits, int64_t rows, int64_t cols, int64_t row_stride,
+                                  int64_t* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  if (rows < 0 || cols <= 0 || row_stride < cols) return fail(NIE_EINVAL, "bad logits shape");
+  if (rows == 0) return NIE_OK;
+  if (!logits || !out || !workspace) return fail(NIE_EINVAL, "null pointer argument");
+  const int64_t pieces = cdiv(cols, kArgmaxPieceCols);
+  if (rows > 0x7fffffffLL || pieces > 0xffffLL) return fail(NIE_EINVAL, "too many rows or columns");
+  if (workspace_bytes < nie_argmax_rows_workspace_bytes(rows, cols) || ((uintptr_t)workspace % 16) != 0) {
+    return fail(NIE_EINVAL, "argmax_rows_split: workspace too small or misaligned");
+  }
+  ArgmaxPartial* part = reinterpret_cast<ArgmaxPartial*>(workspace);
+  const dim3 grid((unsigned)rows, (unsigned)pieces);
+  if (dtype == NIE_DTYPE_BF16) {
+    hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, grid, dim3(kArgmaxThreads), 0, (hipStream_t)stream, logits,
+                       row_stride, cols, out, part);
+  } else {
+    hipLaunchKernelGGL(argmax_rows_kernel<float>, grid, dim3(kArgmaxThreads), 0, (hipStream_t)stream, logits,
+                       row_stride, cols, out, part);
+  }
+  rc = launched("argmax_rows");
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3((unsigned)rows), dim3(kWave), 0, (hipStream_t)stream, part, pieces,
+                     out);
+  return launched("argmax_merge");
 }
 
 NIE_API int nie_rms_norm(int dtype, const void* x, int64_t x_stride, const void* residual,

@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "nie_kv_copy_blocks",
     "nie_rope_kv_append",
     "nie_argmax_rows",
+    "nie_argmax_rows_workspace_bytes",
+    "nie_argmax_rows_split",
     "nie_rms_norm",
     "nie_silu_mul",
     "nie_linear_rows",
@@ -80,6 +82,8 @@ _SIGNATURES = {
         ],
     ),
     "nie_argmax_rows": (_i32, [_i32, _ptr, _i64, _i64, _i64, _ptr, _ptr]),
+    "nie_argmax_rows_workspace_bytes": (_i64, [_i64, _i64]),
+    "nie_argmax_rows_split": (_i32, [_i32, _ptr, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr]),
     "nie_rms_norm": (
         _i32,
         [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _f32, _ptr],
@@ -369,6 +373,9 @@ def rope_kv_append(
     _check(rc, "nie_rope_kv_append")
 
 
+ARGMAX_PIECE_COLS = 8192
+
+
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Index of the largest value of each row of a 2D logits tensor (torch.argmax(dim=-1) semantics), int64."""
     _require_gpu(logits)
@@ -379,9 +386,20 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     elif out.dtype != torch.int64 or out.shape != (rows,) or not out.is_contiguous() or out.device != logits.device:
         raise ValueError("out must be a contiguous int64 tensor with one entry per row")
-    rc = load_library().nie_argmax_rows(dtype_code(logits.dtype), logits.data_ptr(), rows, logits.shape[1],
-                                        logits.stride(0) if rows > 1 else logits.shape[1], out.data_ptr(),
-                                        _stream(logits.device))
+    cols = logits.shape[1]
+    stride = logits.stride(0) if rows > 1 else cols
+    lib = load_library()
+    if cols >= 2 * ARGMAX_PIECE_COLS:
+        # long rows (an LM head's logits): one workgroup per piece of a row,
+        # then a merge of the pieces' (value, index) pairs
+        ws_bytes = lib.nie_argmax_rows_workspace_bytes(rows, cols)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=logits.device)
+        rc = lib.nie_argmax_rows_split(dtype_code(logits.dtype), logits.data_ptr(), rows, cols, stride,
+                                       out.data_ptr(), ws.data_ptr(), ws_bytes, _stream(logits.device))
+        _check(rc, "nie_argmax_rows_split")
+        return out
+    rc = lib.nie_argmax_rows(dtype_code(logits.dtype), logits.data_ptr(), rows, cols, stride, out.data_ptr(),
+                             _stream(logits.device))
     _check(rc, "nie_argmax_rows")
     return out
 

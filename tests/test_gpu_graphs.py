@@ -49,7 +49,16 @@ def test_argmax_rows_matches_torch(dtype):
     aligned[1, 128255] = 100.0
     aligned[2, 64000] = float("nan")
     aligned[3] = 1.0
-    assert torch.equal(_native.argmax_rows(aligned), aligned.argmax(dim=-1))
+    aligned[6, 8191] = aligned[6, 8192] = 100.0  # a tie across two pieces of the split form
+    aligned[7, 128255] = float("inf")
+    assert torch.equal(_native.argmax_rows(aligned), aligned.argmax(dim=-1))  # split form (>= 2 pieces)
+    # the split form on rows that start off 16-byte alignment and a short last piece
+    wide2 = torch.randn((5, 8192 * 3 + 11), generator=gen, device=DEV).to(dtype)
+    odd = wide2[:, 1:]
+    odd[1, 8192 * 2 + 5] = 100.0
+    assert torch.equal(_native.argmax_rows(odd), odd.argmax(dim=-1))
+    short = torch.randn((3, 8192), generator=gen, device=DEV).to(dtype)  # one-workgroup form
+    assert torch.equal(_native.argmax_rows(short), short.argmax(dim=-1))
 
 
 def _graph_model(dtype):

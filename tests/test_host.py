@@ -475,6 +475,15 @@ def test_library_rejects_bad_decoder_and_fused_arguments():
     assert lib.nie_rms_norm_linear_rows(1, p, 2048, None, 0, None, 0, p + 2, 1e-5, 4, p, 64, 2048, 0, p, 64,
                                         None) == -1  # misaligned norm weight
     assert b"rms_norm_linear_rows" in lib.nie_last_error()
+    # nie_argmax_rows_split(dtype, logits, rows, cols, row_stride, out, ws, ws_bytes, stream)
+    need = lib.nie_argmax_rows_workspace_bytes(16, 128256)
+    assert need == 16 * 16 * 16  # 16 pieces of 8192 columns per row, 16 bytes per pair
+    assert lib.nie_argmax_rows_workspace_bytes(0, 100) == 0
+    assert lib.nie_argmax_rows_split(1, p, 16, 128256, 128256, p, p, need - 16, None) == -1  # workspace too small
+    assert lib.nie_argmax_rows_split(1, p, 16, 128256, 128256, p, p + 8, need, None) == -1  # misaligned
+    assert lib.nie_argmax_rows_split(1, p, 16, 128256, 100, p, p, need, None) == -1  # stride < cols
+    assert lib.nie_argmax_rows_split(1, p, 16, 128256, 128256, p, None, need, None) == -1  # no workspace
+    assert lib.nie_argmax_rows_split(1, p, 0, 128256, 128256, p, p, need, None) == 0  # no rows
     # nie_paged_decode_append with a batch but no new rows, or one RoPE table only
     args = dict(q=p, k_cache=p, v_cache=p, tables=p, lens=p, out=p)
     base = [1, args["q"], 32 * 64, 64]
