@@ -600,13 +600,13 @@ def _linear_inputs(rows, n, k, seed, x_cols=None):
 
 
 @pytest.mark.parametrize("rows", [1, 5, 16])
-@pytest.mark.parametrize("n,k", [(3072, 2048), (2048, 8192), (32768, 2048)])
+@pytest.mark.parametrize("n,k", [(3072, 2048), (2048, 8192), (1024, 4096), (32768, 2048)])
 def test_linear_rows_matches_float64_product(rows, n, k):
     """nie_linear_rows against x . W^T in float64 on the CPU, rounded to bf16:
     every output within half a bf16 ulp of the exact product (plus the fp32
     accumulation's error), at most 1% of outputs one ulp away from torch's own
-    bf16 GEMM on the GPU.  (32768, 2048) takes the two-tile launch; x is a
-    column slice of a wider tensor (row stride > k)."""
+    bf16 GEMM on the GPU.  k = 2048, 4096 and 8192 are the kernel's 2-, 4- and
+    8-pass builds; x is a column slice of a wider tensor (row stride > k)."""
     _log(f"linear_rows rows={rows} n={n} k={k}")
     x_full, w = _linear_inputs(rows, n, k, seed=rows * 7 + n, x_cols=k + 64)
     x = x_full[:, 32:32 + k]
