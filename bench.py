@@ -425,14 +425,21 @@ def run_e2e(args):
     # matmul / mask / softmax) under the same scheduler, on the first steps only
     k = args.e2e_ref_steps
     ours_k, _, ours_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
+    # the reference's algorithms end to end: its attention loop and torch's
+    # GEMM for every projection
+    import nano_infer_engine.layers.linear as linear_module
+
     saved = attention_module.attention_core
+    saved_native = linear_module.USE_NATIVE
     attention_module.attention_core = reference_ops.attention_core_like_product
+    linear_module.USE_NATIVE = False
     try:
         ref_k, _, ref_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
     finally:
         attention_module.attention_core = saved
+        linear_module.USE_NATIVE = saved_native
     same = all(torch.equal(a.sequence, b.sequence) for a, b in zip(ours_reqs, ref_reqs))
-    log(f"e2e first {k} steps: ours {ours_k * 1e3:.1f} ms, reference attention {ref_k * 1e3:.1f} ms "
+    log(f"e2e first {k} steps: ours {ours_k * 1e3:.1f} ms, reference algorithms {ref_k * 1e3:.1f} ms "
         f"({ref_k / ours_k:.1f}x); sequences identical: {same}")
     del model
     torch.cuda.empty_cache()
