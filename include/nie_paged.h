@@ -350,6 +350,41 @@ int nie_paged_decode_append(int dtype,
                             void* stream);
 
 /*
+ * nie_paged_decode_append without a workspace argument: the split partials
+ * go to a device array the library owns (nie_paged_decode_noalloc_max_bytes()
+ * bytes = 32 MiB per GPU, held from the device's first call until the
+ * process ends).  The call allocates nothing (no hipMalloc, no allocating
+ * library routine); the first call on a device looks the array's address up
+ * once.  Every other argument, and the result, is nie_paged_decode_append's.
+ * A call whose partials would exceed the array (nie_paged_decode_workspace_bytes
+ * of the same arguments above the maximum, for a call that splits) returns
+ * NIE_EINVAL with a message saying so.  All calls on one GPU share the
+ * array: calls that overlap in time on one GPU (different streams, or
+ * different threads) race.  Nothing in the array needs clearing between
+ * calls (each call writes every partial it reads).
+ * No counterpart in the reference: this entry point exists for callers that
+ * cannot allocate device memory — code under HIP graph capture, tight
+ * serving loops and harnesses that forbid hipMalloc.
+ */
+int64_t nie_paged_decode_noalloc_max_bytes(void);
+int nie_paged_decode_append_noalloc(int dtype,
+                                    const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                    const void* k_new, int64_t k_new_stride,
+                                    const void* v_new, int64_t v_new_stride,
+                                    const void* cos_table, const void* sin_table, int64_t table_rows,
+                                    void* k_cache, void* v_cache,
+                                    int64_t num_layers, int64_t layer_index,
+                                    int64_t num_blocks, int64_t block_size,
+                                    int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                    const int32_t* block_tables, int64_t table_stride,
+                                    const int32_t* seq_lens, int64_t batch,
+                                    int64_t max_seq_len, int64_t total_seq_len,
+                                    float scale,
+                                    void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                    const int32_t* host_seq_lens,
+                                    void* stream);
+
+/*
  * Workspace bytes needed by nie_varlen_prefill (host values: number of
  * sequences, total and maximum query length, maximum context+query length,
  * and the same optional host copies of cu_seqlens_q / context_lens as the

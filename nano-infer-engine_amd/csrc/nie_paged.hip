@@ -36,6 +36,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 
 #include "nie_paged.h"
@@ -3606,7 +3607,8 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
                       const int32_t* block_tables, int64_t table_stride, const int32_t* seq_lens, int64_t batch,
                       int64_t max_seq_len, int64_t total_seq_len, float scale, void* out, int64_t out_stride_b,
                       int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
-                      const int32_t* host_seq_lens, const DecodeAppend& append, void* stream) {
+                      const int32_t* host_seq_lens, const DecodeAppend& append, void* stream,
+                      bool static_scratch = false) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -3656,6 +3658,12 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   const bool may_split = cdiv(max_seq_len, kTileKeys) > tps;
   const int64_t need = items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
   if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
+    if (static_scratch) {
+      return fail(NIE_EINVAL,
+                  "split partials need %lld bytes, beyond the %lld-byte static scratch of the allocation-free "
+                  "entry point; call nie_paged_decode_append with a workspace instead",
+                  (long long)need, (long long)workspace_bytes);
+    }
     return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,
                 (long long)workspace_bytes);
   }
@@ -3745,6 +3753,92 @@ NIE_API int nie_paged_decode_append(int dtype, const void* q, int64_t q_stride_b
                            block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
                            max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, workspace,
                            workspace_bytes, host_seq_lens, append, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode step.  The split partials of
+// nie_paged_decode_append_noalloc live in `scratch`, a library-owned device
+// array (each GPU that loads the library holds its own copy, at its own
+// address, until the process ends).  In host code `scratch` names a host
+// stand-in, not device memory, so host code never passes it to a kernel:
+// the device address is looked up once per device with hipGetSymbolAddress
+// (with that device current) and kept in g_scratch_ptr.  The partials are
+// fully written by the decode kernel before the merge kernel reads them, so
+// the array needs no clearing between calls; calls that overlap in time on
+// one GPU share it and race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = 32ll << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (the current
+// device for the null stream).
+int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t err = hipStreamGetDevice((hipStream_t)stream, &dev);
+  if (err != hipSuccess) return fail(NIE_EINVAL, "hipStreamGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kScratchDevices) {
+    return fail(NIE_EUNSUPPORTED, "device %d is beyond the %d devices the static scratch tracks", dev,
+                kScratchDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    err = hipGetDevice(&cur);
+    if (err != hipSuccess) return fail(NIE_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(err));
+    if (cur != dev && (err = hipSetDevice(dev)) != hipSuccess) {
+      return fail(NIE_ELAUNCH, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(err));
+    }
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (err != hipSuccess || p == nullptr) {
+      return fail(NIE_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(err));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NIE_OK;
+}
+
+}  // namespace
+
+NIE_API int64_t nie_paged_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+NIE_API int nie_paged_decode_append_noalloc(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                            const void* k_new, int64_t k_new_stride, const void* v_new,
+                                            int64_t v_new_stride, const void* cos_table, const void* sin_table,
+                                            int64_t table_rows, void* k_cache, void* v_cache, int64_t num_layers,
+                                            int64_t layer_index, int64_t num_blocks, int64_t block_size,
+                                            int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                            const int32_t* block_tables, int64_t table_stride,
+                                            const int32_t* seq_lens, int64_t batch, int64_t max_seq_len,
+                                            int64_t total_seq_len, float scale, void* out, int64_t out_stride_b,
+                                            int64_t out_stride_h, const int32_t* host_seq_lens, void* stream) {
+  if (batch > 0 && (!k_new || !v_new)) return fail(NIE_EINVAL, "null pointer argument");
+  void* ws = nullptr;
+  if (batch > 0) {
+    const int rc = scratch_address(stream, &ws);
+    if (rc) return rc;
+  }
+  DecodeAppend append;
+  append.k_new = k_new;
+  append.k_stride = k_new_stride;
+  append.v_new = v_new;
+  append.v_stride = v_new_stride;
+  append.cos_table = cos_table;
+  append.sin_table = sin_table;
+  append.table_rows = table_rows;
+  return paged_decode_call(dtype, q, q_stride_b, q_stride_h, k_cache, v_cache, num_layers, layer_index, num_blocks,
+                           block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
+                           max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, ws, kScratchBytes,
+                           host_seq_lens, append, stream, /*static_scratch=*/true);
 }
 
 NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query_tokens,

@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
+    "nie_paged_decode_noalloc_max_bytes",
+    "nie_paged_decode_append_noalloc",
     "nie_varlen_prefill_workspace_bytes",
     "nie_varlen_prefill",
 )
@@ -124,6 +126,23 @@ _SIGNATURES = {
             _f32,                            # scale
             _ptr, _i64, _i64,                # out, strides
             _ptr, _i64,                      # workspace, bytes
+            _ptr, _ptr,                      # host seq_lens, stream
+        ],
+    ),
+    "nie_paged_decode_noalloc_max_bytes": (_i64, []),
+    "nie_paged_decode_append_noalloc": (
+        _i32,
+        [
+            _i32, _ptr, _i64, _i64,          # dtype, q, q strides
+            _ptr, _i64, _ptr, _i64,          # new K rows, stride, new V rows, stride
+            _ptr, _ptr, _i64,                # RoPE cos / sin tables, rows
+            _ptr, _ptr,                      # caches
+            _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
+            _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
+            _ptr, _i64,                      # block tables, stride
+            _ptr, _i64, _i64, _i64,          # seq_lens, batch, max, total
+            _f32,                            # scale
+            _ptr, _i64, _i64,                # out, strides
             _ptr, _ptr,                      # host seq_lens, stream
         ],
     ),
