@@ -36,6 +36,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -1956,7 +1957,30 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
 // r * (kDecodeFixedTiles + tiles per split), where tiles per split is the
 // smallest that fits the call into r rounds, within [4, 128] (128 = the
 // per-split block-table window, two VGPRs per lane).
-constexpr int64_t kDecodeCUs = 256;  // MI355X
+constexpr int64_t kDefaultCUs = 256;  // MI355X, when the device cannot be queried
+
+// Compute units of the current device (hipDeviceAttributeMultiprocessorCount),
+// queried once per device; kDefaultCUs when there is no device to ask (the
+// workspace queries also run on hosts without a GPU).
+int64_t device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cached[kMaxDev] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return kDefaultCUs;
+  }
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = (int)kDefaultCUs;
+    }
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 constexpr int64_t kDecodeMinTilesPerSplit = 4;
 constexpr int64_t kDecodeMaxTilesPerSplit = kTableWindow;
 constexpr int64_t kDecodeFixedTiles = 4;
@@ -2755,7 +2779,7 @@ struct PrefillPlan {
 // Workgroups a prefill call aims for with host metadata: the split length is
 // chosen so the items fill the GPU about once (two workgroups fit a CU at
 // head_dim 64; 1.5 per CU measured fastest on the mixed chunked-prefill step).
-constexpr int64_t kPrefillSlots = 3 * kDecodeCUs / 2;
+inline int64_t prefill_slots() { return 3 * device_cus() / 2; }
 
 // Key tiles visible to query tile qt of a request with n query tokens after
 // ctx cached ones (host side of prefill_key_tiles).
@@ -2793,7 +2817,7 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
         max_kt = kt > max_kt ? kt : max_kt;
       }
     }
-    p.tps = clamp_tps(cdiv(work * kv_heads, kPrefillSlots));
+    p.tps = clamp_tps(cdiv(work * kv_heads, prefill_slots()));
     int64_t items = 0;
     for (int64_t r = 0; r < num_seqs; ++r) {
       const int64_t n = host_cu[r + 1] - host_cu[r];
@@ -3027,7 +3051,8 @@ DecodePlan plan_decode_t(int64_t kv_heads, bool uniform, int64_t batch, int64_t 
   p.heads = decode_heads<T, D>(kv_heads);
   p.resident = uniform ? decode_resident_u<T, D, true>(p.heads) : decode_resident_u<T, D, false>(p.heads);
   const int64_t groups = kv_heads / p.heads;
-  const int64_t slots = (kDecodeCUs * p.resident) / groups > 0 ? (kDecodeCUs * p.resident) / groups : 1;
+  const int64_t cus = device_cus();
+  const int64_t slots = (cus * p.resident) / groups > 0 ? (cus * p.resident) / groups : 1;
   const int64_t tiles = cdiv(total_seq_len, kTileKeys) + batch;  // >= sum_b ceil(len_b / 16)
   p.tps = kDecodeMaxTilesPerSplit;
   int64_t best = -1;
@@ -3062,7 +3087,8 @@ int64_t decode_items_exact(const int32_t* lens, int64_t batch, int64_t tps) {
 // r * (kDecodeFixedTiles + tiles per split), as in plan_decode_t.
 DecodePlan plan_decode_exact(DecodePlan p, int64_t kv_heads, const int32_t* lens, int64_t batch) {
   const int64_t groups = kv_heads / p.heads;
-  const int64_t slots = (kDecodeCUs * p.resident) / groups > 0 ? (kDecodeCUs * p.resident) / groups : 1;
+  const int64_t cus = device_cus();
+  const int64_t slots = (cus * p.resident) / groups > 0 ? (cus * p.resident) / groups : 1;
   int64_t best = -1;
   for (int64_t r = 1; r <= kDecodeMaxRounds; ++r) {
     if (decode_items_exact(lens, batch, kDecodeMaxTilesPerSplit) > r * slots) continue;
@@ -3478,7 +3504,8 @@ template <bool kNorm>
 int launch_linear(const LinearArgs& a, int epilogue, hipStream_t s) {
   // one workgroup per CU (the ring takes 128 KiB of LDS), at most one per tile
   const int64_t tiles = a.n / 16;
-  const dim3 grid((unsigned)(tiles < kDecodeCUs ? tiles : kDecodeCUs)), block(kLinearWaves * kWave);
+  const int64_t cus = device_cus();
+  const dim3 grid((unsigned)(tiles < cus ? tiles : cus)), block(kLinearWaves * kWave);
   const bool silu = epilogue == NIE_LINEAR_SILU_MUL;
   if constexpr (kNorm) {
     if (a.res != nullptr) {

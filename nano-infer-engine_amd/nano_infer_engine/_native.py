@@ -504,22 +504,31 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 
 
 LINEAR_MAX_ROWS = 16
-LINEAR_K_MULTIPLE = 2048
+#: In-feature sizes nie_linear_rows is built for; the SiLU epilogue only for the first two.
+LINEAR_K_BUILT = (2048, 4096, 8192)
+LINEAR_K_BUILT_SILU = (2048, 4096)
 LINEAR_PLAIN = 0
 LINEAR_SILU_MUL = 1
 
 
-def linear_rows_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
-    """Whether nie_linear_rows takes ``F.linear(x, weight)``: bf16 on the GPU,
-    at most 16 rows, in-features a multiple of 2048, out-features of 16."""
+def linear_rows_supported(x: torch.Tensor, weight: torch.Tensor, silu_mul: bool = False) -> bool:
+    """Whether nie_linear_rows takes ``F.linear(x, weight)`` (with the SwiGLU
+    epilogue when ``silu_mul``): bf16 on the GPU, at most 16 rows, an
+    in-feature size the library is built for, out-features a multiple of 16."""
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or weight.ndim != 2 or x.ndim == 0:
         return False
     if not x.is_cuda or weight.device != x.device:
         return False
     n, k = weight.shape
-    rows = x.numel() // max(x.shape[-1], 1)
-    return (x.shape[-1] == k and 0 < rows <= LINEAR_MAX_ROWS and k % LINEAR_K_MULTIPLE == 0 and n % 16 == 0
-            and n > 0)
+    return x.shape[-1] == k and linear_rows_shape_built(x.numel() // max(k, 1), n, k, silu_mul)
+
+
+def linear_rows_shape_built(rows: int, n: int, k: int, silu_mul: bool = False) -> bool:
+    """The shapes nie_linear_rows is built for (its NIE_EUNSUPPORTED check on
+    the host): 1..16 rows, n a positive multiple of 16 (of 32 for a
+    ``[gate; up]`` weight), k in 2048 / 4096, or 8192 without the SiLU epilogue."""
+    built = LINEAR_K_BUILT_SILU if silu_mul else LINEAR_K_BUILT
+    return 0 < rows <= LINEAR_MAX_ROWS and k in built and n > 0 and n % (32 if silu_mul else 16) == 0
 
 
 def linear_rows(x: torch.Tensor, weight: torch.Tensor, silu_mul: bool = False) -> torch.Tensor:
@@ -529,12 +538,10 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, silu_mul: bool = False) -
     result is ``silu(gate) * up`` (``layers/mlp.py:18-22``), half as wide.
     """
     _require_gpu(x, weight)
-    if not linear_rows_supported(x, weight):
+    if not linear_rows_supported(x, weight, silu_mul):
         raise RuntimeError(f"nie_linear_rows does not take x {tuple(x.shape)} {x.dtype} with weight "
-                           f"{tuple(weight.shape)} {weight.dtype}")
+                           f"{tuple(weight.shape)} {weight.dtype}" + (" and the SiLU epilogue" if silu_mul else ""))
     n, k = weight.shape
-    if silu_mul and n % 32 != 0:
-        raise RuntimeError("a [gate; up] weight needs a multiple of 32 rows")
     n_out = n // 2 if silu_mul else n
     xs = _aligned(_norm_rows(x, k))
     w = _aligned(weight.detach() if weight.is_contiguous() else weight.detach().contiguous())
@@ -567,7 +574,7 @@ def rms_norm_linear_rows(
     arithmetic is ``rms_norm``'s (``layers/rms_norm.py:25-31``).
     """
     _require_gpu(x, weight, norm_weight)
-    if not linear_rows_supported(x, weight) or weight.shape[1] != RMS_NORM_LINEAR_K:
+    if not linear_rows_supported(x, weight, silu_mul) or weight.shape[1] != RMS_NORM_LINEAR_K:
         raise RuntimeError(f"nie_rms_norm_linear_rows does not take x {tuple(x.shape)} {x.dtype} with weight "
                            f"{tuple(weight.shape)} {weight.dtype}")
     n, k = weight.shape
@@ -576,8 +583,6 @@ def rms_norm_linear_rows(
     if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
                                  or residual.device != x.device):
         raise ValueError("residual must match x")
-    if silu_mul and n % 32 != 0:
-        raise RuntimeError("a [gate; up] weight needs a multiple of 32 rows")
     n_out = n // 2 if silu_mul else n
     xs = _aligned(_norm_rows(x, k))
     rows = xs.shape[0]
@@ -636,19 +641,26 @@ def kv_copy_blocks(
     A side whose block list is ``None`` is a packed staging tensor of shape
     (L, count, BS, Hkv, D); otherwise it is a pool indexed by the list.
     """
-    _require_gpu(src_k, src_v, dst_k, dst_v)
     for t in (src_k, src_v, dst_k, dst_v):
         if t.ndim != 5 or not t.is_contiguous():
             raise ValueError("block copies need contiguous 5D K/V tensors")
+    # the kernel indexes V with K's geometry, and a packed side with `count`
+    # as its per-layer block count
+    if src_v.shape != src_k.shape or dst_v.shape != dst_k.shape:
+        raise ValueError("V tensors must have the shape of their K tensors")
     if src_k.shape[0] != dst_k.shape[0] or src_k.shape[2:] != dst_k.shape[2:]:
         raise ValueError("source and destination layouts differ")
-    if src_k.dtype != dst_k.dtype:
+    if src_k.dtype != dst_k.dtype or src_v.dtype != src_k.dtype or dst_v.dtype != dst_k.dtype:
         raise ValueError("source and destination dtypes differ")
-    for blocks in (src_blocks, dst_blocks):
-        if blocks is not None:
-            _require_gpu(blocks)
-            if blocks.dtype != torch.int32 or blocks.ndim != 1 or blocks.shape[0] < count:
-                raise ValueError("block lists must be 1D int32 tensors with `count` entries")
+    if count < 0:
+        raise ValueError("count must be non-negative")
+    for side, blocks, pool in (("source", src_blocks, src_k), ("destination", dst_blocks, dst_k)):
+        if blocks is None:
+            if pool.shape[1] != count:
+                raise ValueError(f"a packed {side} must hold exactly `count` blocks per layer")
+        elif blocks.dtype != torch.int32 or blocks.ndim != 1 or blocks.shape[0] < count:
+            raise ValueError("block lists must be 1D int32 tensors with `count` entries")
+    _require_gpu(src_k, src_v, dst_k, dst_v, *(b for b in (src_blocks, dst_blocks) if b is not None))
     num_layers, _, block_size, kv_heads, head_dim = src_k.shape
     rc = load_library().nie_kv_copy_blocks(
         dtype_code(src_k.dtype),

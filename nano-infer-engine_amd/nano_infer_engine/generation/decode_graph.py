@@ -24,6 +24,7 @@ sequences past ``max_graph_len`` run eagerly.
 
 from __future__ import annotations
 
+from collections import OrderedDict
 from dataclasses import dataclass
 
 import numpy as np
@@ -52,19 +53,32 @@ class _CapturedStep:
 class DecodeGraphRunner:
     """Captures and replays the decode step of ``model`` over ``cache``."""
 
-    def __init__(self, model, cache: PagedKVCache, max_batch_size: int, max_graph_len: int = 32768):
+    def __init__(self, model, cache: PagedKVCache, max_batch_size: int, max_graph_len: int = 32768,
+                 max_graphs: int = 64):
         if cache.keys.device.type != "cuda":
             raise RuntimeError("decode graphs need the cache on a ROCm GPU")
+        if max_graphs < 1:
+            raise ValueError("max_graphs must be positive")
         self.model = model
         self.cache = cache
         self.max_batch_size = max_batch_size
         self.max_graph_len = max_graph_len
+        self.max_graphs = max_graphs
         self.device = cache.keys.device
         # captures run on a side stream of default priority
         self._stream = torch.cuda.Stream(self.device)
-        self._steps: dict[tuple[int, int], _CapturedStep] = {}
+        # Every capture allocates from one shared memory pool: the steps never
+        # run concurrently (one stream), so their activations can share
+        # memory, and each step's outputs (logits, next IDs) stay referenced by
+        # its _CapturedStep, so no other capture is handed them.  A KV pool
+        # sized to most of HBM then leaves room for one set of activations
+        # plus a B x vocab logits buffer per graph, not a private pool each.
+        self._pool = torch.cuda.graph_pool_handle()
+        # least recently replayed first; at most max_graphs are kept
+        self._steps: OrderedDict[tuple[int, int], _CapturedStep] = OrderedDict()
         self.captures = 0
         self.replays = 0
+        self.evictions = 0
 
     def supports(self, batch_size: int, max_seq_len: int) -> bool:
         return 0 < batch_size <= self.max_batch_size and decode_plan_bound(max_seq_len) <= self.max_graph_len
@@ -109,7 +123,7 @@ class DecodeGraphRunner:
             _native.argmax_rows(logits, out=next_ids)
             stream.synchronize()
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
+            with torch.cuda.graph(graph, stream=stream, pool=self._pool):
                 logits = model.run_tokens(ids, cache, batch)
                 _native.argmax_rows(logits, out=next_ids)
         torch.cuda.current_stream(self.device).wait_stream(stream)
@@ -152,8 +166,17 @@ class DecodeGraphRunner:
         key = (b, bound)
         step = self._steps.get(key)
         if step is None:
+            if len(self._steps) >= self.max_graphs:
+                # drop the least recently replayed capture (its logits stay
+                # alive while a request still holds a view of them)
+                _, old = self._steps.popitem(last=False)
+                old.copied.synchronize()
+                del old
+                self.evictions += 1
             step = self._capture(b, bound)
             self._steps[key] = step
+        else:
+            self._steps.move_to_end(key)
 
         # host metadata into the pinned staging buffers (once the previous
         # step's copies out of them have run), then one copy each

@@ -27,8 +27,8 @@ USE_NATIVE = True
 _FULL_GRID_TILES = 256
 
 
-def _native_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
-    if not USE_NATIVE or not _native.linear_rows_supported(x, weight):
+def _native_ok(x: torch.Tensor, weight: torch.Tensor, silu_mul: bool = False) -> bool:
+    if not USE_NATIVE or not _native.linear_rows_supported(x, weight, silu_mul):
         return False
     n, k = weight.shape
     if k > 4096 and n // 16 < _FULL_GRID_TILES:
@@ -53,7 +53,7 @@ def apply(module: nn.Linear, x: torch.Tensor) -> torch.Tensor:
 def silu_mul_linear(x: torch.Tensor, gate_up_weight: torch.Tensor, inner: int) -> torch.Tensor | None:
     """``silu(x . Wg^T) * (x . Wu^T)`` from the stacked ``[gate; up]`` weight in one
     launch, or None when the HIP path does not take the shapes."""
-    if gate_up_weight.shape[0] != 2 * inner or not _native_ok(x, gate_up_weight) or inner % 16:
+    if gate_up_weight.shape[0] != 2 * inner or not _native_ok(x, gate_up_weight, silu_mul=True) or inner % 16:
         return None
     return _native.linear_rows(x, gate_up_weight, silu_mul=True)
 
@@ -76,7 +76,8 @@ def rms_norm_linear(x: torch.Tensor, residual: torch.Tensor | None, norm: nn.Mod
     nw = getattr(norm, "weight", None)
     if nw is None or nw.shape != (x.shape[-1],) or nw.dtype != x.dtype or nw.device != x.device:
         return None
-    if weight.ndim != 2 or weight.shape[1] != _native.RMS_NORM_LINEAR_K or not _native_ok(x, weight):
+    if (weight.ndim != 2 or weight.shape[1] != _native.RMS_NORM_LINEAR_K
+            or not _native_ok(x, weight, silu_mul=silu_mul)):
         return None
     if torch.is_grad_enabled() and nw.requires_grad:
         return None

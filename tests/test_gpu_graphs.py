@@ -73,9 +73,11 @@ def _cache(model, num_blocks=256):
     return PagedKVCache(num_blocks, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim, model.embed.weight.dtype, DEV)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_decode_graph_replays_match_eager_step(dtype):
-    _log(f"decode graph vs eager {dtype}")
+@pytest.mark.parametrize("dtype,max_graphs", [(torch.float32, 64), (torch.bfloat16, 64), (torch.bfloat16, 1)])
+def test_decode_graph_replays_match_eager_step(dtype, max_graphs):
+    """Replays equal eager steps; captures share one memory pool, and with
+    max_graphs=1 every new (batch, bucket) key evicts the previous capture."""
+    _log(f"decode graph vs eager {dtype} max_graphs={max_graphs}")
     model = _graph_model(dtype)
     gen = torch.Generator(device=DEV).manual_seed(1)
     # the first prompt crosses the 512-token plan bucket during the decode steps
@@ -85,7 +87,7 @@ def test_decode_graph_replays_match_eager_step(dtype):
     with torch.inference_mode():
         first = paged_prefill(model, tuple(prompts), graph_cache, ids)
         assert torch.equal(first, paged_prefill(model, tuple(prompts), eager_cache, ids))
-    runner = DecodeGraphRunner(model, graph_cache, max_batch_size=4)
+    runner = DecodeGraphRunner(model, graph_cache, max_batch_size=4, max_graphs=max_graphs)
     tokens = first.argmax(dim=-1)
     active = list(ids)
     for step in range(24):
@@ -110,7 +112,8 @@ def test_decode_graph_replays_match_eager_step(dtype):
             assert torch.equal(gk, ek) and torch.equal(gv, ev)
     assert graph_cache.get_sequence_length("a") > 512  # the bucket was crossed
     assert runner.captures == 3 and runner.replays == 24
-    _log(f"  captures={runner.captures} replays={runner.replays}")
+    assert runner.evictions == (0 if max_graphs >= 3 else 2)
+    _log(f"  captures={runner.captures} replays={runner.replays} evictions={runner.evictions}")
 
 
 def test_scheduler_tokens_identical_with_decode_graphs():

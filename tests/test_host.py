@@ -356,6 +356,43 @@ def test_linear_rows_support_checks():
         _native.linear_rows(x, w)
 
 
+def test_kv_copy_blocks_validates_shapes_before_touching_the_device():
+    """The block-copy kernel indexes V with K's geometry and a packed side
+    with `count` blocks per layer, so mismatched tensors are refused on the
+    host (ValueError) before any device check or launch."""
+    pool = torch.zeros((2, 10, 4, 2, 8))
+    staged = torch.zeros((2, 3, 4, 2, 8))
+    blocks = torch.tensor([1, 5, 7], dtype=torch.int32)
+    with pytest.raises(ValueError, match="shape of their K"):
+        _native.kv_copy_blocks(pool, torch.zeros((2, 9, 4, 2, 8)), blocks, staged, staged.clone(), None, 3)
+    with pytest.raises(ValueError, match="shape of their K"):
+        _native.kv_copy_blocks(pool, pool.clone(), blocks, staged, torch.zeros((2, 4, 4, 2, 8)), None, 3)
+    with pytest.raises(ValueError, match="packed destination"):
+        _native.kv_copy_blocks(pool, pool.clone(), blocks, staged, staged.clone(), None, 2)
+    with pytest.raises(ValueError, match="packed source"):
+        _native.kv_copy_blocks(staged, staged.clone(), None, pool, pool.clone(), blocks, 2)
+    with pytest.raises(ValueError, match="`count` entries"):
+        _native.kv_copy_blocks(pool, pool.clone(), blocks[:2], staged, staged.clone(), None, 3)
+    # consistent shapes pass validation and stop at the device check
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        _native.kv_copy_blocks(pool, pool.clone(), blocks, staged, staged.clone(), None, 3)
+
+
+@pytest.mark.parametrize(
+    "rows,n,k,silu,built",
+    [(16, 3072, 2048, False, True), (1, 16384, 2048, True, True), (16, 2048, 8192, False, True),
+     (16, 8192, 4096, True, True),
+     # in-feature sizes the library has no instantiation for stay with torch's GEMM
+     (16, 4096, 14336, False, False), (16, 2048, 6144, False, False), (16, 16384, 8192, True, False),
+     (17, 3072, 2048, False, False), (16, 3080, 2048, False, False), (16, 48, 2048, True, False)],
+)
+def test_linear_rows_predicate_matches_the_built_kernels(rows, n, k, silu, built):
+    """The host predicate admits exactly the shapes the C entry point accepts
+    (its check_linear: k 2048 / 4096, or 8192 without the SwiGLU epilogue), so
+    every other projection falls back to torch's GEMM instead of raising."""
+    assert _native.linear_rows_shape_built(rows, n, k, silu) is built
+
+
 def test_rope_table_validation():
     """RoPE tables for the fused decode: (rows, head_dim / 2), the query dtype,
     contiguous, the same shape; None means no rotation."""
