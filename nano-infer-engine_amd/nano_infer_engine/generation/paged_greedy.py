@@ -1,4 +1,12 @@
-"""Synchronous greedy generation through the scheduler (``generation/paged_greedy.py:11-91`` of the reference)."""
+"""Synchronous greedy generation of a fixed prompt list through the scheduler.
+
+Observable behaviour follows ``generation/paged_greedy.py:11-91`` of the
+reference engine: inputs and capacity are checked before anything is
+prefilled (every request must fit the cache on its own; without a batch
+limit all of them must fit together), the prompts run FIFO through a
+:class:`ContinuousBatchingScheduler` to completion, and the first failed
+request's error is raised.
+"""
 
 from __future__ import annotations
 
@@ -7,7 +15,7 @@ import torch
 from nano_infer_engine.generation.config import GenerationConfig, RaggedGenerationOutput
 from nano_infer_engine.generation.paged_prefill import _validate_paged_prefill_inputs
 from nano_infer_engine.generation.request import RequestStatus
-from nano_infer_engine.generation.scheduler import ContinuousBatchingScheduler
+from nano_infer_engine.generation.scheduler import ContinuousBatchingScheduler, reserved_block_count
 from nano_infer_engine.paged_cache import PagedKVCache
 
 
@@ -21,35 +29,33 @@ def paged_greedy_generate(
     *,
     max_batch_size: int | None = None,
 ) -> RaggedGenerationOutput:
-    """Run a FIFO queue of prompts to completion over a shared paged cache."""
+    """Greedy-decode every prompt over a shared paged cache; sequences in input order."""
     if not config.use_cache:
         raise ValueError("paged greedy generation requires config.use_cache=True")
-    if max_batch_size is not None and (
-        isinstance(max_batch_size, bool) or not isinstance(max_batch_size, int) or max_batch_size <= 0
-    ):
+    batch_limited = max_batch_size is not None
+    if batch_limited and (isinstance(max_batch_size, bool) or not isinstance(max_batch_size, int)
+                          or max_batch_size <= 0):
         raise ValueError("max_batch_size must be a positive integer")
     _validate_paged_prefill_inputs(prompts, paged_cache, sequence_ids)
-    budget = paged_cache.allocator.free_block_count
-    needed = []
-    for prompt, sequence_id in zip(prompts, sequence_ids):
-        blocks = (prompt.shape[1] + config.max_new_tokens - 1 + paged_cache.block_size - 1) // paged_cache.block_size
-        if blocks > budget:
-            raise ValueError(f"request cannot fit in paged cache: {sequence_id}")
-        needed.append(blocks)
-    if max_batch_size is None and sum(needed) > budget:
+    free = paged_cache.allocator.free_block_count
+    needs = {s: reserved_block_count(p.shape[1], config.max_new_tokens, paged_cache.block_size)
+             for p, s in zip(prompts, sequence_ids)}
+    too_big = next((s for s, n in needs.items() if n > free), None)
+    if too_big is not None:
+        raise ValueError(f"request cannot fit in paged cache: {too_big}")
+    if not batch_limited and sum(needs.values()) > free:
         raise ValueError("not enough free blocks for paged generation")
-    scheduler = ContinuousBatchingScheduler(
-        model,
-        config,
-        paged_cache,
-        max_batch_size or len(prompts),
-        release_on_token_limit=max_batch_size is not None,
-    )
+
+    # without a batch limit every request decodes at once and keeps its blocks
+    # until the end; with one, a request's blocks are freed at its token limit
+    # so the queue behind it can be admitted
+    scheduler = ContinuousBatchingScheduler(model, config, paged_cache, max_batch_size or len(prompts),
+                                            release_on_token_limit=batch_limited)
     requests = [scheduler.add_request(s, p) for p, s in zip(prompts, sequence_ids)]
     scheduler.run_until_idle()
-    failed = next((r for r in requests if r.status is RequestStatus.FAILED), None)
-    if failed is not None:
-        raise RuntimeError(f"paged prefill failed: {failed.sequence_id}") from failed.error
+    for request in requests:
+        if request.status is RequestStatus.FAILED:
+            raise RuntimeError(f"paged prefill failed: {request.sequence_id}") from request.error
     device = prompts[0].device
     return RaggedGenerationOutput(
         sequences=tuple(r.sequence for r in requests),

@@ -293,6 +293,11 @@ def test_prefill_chunks_then_decode_in_one_ragged_forward():
     assert model.ragged_calls == [(("request-b", "request-a"), (0, 2, 3))]
     assert out.token_events[0].sequence_id == "request-a"
     assert b.status is RequestStatus.ACTIVE
+    # the step's plan, as the scheduler exposes it: prompt piece first, then
+    # the decode row with the token just sampled
+    plan = s.last_plan
+    assert plan.sequence_ids == ("request-b", "request-a") and plan.query_lens == (2, 1)
+    assert plan.input_ids().tolist() == [4, 5, 9]
 
 
 def test_paged_prefill_chunks_returns_last_token_rows():
