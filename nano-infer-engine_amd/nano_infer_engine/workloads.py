@@ -151,6 +151,52 @@ def decode_long(num_layers: int = 1, seed: int = 4, num_blocks: int | None = Non
 
 
 # ---------------------------------------------------------------------------
+# End-to-end serving: the Llama-3.2-1B-shaped model and its request mix
+# ---------------------------------------------------------------------------
+SERVING_REQUESTS = 64
+SERVING_NEW_TOKENS = 256
+SERVING_MAX_BATCH = 16
+SERVING_CHUNK = 128
+SERVING_STEP_BUDGET = 512
+
+
+def serving_model(device, seed: int = 3):
+    """Llama-3.2-1B shape (``LlamaConfig`` defaults: hidden 2048, 16 layers,
+    32 / 8 heads, MLP 8192, vocab 128256, tied embeddings), bf16, every
+    Linear / Embedding weight N(0, 0.02), norm weights 1."""
+    from torch import nn
+
+    from nano_infer_engine.models.llama import Llama3_2, LlamaConfig
+
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = Llama3_2(LlamaConfig())
+    model = model.to(torch.bfloat16).eval()
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding)):
+                m.weight.normal_(0.0, 0.02)
+    return model
+
+
+def serving_prompts(device, vocab: int, count: int = SERVING_REQUESTS, seed: int = 3,
+                    lengths: tuple[int, int] = (128, 2048)) -> list[torch.Tensor]:
+    """``count`` prompts of token IDs uniform over the vocabulary, lengths
+    uniform in ``lengths`` (inclusive), each (1, n) int64."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lengths[0], lengths[1] + 1, size=count)
+    return [torch.from_numpy(rng.integers(0, vocab, size=(1, int(n)))).to(device) for n in lens]
+
+
+def serving_cache_blocks(prompts, max_new_tokens: int, max_batch: int = SERVING_MAX_BATCH,
+                         block_size: int = BLOCK_SIZE) -> int:
+    """Pool blocks for a serving run: max_batch requests of the longest
+    prompt at full length, plus 64 spare."""
+    per_request = -(-(max(p.shape[1] for p in prompts) + max_new_tokens) // block_size)
+    return max_batch * per_request + 64
+
+
+# ---------------------------------------------------------------------------
 # Algorithmic traffic / work (what roofline fractions are computed from)
 # ---------------------------------------------------------------------------
 def decode_bytes(seq_lens, q_heads=Q_HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM, block_size=BLOCK_SIZE, elt=2) -> int:

@@ -105,10 +105,12 @@ def ragged_attention_reference(
         write_tokens(keys, values, layer_index, table, block_size, ctx, k[start:end], v[start:end])
         total = ctx + n
         ks, vs = gather_tokens(keys, values, layer_index, table, block_size, total)
+        # right operands of the batched products made contiguous: on ROCm a
+        # bf16 bmm over a transposed view has faulted the GPU
         ks = ks.repeat_interleave(group, dim=1).transpose(0, 1)
-        vs = vs.repeat_interleave(group, dim=1).transpose(0, 1)
+        vs = vs.repeat_interleave(group, dim=1).transpose(0, 1).contiguous()
         query = q[start:end].transpose(0, 1)
-        scores = query @ ks.transpose(-1, -2) * scale
+        scores = query @ ks.transpose(-1, -2).contiguous() * scale
         q_pos = torch.arange(ctx, total, device=q.device)[:, None]
         k_pos = torch.arange(total, device=q.device)[None, :]
         scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
