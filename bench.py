@@ -1,20 +1,25 @@
-"""Benchmark of the paged-attention decode path on one MI355X.
+"""Benchmark of the ragged paged-attention path on one MI355X.
 
-Workload (one "step"): a continuous-batching decode step of the Llama-3.2-1B
-attention geometry — 16 ragged sequences with lognormal context lengths
-(median 2048, sigma 1, clipped to [32, 29600], seed 1), 32 query / 8 KV
-heads, head_dim 64, block_size 16, bf16, block tables drawn from a seeded
+Workload of ``value`` (one "step"): a continuous-batching decode step of the
+Llama-3.2-1B attention geometry — 16 ragged sequences with lognormal context
+lengths (median 2048, sigma 1, clipped to [32, 29600], seed 1), 32 query / 8
+KV heads, head_dim 64, block_size 16, bf16, block tables drawn from a seeded
 permutation of a pool twice the size needed.  For each of the 16 layers the
-step appends one new K/V token per sequence through ``slot_mapping`` and runs
-paged decode attention over the grown sequences.  16 layers give a 1.4 GB
-working set, far beyond the 256 MB last-level cache, so every step reads
-its KV from HBM.
+step appends one new K/V token per sequence and runs paged decode attention
+over the grown sequences (one fused launch per layer).  16 layers give a
+1.4 GB working set, far beyond the 256 MB last-level cache, so every step
+reads its KV from HBM.
 
 Prints one JSON line.  ``value`` = algorithmic bytes (decode K/V/Q/O/table
 reads + append traffic) per second over the timed steps.  ``roofline`` is
-for the decode-attention op, timed per launch with HIP events on its
-stream.  ``cpu_baseline`` times the oracle's restatement of the reference
-PyTorch algorithm on the host cores over a bounded sample.
+for the decode-attention call, timed per launch with HIP events on its
+stream.  Further fields: the same step planned as the serving path plans it
+(``serving_plan_decode``), the 4-sequence decode call (``decode_small``),
+the 16 x 29600 stress step on a pool of ~90% of free HBM, attention only and
+through the whole model (``stress_16x29600``), the mixed chunked-prefill
+step (``mixed_prefill_step``), end-to-end serving of the Llama-3.2-1B-shaped
+model (``e2e_llama1b_serving``) and the reference algorithm's own times on
+the GPU and on the host cores (``reference_path``, ``cpu_baseline``).
 """
 
 from __future__ import annotations
@@ -31,6 +36,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_PROFILE = os.path.join("profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json")
 
 
 def parse_args():
@@ -39,21 +45,23 @@ def parse_args():
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--layers", type=int, default=16)
-    p.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
     p.add_argument("--unfused-append", action="store_true",
                    help="decode step as nie_kv_append then nie_paged_decode (two launches per layer)")
-    p.add_argument("--skip-stress", action="store_true", help="do not run the 16x29600 decode figure")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
-    p.add_argument("--skip-mixed", action="store_true", help="do not run the mixed chunked-prefill figure")
-    p.add_argument("--skip-e2e", action="store_true", help="do not run the end-to-end serving figure")
-    p.add_argument("--e2e-only", action="store_true", help="run only the end-to-end serving figure")
-    p.add_argument("--e2e-ref-steps", type=int, default=3,
-                   help="scheduler steps timed with the reference attention algorithm")
-    p.add_argument("--mixed-only", action="store_true", help="run only the mixed chunked-prefill figure")
-    p.add_argument("--linear-only", action="store_true",
-                   help="run only the decode-step projection GEMM figure (nie_linear_rows vs torch's GEMM)")
-    p.add_argument("--stress-only", action="store_true",
-                   help="run only the 16x29600 decode figure (for per-workload profiles)")
+    p.add_argument("--only", choices=["decode", "small", "stress", "mixed", "e2e", "linear", "reference"],
+                   help="run one leg and print its JSON only")
+    p.add_argument("--skip", action="append", default=[],
+                   choices=["small", "stress", "stress-model", "mixed", "e2e", "reference", "cpu", "lockstep"],
+                   help="leave a leg out of the default line (repeatable)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU baseline sample")
+    p.add_argument("--pool-fraction", type=float, default=0.9,
+                   help="stress step: KV pool as a fraction of the free device memory")
+    p.add_argument("--stress-steps", type=int, default=256, help="stress step: decode steps (one append each)")
+    p.add_argument("--lockstep-requests", type=int, default=16,
+                   help="serving requests replayed on the reference algorithm (bf16 and fp32)")
+    p.add_argument("--lockstep-variant", action="store_true",
+                   help="also replay on the bf16 variant with fp32 attention products")
+    p.add_argument("--native-gemm", choices=["on", "off"], default="on",
+                   help="serving legs: decode-step projections on nie_linear_rows (on) or torch's GEMM (off)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 4 device-to-device copies of MIB MiB (reference for HBM byte counters)")
     return p.parse_args()
@@ -63,20 +71,34 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-class DecodeBench:
-    """Device state for repeated append+decode steps over one workload."""
+def _median_us(pairs) -> float:
+    import numpy as np
 
-    def __init__(self, wl, steps_total: int, device, seed: int):
+    return float(np.median([a.elapsed_time(b) for a, b in pairs])) * 1e3
+
+
+# ---------------------------------------------------------------------------
+# decode steps over a synthetic pool
+# ---------------------------------------------------------------------------
+class DecodeBench:
+    """Device state for repeated append + decode steps over one workload.
+
+    ``pool_blocks``: pool size (default: twice the blocks the steps need); the
+    tables are a seeded permutation of the whole pool.  Only the blocks the
+    tables use are filled with N(0, 1) values (the rest is never read), so a
+    pool of most of HBM costs no fill time.
+    """
+
+    def __init__(self, wl, steps_total: int, device, seed: int, pool_blocks: int | None = None):
         import numpy as np
         import torch
 
         self.wl = wl
         self.device = device
         bs = wl.block_size
-        # extend every table so it holds the tokens appended by all steps
         rng = np.random.default_rng(seed + 500)
         need = [-(-(c + steps_total + 1) // bs) for c in wl.context_lens]
-        self.num_blocks = max(int(sum(need) * 2), wl.num_blocks)
+        self.num_blocks = pool_blocks or max(int(sum(need) * 2), wl.num_blocks)
         perm = rng.permutation(self.num_blocks)
         tables, cursor = [], 0
         for n in need:
@@ -86,13 +108,17 @@ class DecodeBench:
         table_arr = np.zeros((len(tables), width), dtype=np.int32)
         for r, t in enumerate(tables):
             table_arr[r, : len(t)] = t
+        self.table_arr = table_arr
         shape = (wl.num_layers, self.num_blocks, bs, wl.kv_heads, wl.head_dim)
         gen = torch.Generator(device=device).manual_seed(seed)
-        self.k_cache = torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16)
-        self.v_cache = torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16)
+        self.k_cache = torch.empty(shape, device=device, dtype=torch.bfloat16)
+        self.v_cache = torch.empty(shape, device=device, dtype=torch.bfloat16)
+        used = torch.from_numpy(np.unique(np.concatenate(tables)).astype(np.int64)).to(device)
+        fill = (wl.num_layers, used.numel(), bs, wl.kv_heads, wl.head_dim)
+        for cache in (self.k_cache, self.v_cache):
+            cache[:, used] = torch.randn(fill, generator=gen, device=device, dtype=torch.bfloat16)
         self.tables = torch.from_numpy(table_arr).to(device)
         b = len(tables)
-        # per-step metadata, built before any timing
         slots = np.zeros((steps_total, b), dtype=np.int64)
         lens = np.zeros((steps_total, b), dtype=np.int32)
         self.max_len, self.total_len, self.seq_lens_host = [], [], []
@@ -111,7 +137,32 @@ class DecodeBench:
         self.out = torch.empty_like(self.q)
         self.scale = wl.head_dim**-0.5
 
-    def step(self, s: int, events: list | None = None, fused: bool = True) -> None:
+    def pool_bytes(self) -> int:
+        return 2 * self.k_cache.numel() * self.k_cache.element_size()
+
+    def prepared(self, s: int, serving_plan: bool = False):
+        """The step's decode launch.  serving_plan: planned as the serving path
+        plans it (``paged_batch.RaggedBatch``): no host lengths, every row at
+        the 512-rounded bound of the longest sequence."""
+        from nano_infer_engine import _native
+        from nano_infer_engine.paged_batch import decode_plan_bound
+
+        if not serving_plan:
+            return _native.PreparedDecode(self.k_cache, self.v_cache, self.tables, self.lens[s], self.max_len[s],
+                                          self.total_len[s], self.wl.q_heads, self.scale,
+                                          seq_lens_host=self.seq_lens_host[s])
+        bound = decode_plan_bound(self.max_len[s])
+        tables = self.tables
+        width = -(-bound // self.wl.block_size)
+        if tables.shape[1] < width:
+            import torch
+
+            pad = torch.zeros((tables.shape[0], width - tables.shape[1]), dtype=tables.dtype, device=tables.device)
+            tables = torch.cat([tables, pad], dim=1)
+        return _native.PreparedDecode(self.k_cache, self.v_cache, tables, self.lens[s], bound,
+                                      bound * tables.shape[0], self.wl.q_heads, self.scale)
+
+    def step(self, s: int, events: list | None = None, fused: bool = True, serving_plan: bool = False) -> None:
         """One decode step over every layer; optionally brackets each decode launch with HIP events.
 
         fused: one ``nie_paged_decode_append`` launch per layer writes the new
@@ -125,9 +176,7 @@ class DecodeBench:
         from nano_infer_engine import _native
 
         append = None if fused else _native.PreparedAppend(self.k_cache, self.v_cache, self.slots[s])
-        decode = _native.PreparedDecode(self.k_cache, self.v_cache, self.tables, self.lens[s], self.max_len[s],
-                                        self.total_len[s], self.wl.q_heads, self.scale,
-                                        seq_lens_host=self.seq_lens_host[s])
+        decode = self.prepared(s, serving_plan)
         for layer in range(self.wl.num_layers):
             if append is not None:
                 append(self.k_new, self.v_new, layer)
@@ -143,7 +192,34 @@ class DecodeBench:
                 events.append((start, end))
 
 
-def run_gpu(args):
+def _event_rate(bench, ev, first_step: int, steps: int, fused: bool):
+    """(bytes per call, median call seconds, GB/s) of HIP-event-timed calls.
+
+    The median: an event pair also spans the host's submission of the call,
+    and a host stall (the garbage collector, a page fault) lengthens a few
+    pairs to 100 us or more."""
+    from nano_infer_engine import workloads
+
+    avg = _median_us(ev) / 1e6
+    per_call = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(first_step, first_step + steps))
+    per_call = per_call * bench.wl.num_layers / len(ev)
+    if fused:
+        per_call += workloads.append_bytes(len(bench.wl.context_lens))
+    return per_call, avg, per_call / avg / 1e9
+
+
+def _measured_traffic():
+    """HBM bytes per decode call of the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE)."""
+    try:
+        with open(os.path.join(REPO, TRAFFIC_PROFILE)) as f:
+            data = json.load(f)
+        return data.get("hbm_bytes_per_launch"), data.get("algorithmic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None, None
+
+
+def run_decode(args):
+    """The ``value`` leg: configuration 2 over 16 layers, host-planned launches."""
     import torch
 
     from nano_infer_engine import _native, workloads
@@ -153,19 +229,18 @@ def run_gpu(args):
     _native.load_library()
     wl = workloads.decode_ragged(num_layers=args.layers)
     # steps [0, W) warm up, [W, W+K) are the timed steps, [W+K, W+2K) are
-    # timed again per call with HIP events (kept out of the wall-clock pass,
-    # whose host and queue work they would add to)
+    # timed again per call with HIP events and [W+2K, W+3K) with the serving
+    # plan (kept out of the wall-clock pass, whose host and queue work the
+    # events would add to)
     timed_end = args.warmup + args.steps
-    total_steps = timed_end + args.steps
+    total_steps = timed_end + 2 * args.steps
     bench = DecodeBench(wl, total_steps, device, seed=1)
     log(f"workload: {len(wl.context_lens)} seqs, contexts {wl.context_lens}, layers {args.layers}, "
-        f"pool {bench.num_blocks} blocks ({2 * bench.k_cache.numel() * 2 / 1e9:.2f} GB)")
-
+        f"pool {bench.num_blocks} blocks ({bench.pool_bytes() / 1e9:.2f} GB)")
     fused = not args.unfused_append
     for s in range(args.warmup):
         bench.step(s, fused=fused)
     torch.cuda.synchronize()
-
     t0 = time.perf_counter()
     for s in range(args.warmup, timed_end):
         bench.step(s, fused=fused)
@@ -173,25 +248,27 @@ def run_gpu(args):
     elapsed = time.perf_counter() - t0
 
     ev: list = []
-    for s in range(timed_end, total_steps):
+    for s in range(timed_end, timed_end + args.steps):
         bench.step(s, ev, fused=fused)
     torch.cuda.synchronize()
+    bytes_per_call, avg_s, achieved = _event_rate(bench, ev, timed_end, args.steps, fused)
 
-    step_append = workloads.append_bytes(len(wl.context_lens))
+    serve_ev: list = []
+    bench.step(timed_end + args.steps, fused=fused, serving_plan=True)  # warm the bound-planned launch
+    for s in range(timed_end + args.steps, total_steps):
+        bench.step(s, serve_ev, fused=fused, serving_plan=True)
+    torch.cuda.synchronize()
+    s_bytes, s_avg, s_gbs = _event_rate(bench, serve_ev, timed_end + args.steps, args.steps, fused)
+
     decode_bytes = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(args.warmup, timed_end))
     decode_bytes *= args.layers
-    append_bytes = step_append * args.layers * args.steps
-    event_bytes = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(timed_end, total_steps))
-    launch_ms = [a.elapsed_time(b) for a, b in ev]
-    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
-    # a fused call also moves the appended rows
-    bytes_per_launch = event_bytes * args.layers / len(launch_ms) + (step_append if fused else 0)
-    achieved = bytes_per_launch / avg_launch_s / 1e9
+    append_bytes = workloads.append_bytes(len(wl.context_lens)) * args.layers * args.steps
     value = (decode_bytes + append_bytes) / elapsed / 1e9
     call = "nie_paged_decode_append" if fused else "nie_paged_decode"
     log(f"timed {args.steps} steps in {elapsed * 1e3:.2f} ms ({value:.0f} GB/s); {call} call avg "
-        f"{avg_launch_s * 1e6:.2f} us for {bytes_per_launch / 1e6:.2f} MB -> {achieved:.0f} GB/s")
-
+        f"{avg_s * 1e6:.2f} us for {bytes_per_call / 1e6:.2f} MB -> {achieved:.0f} GB/s; serving plan "
+        f"{s_avg * 1e6:.2f} us -> {s_gbs:.0f} GB/s")
+    traffic, traffic_alg = _measured_traffic()
     result = {
         "metric": "paged-attn HBM GB/s (% of peak); e2e output tok/s, Llama-1B-shape batch 16",
         "value": round(value, 2),
@@ -223,32 +300,91 @@ def run_gpu(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": _measured_traffic(),
-            "algorithmic_bytes_per_launch": int(bytes_per_launch),
-            "avg_launch_us": round(avg_launch_s * 1e6, 3),
+            "traffic": traffic,
+            "traffic_source": f"{TRAFFIC_PROFILE}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this call on this "
+                              f"workload (algorithmic bytes there: {traffic_alg}), scaled by a 1 GiB copy",
+            "algorithmic_bytes_per_launch": int(bytes_per_call),
+            "avg_launch_us": round(avg_s * 1e6, 3),
+        },
+        "serving_plan_decode": {
+            "plan": "as the serving path plans it: no host lengths, every row at the 512-rounded bound",
+            "avg_launch_us": round(s_avg * 1e6, 3), "achieved_GBs": round(s_gbs, 1),
+            "frac": round(s_gbs / HBM_PEAK_GBS, 4),
         },
     }
     del bench
     torch.cuda.empty_cache()
-    if not args.skip_stress:
-        result["stress_16x29600"] = run_stress(args)
-    if not args.skip_mixed:
-        result["mixed_prefill_step"] = run_mixed(args)
-    if not args.skip_e2e:
-        result["e2e_llama1b_serving"] = run_e2e(args)
     return result
 
 
+def run_decode_small(args):
+    """Configuration 1: 4 sequences {17, 64, 129, 500}, 256-block pool, one call, bf16."""
+    import torch
+
+    from nano_infer_engine import _native, workloads
+
+    device = torch.device("cuda:0")
+    wl = workloads.decode_small()
+    kc, vc = wl.pool(torch.bfloat16, device)
+    q, _, _ = wl.new_tokens(torch.bfloat16, device)
+    tables = torch.from_numpy(wl.table_array()).to(device)
+    lens = torch.tensor(wl.seq_lens, dtype=torch.int32, device=device)
+    decode = _native.PreparedDecode(kc, vc, tables, lens, max(wl.seq_lens), sum(wl.seq_lens), wl.q_heads,
+                                    wl.head_dim**-0.5, seq_lens_host=wl.seq_lens)
+    out = torch.empty_like(q)
+    for _ in range(10):
+        decode(q, 0, out)
+    ev = []
+    for _ in range(100):
+        e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        e[0].record()
+        decode(q, 0, out)
+        e[1].record()
+        ev.append(e)
+    torch.cuda.synchronize()
+    us = _median_us(ev)
+    nbytes = workloads.decode_bytes(wl.seq_lens)
+    log(f"decode small: {us:.2f} us for {nbytes / 1e6:.3f} MB")
+    return {"avg_launch_us": round(us, 2), "bytes_per_launch": nbytes,
+            "achieved_GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+# ---------------------------------------------------------------------------
+# configuration 5: 16 x 29600 contexts on a pool of most of HBM
+# ---------------------------------------------------------------------------
+def _free_bytes() -> int:
+    import torch
+
+    torch.cuda.empty_cache()
+    return torch.cuda.mem_get_info()[0]
+
+
 def run_stress(args):
-    """Decode over 16 x 29600-token contexts (970 MB per layer-step), one layer."""
+    """Decode over 16 x 29600-token contexts (970 MB per layer-step) with one
+    append per step, on one layer whose pool is ``--pool-fraction`` of the
+    free device memory with fully permuted tables."""
     import torch
 
     from nano_infer_engine import workloads
 
     device = torch.device("cuda:0")
-    steps, warmup = 20, 3
+    steps, warmup = args.stress_steps, 5
     wl = workloads.decode_long(num_layers=1)
-    bench = DecodeBench(wl, steps + warmup, device, seed=4)
+    block_bytes = 2 * wl.block_size * wl.kv_heads * wl.head_dim * 2  # K + V of one block, bf16
+    bench = None
+    for fraction in (args.pool_fraction, 0.8 * args.pool_fraction, 0.6 * args.pool_fraction):
+        pool_blocks = int(_free_bytes() * fraction) // block_bytes
+        try:
+            bench = DecodeBench(wl, steps + warmup, device, seed=4, pool_blocks=pool_blocks)
+            break
+        except torch.OutOfMemoryError:
+            log(f"stress pool of {fraction:.0%} of free memory did not fit; trying less")
+            torch.cuda.empty_cache()
+    if bench is None:
+        raise RuntimeError("no stress pool fits")
+    args = argparse.Namespace(**{**vars(args), "pool_fraction": fraction})
+    log(f"stress pool: {pool_blocks} blocks = {bench.pool_bytes() / 1e9:.1f} GB "
+        f"({args.pool_fraction:.0%} of free), tables over the whole pool")
     fused = not args.unfused_append
     for s in range(warmup):
         bench.step(s, fused=fused)
@@ -257,19 +393,74 @@ def run_stress(args):
     for s in range(warmup, warmup + steps):
         bench.step(s, ev, fused=fused)
     torch.cuda.synchronize()
-    launch_ms = [a.elapsed_time(b) for a, b in ev]
-    avg = sum(launch_ms) / len(launch_ms) / 1e3
-    per_launch = sum(workloads.decode_bytes(bench.seq_lens_host[s]) for s in range(warmup, warmup + steps)) / steps
-    if fused:
-        per_launch += workloads.append_bytes(len(wl.context_lens))
-    gbs = per_launch / avg / 1e9
-    log(f"stress 16x29600: {avg * 1e6:.1f} us per layer-step, {gbs:.0f} GB/s")
+    per_call, avg, gbs = _event_rate(bench, ev, warmup, steps, fused)
+    log(f"stress 16x29600: {avg * 1e6:.1f} us per layer-step over {steps} steps, {gbs:.0f} GB/s")
+    out = {"avg_launch_us": round(avg * 1e6, 2), "bytes_per_launch": int(per_call),
+           "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "steps": steps,
+           "pool_blocks": pool_blocks, "pool_GB": round(bench.pool_bytes() / 1e9, 1),
+           "pool_fraction_of_free": args.pool_fraction}
     del bench
     torch.cuda.empty_cache()
-    return {"avg_launch_us": round(avg * 1e6, 2), "bytes_per_launch": int(per_launch),
-            "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
 
 
+def run_stress_model(args):
+    """The 16 x 29600 decode through the whole Llama-3.2-1B-shaped model:
+    captured decode steps (``DecodeGraphRunner``) over a 16-layer cache of
+    ``--pool-fraction`` of the free memory whose allocator hands out blocks in
+    a seeded random order; the contexts' K/V are N(0, 1) values."""
+    import numpy as np
+    import torch
+
+    from nano_infer_engine import workloads
+    from nano_infer_engine.generation.decode_graph import DecodeGraphRunner
+    from nano_infer_engine.paged_cache import PagedKVCache
+
+    device = torch.device("cuda:0")
+    model = workloads.serving_model(device)
+    cfg = model.config
+    steps, ctx = args.stress_steps, 29600
+    block_bytes = 2 * cfg.num_layers * 16 * cfg.kv_head_num * cfg.head_dim * 2
+    # leave room for activations and a few captured graphs
+    pool_blocks = int((_free_bytes() - (4 << 30)) * args.pool_fraction) // block_bytes
+    cache = PagedKVCache(pool_blocks, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim, torch.bfloat16, device)
+    # a permuted free list: take every block, give them back in random order
+    everything = cache.allocator.allocate(pool_blocks)
+    cache.allocator.free(np.random.default_rng(5).permutation(everything).tolist())
+    ids = tuple(f"long-{i}" for i in range(16))
+    for sid in ids:
+        cache.ensure_capacity(sid, ctx + steps + 1)
+        cache.advance(sid, ctx)
+    used = torch.tensor(sorted(b for sid in ids for b in cache.get_block_table(sid)), device=device)
+    gen = torch.Generator(device=device).manual_seed(4)
+    for layer in range(cfg.num_layers):
+        for pool in (cache.keys, cache.values):
+            pool[layer, used] = torch.randn((used.numel(), 16, cfg.kv_head_num, cfg.head_dim), generator=gen,
+                                            device=device, dtype=torch.bfloat16)
+    runner = DecodeGraphRunner(model, cache, 16)
+    tokens = torch.randint(0, cfg.vocab_size, (16,), generator=gen, device=device)
+    times = []
+    for s in range(steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _, tokens = runner.step(tokens, ids)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times[3:])) * 1e3
+    kv = workloads.decode_bytes([ctx + steps // 2] * 16) * cfg.num_layers
+    log(f"stress full model: {ms:.3f} ms per decode step (median of {steps - 3}; {runner.captures} captures), "
+        f"pool {pool_blocks} blocks = {2 * cache.keys.numel() * 2 / 1e9:.1f} GB")
+    out = {"ms_per_step": round(ms, 3), "output_tok_per_s": round(16 / ms * 1e3, 1), "steps": steps,
+           "attention_bytes_per_step": kv, "pool_blocks": pool_blocks,
+           "pool_GB": round(2 * cache.keys.numel() * 2 / 1e9, 1), "graph_captures": runner.captures}
+    del runner, cache, model
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# configuration 3: mixed chunked-prefill step
+# ---------------------------------------------------------------------------
 def run_mixed(args):
     """Mixed chunked-prefill step: 4 x 128-token chunks on contexts {0, 384, 1024, 4000}
     + 12 decode rows (contexts U[256, 8192]), packed varlen layout, one layer.
@@ -322,8 +513,7 @@ def run_mixed(args):
     torch.cuda.synchronize()
     # medians: an event pair also spans the host's launch of the call, so a
     # host stall (a page fault, the garbage collector) would skew a mean
-    p_us = float(np.median([a.elapsed_time(b) for a, b in pev])) * 1e3
-    d_us = float(np.median([a.elapsed_time(b) for a, b in dev_])) * 1e3
+    p_us, d_us = _median_us(pev), _median_us(dev_)
     flops = workloads.prefill_flops(wl.context_lens[:n_pref], wl.query_lens[:n_pref])
     tflops = flops / (p_us * 1e-6) / 1e12
     dbytes = workloads.decode_bytes(seq_lens[n_pref:])
@@ -341,59 +531,33 @@ def run_mixed(args):
     }
 
 
-E2E_REQUESTS = 64
-E2E_NEW_TOKENS = 256
-
-
-def build_e2e_model(device):
-    """Llama-3.2-1B shape (LlamaConfig defaults), bf16, Linear/Embedding weights N(0, 0.02), norms 1."""
-    import torch
-    from torch import nn
-
-    from nano_infer_engine.models.llama import Llama3_2, LlamaConfig
-
-    torch.manual_seed(3)
-    with torch.device(device):
-        model = Llama3_2(LlamaConfig())
-    model = model.to(torch.bfloat16).eval()
-    with torch.no_grad():
-        for m in model.modules():
-            if isinstance(m, (nn.Linear, nn.Embedding)):
-                m.weight.normal_(0.0, 0.02)
-    return model
-
-
-def e2e_prompts(device, vocab, count=E2E_REQUESTS, seed=3):
-    import numpy as np
-    import torch
-
-    rng = np.random.default_rng(seed)
-    lens = rng.integers(128, 2049, size=count)
-    return [torch.from_numpy(rng.integers(0, vocab, size=(1, int(n)))).to(device) for n in lens]
-
-
-def e2e_run(model, prompts, device, max_new_tokens, max_steps=None, graphs=True):
+# ---------------------------------------------------------------------------
+# configuration 4: end-to-end serving
+# ---------------------------------------------------------------------------
+def serve(model, prompts, device, max_new_tokens, graphs=True):
     """Serve every prompt through the continuous-batching scheduler; returns (seconds, steps, requests).
 
     With ``graphs`` the all-decode steps replay captured HIP graphs (captures
     happen inside the timed region, as in a fresh server)."""
     import torch
 
+    from nano_infer_engine import workloads
     from nano_infer_engine.generation import ContinuousBatchingScheduler, GenerationConfig
     from nano_infer_engine.paged_cache import PagedKVCache
 
     cfg = model.config
-    blocks_per_request = -(-(max(p.shape[1] for p in prompts) + max_new_tokens) // 16)
-    cache = PagedKVCache(16 * blocks_per_request + 64, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim,
-                         torch.bfloat16, device)
-    gen = GenerationConfig(max_new_tokens=max_new_tokens, eos_token_id=None, prefill_chunk_size=128,
-                           max_prefill_tokens_per_step=512)
-    sched = ContinuousBatchingScheduler(model, gen, cache, max_batch_size=16, decode_graphs=graphs)
+    cache = PagedKVCache(workloads.serving_cache_blocks(prompts, max_new_tokens), 16, cfg.num_layers,
+                         cfg.kv_head_num, cfg.head_dim, torch.bfloat16, device)
+    gen = GenerationConfig(max_new_tokens=max_new_tokens, eos_token_id=None,
+                           prefill_chunk_size=workloads.SERVING_CHUNK,
+                           max_prefill_tokens_per_step=workloads.SERVING_STEP_BUDGET)
+    sched = ContinuousBatchingScheduler(model, gen, cache, max_batch_size=workloads.SERVING_MAX_BATCH,
+                                        decode_graphs=graphs)
     reqs = [sched.add_request(f"request-{i}", p) for i, p in enumerate(prompts)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     steps = 0
-    while sched.has_work and (max_steps is None or steps < max_steps):
+    while sched.has_work:
         sched.step()
         steps += 1
     torch.cuda.synchronize()
@@ -401,46 +565,27 @@ def e2e_run(model, prompts, device, max_new_tokens, max_steps=None, graphs=True)
 
 
 def run_e2e(args):
-    """Configuration-4 serving run, and the same model with the reference attention algorithm."""
+    """Configuration 4: 64 requests x 256 greedy tokens, graph-replayed and eager decode steps."""
     import torch
 
-    import nano_infer_engine.layers.attention as attention_module
-    from oracle import reference_ops
+    import nano_infer_engine.layers.linear as linear_module
+    from nano_infer_engine import workloads
 
+    linear_module.USE_NATIVE = args.native_gemm == "on"
     device = torch.device("cuda:0")
-    model = build_e2e_model(device)
-    prompts = e2e_prompts(device, model.config.vocab_size)
-    e2e_run(model, prompts[:2], device, 8)  # warm-up: library load, GEMM heuristics
-    secs, steps, reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS)
+    model = workloads.serving_model(device)
+    prompts = workloads.serving_prompts(device, model.config.vocab_size)
+    serve(model, prompts[:2], device, 8)  # warm-up: library load, GEMM heuristics
+    secs, steps, reqs = serve(model, prompts, device, workloads.SERVING_NEW_TOKENS)
     out_tokens = sum(r.generated_tokens for r in reqs)
     tok_s = out_tokens / secs
     log(f"e2e: {out_tokens} output tokens from {len(prompts)} requests in {secs:.2f} s "
         f"({steps} steps) -> {tok_s:.0f} tok/s")
-    eager_secs, _, eager_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, graphs=False)
+    eager_secs, _, eager_reqs = serve(model, prompts, device, workloads.SERVING_NEW_TOKENS, graphs=False)
     eager_tok_s = sum(r.generated_tokens for r in eager_reqs) / eager_secs
     same_modes = all(torch.equal(a.sequence, b.sequence) for a, b in zip(reqs, eager_reqs))
     log(f"e2e eager (no decode graphs): {eager_secs:.2f} s -> {eager_tok_s:.0f} tok/s; "
         f"tokens identical to the graph run: {same_modes}")
-    # the reference attention algorithm (per-request gather / repeat_interleave /
-    # matmul / mask / softmax) under the same scheduler, on the first steps only
-    k = args.e2e_ref_steps
-    ours_k, _, ours_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
-    # the reference's algorithms end to end: its attention loop and torch's
-    # GEMM for every projection
-    import nano_infer_engine.layers.linear as linear_module
-
-    saved = attention_module.attention_core
-    saved_native = linear_module.USE_NATIVE
-    attention_module.attention_core = reference_ops.attention_core_like_product
-    linear_module.USE_NATIVE = False
-    try:
-        ref_k, _, ref_reqs = e2e_run(model, prompts, device, E2E_NEW_TOKENS, max_steps=k)
-    finally:
-        attention_module.attention_core = saved
-        linear_module.USE_NATIVE = saved_native
-    same = all(torch.equal(a.sequence, b.sequence) for a, b in zip(ours_reqs, ref_reqs))
-    log(f"e2e first {k} steps: ours {ours_k * 1e3:.1f} ms, reference algorithms {ref_k * 1e3:.1f} ms "
-        f"({ref_k / ours_k:.1f}x); sequences identical: {same}")
     del model
     torch.cuda.empty_cache()
     return {
@@ -450,11 +595,187 @@ def run_e2e(args):
         "output_tokens": out_tokens,
         "seconds": round(secs, 3),
         "scheduler_steps": steps,
+        "decode_gemm": "nie_linear_rows" if linear_module.USE_NATIVE else "torch",
         "workload": "Llama-3.2-1B shape, bf16, random N(0, 0.02) weights; 64 requests, prompts U[128, 2048] "
                     "(seed 3), 256 greedy tokens each, max batch 16, prefill chunk 128, 512 prefill tokens/step",
-        "reference_first_steps": {"steps": k, "ours_ms": round(ours_k * 1e3, 2), "reference_ms": round(ref_k * 1e3, 2),
-                                  "speedup": round(ref_k / ours_k, 2), "sequences_identical": same},
     }
+
+
+# ---------------------------------------------------------------------------
+# the reference algorithm's own times (the oracle, on the GPU and the host)
+# ---------------------------------------------------------------------------
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_host(fn, min_seconds: float, max_reps: int = 1000, warmup: bool = True):
+    """(seconds per call, calls) of fn on the host, after one warm-up call."""
+    if warmup:
+        fn()
+    done, t0 = 0, time.perf_counter()
+    while done < max_reps:
+        fn()
+        done += 1
+        if time.perf_counter() - t0 >= min_seconds:
+            break
+    return (time.perf_counter() - t0) / done, done
+
+
+def _time_gpu(fn, min_seconds: float, max_reps: int = 100):
+    import torch
+
+    def synced():
+        fn()
+        torch.cuda.synchronize()
+
+    return _time_host(synced, min_seconds, max_reps)
+
+
+def run_cpu_baseline(args):
+    """The oracle (the reference's per-block decode loop, torch bf16 on the
+    host cores) on a bounded sample of the ``value`` workload."""
+    import torch
+
+    from nano_infer_engine import workloads
+    from oracle import reference_ops
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    wl = workloads.decode_ragged(num_layers=1)
+    kc, vc = wl.pool(torch.bfloat16)
+    q, _, _ = wl.new_tokens(torch.bfloat16)
+    tables = tuple(tuple(t) for t in wl.tables)
+    lens = tuple(wl.seq_lens)
+    per_call, done = _time_host(lambda: reference_ops.batched_paged_attention_reference(q, kc, vc, tables, lens, 0),
+                                args.cpu_seconds)
+    gbs = workloads.decode_bytes(lens) / per_call / 1e9
+    cpu = _cpu_model()
+    log(f"cpu baseline: {done} layer-steps, {per_call * 1e3:.1f} ms each on {threads} threads ({cpu}) "
+        f"-> {gbs:.3f} GB/s")
+    return {
+        "value": round(gbs, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "cpu_model": cpu,
+        "sample": f"{done} single-layer decode attention calls over the same 16 sequences "
+                  f"({sum(lens)} tokens), the reference's per-block loop in torch bf16 on the host, "
+                  f"{done * per_call:.1f} s",
+    }
+
+
+def run_reference_path(args):
+    """The reference algorithm (the oracle's restatement, torch) timed on the
+    GPU and on the host cores for configurations 1, 2, 3 and 5 (one layer;
+    configuration 5 one step), beside this build's HIP figures."""
+    import torch
+
+    from nano_infer_engine import workloads
+    from oracle import reference_ops
+
+    device = torch.device("cuda:0")
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    out = {"cpu_model": _cpu_model(), "cpu_threads": threads}
+
+    def decode_case(name, wl, cpu_seconds, gpu_seconds, host_warmup=True):
+        # N(0, 1) pool and queries drawn on the device (a 16 x 29600 pool
+        # is 1.9 GB) and copied to the host for the CPU leg
+        gen = torch.Generator(device=device).manual_seed(wl.seed)
+        shape = (1, wl.num_blocks, wl.block_size, wl.kv_heads, wl.head_dim)
+        gk, gv = (torch.randn(shape, generator=gen, device=device, dtype=torch.bfloat16) for _ in range(2))
+        gq = torch.randn((len(wl.seq_lens), wl.q_heads, wl.head_dim), generator=gen, device=device,
+                         dtype=torch.bfloat16)
+        kc, vc, q = gk.cpu(), gv.cpu(), gq.cpu()
+        tables, lens = tuple(tuple(t) for t in wl.tables), tuple(wl.seq_lens)
+        g_s, g_n = _time_gpu(lambda: reference_ops.batched_paged_attention_reference_matmul(gq, gk, gv, tables, lens,
+                                                                                          0), gpu_seconds)
+        c_s, c_n = _time_host(lambda: reference_ops.batched_paged_attention_reference(q, kc, vc, tables, lens, 0),
+                              cpu_seconds, max_reps=50, warmup=host_warmup)
+        nbytes = workloads.decode_bytes(lens)
+        log(f"reference {name}: GPU torch {g_s * 1e3:.2f} ms ({g_n} calls), CPU {c_s * 1e3:.1f} ms ({c_n} calls)")
+        out[name] = {"bytes_per_call": nbytes, "gpu_torch_ms": round(g_s * 1e3, 3),
+                     "gpu_torch_GBs": round(nbytes / g_s / 1e9, 2), "cpu_ms": round(c_s * 1e3, 2),
+                     "cpu_GBs": round(nbytes / c_s / 1e9, 4)}
+        del gk, gv
+        torch.cuda.empty_cache()
+
+    decode_case("config1_decode_small", workloads.decode_small(), 2.0, 1.0)
+    decode_case("config2_decode_step", workloads.decode_ragged(), 2.0, 2.0)
+    decode_case("config5_decode_16x29600", workloads.decode_long(), 1.0, 2.0, host_warmup=False)
+
+    wl = workloads.mixed_prefill()
+    kc, vc = wl.pool(torch.bfloat16)
+    q, k_new, v_new = wl.new_tokens(torch.bfloat16)
+    args_cpu = (q, k_new, v_new, kc, vc)
+    args_gpu = tuple(t.to(device) for t in args_cpu)
+    meta = (0, wl.tables, wl.context_lens, wl.query_lens, wl.head_dim**-0.5)
+    g_s, _ = _time_gpu(lambda: reference_ops.ragged_attention_reference_vectorized(*args_gpu, *meta), 2.0)
+    c_s, _ = _time_host(lambda: reference_ops.ragged_attention_reference(*args_cpu, *meta), 2.0, max_reps=20)
+    flops = workloads.prefill_flops(wl.context_lens[:4], wl.query_lens[:4])
+    log(f"reference config3: GPU torch {g_s * 1e3:.2f} ms, CPU {c_s * 1e3:.1f} ms")
+    out["config3_mixed_step"] = {"gpu_torch_ms": round(g_s * 1e3, 3), "cpu_ms": round(c_s * 1e3, 2),
+                                 "prefill_flops": flops, "note": "whole step (4 prefill chunks + 12 decode rows); "
+                                 "the GPU leg gathers with one index_select per request, the host leg token by token "
+                                 "as the reference does"}
+    del args_gpu
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_lockstep(args):
+    """Configuration 4's numerics and the reference path's end-to-end rate:
+    ``--lockstep-requests`` requests served by the product, every step
+    replayed on the reference algorithm in bf16 and in fp32."""
+    import torch
+
+    import nano_infer_engine.layers.linear as linear_module
+    from nano_infer_engine import workloads
+    from nano_infer_engine.paged_cache import PagedKVCache
+    from oracle import lockstep
+
+    linear_module.USE_NATIVE = args.native_gemm == "on"
+    device = torch.device("cuda:0")
+    model = workloads.serving_model(device)
+    cfg = model.config
+    prompts = workloads.serving_prompts(device, cfg.vocab_size, count=args.lockstep_requests)
+    blocks = workloads.serving_cache_blocks(prompts, workloads.SERVING_NEW_TOKENS)
+
+    def cache(dtype):
+        return PagedKVCache(blocks, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim, dtype, device)
+
+    serve(model, prompts[:2], device, 8)  # warm-up
+    secs, _, reqs = serve(model, prompts, device, workloads.SERVING_NEW_TOKENS)
+    ours = sum(r.generated_tokens for r in reqs) / secs
+    report = lockstep.run_lockstep(model, prompts, cache, max_new_tokens=workloads.SERVING_NEW_TOKENS,
+                                   max_batch_size=workloads.SERVING_MAX_BATCH, chunk=workloads.SERVING_CHUNK,
+                                   budget=workloads.SERVING_STEP_BUDGET, variant=args.lockstep_variant)
+    summary = report.summary()
+    tokens = summary["sampled_rows"]
+    ref_rate = tokens / report.reference_seconds
+    log(f"lockstep: {summary['requests']} requests, top-1 agreement product/reference "
+        f"{summary['top1_agreement_product_reference']:.4f}, product/truth {summary['top1_agreement_product_truth']:.4f}, "
+        f"reference/truth {summary['top1_agreement_reference_truth']:.4f}; reference path {ref_rate:.0f} tok/s "
+        f"against {ours:.0f} tok/s")
+    firsts = summary.pop("first_divergence")
+    summary["first_divergence_tokens"] = sorted(v["token"] for v in firsts.values() if v)
+    summary["reference_output_tok_per_s"] = round(ref_rate, 1)
+    summary["product_output_tok_per_s"] = round(ours, 1)
+    summary["speedup"] = round(ours / ref_rate, 2)
+    summary["decode_gemm"] = "nie_linear_rows" if linear_module.USE_NATIVE else "torch"
+    summary["method"] = ("the product serves the requests as shipped; each step is replayed, teacher-forced, on "
+                         "the reference algorithm (bf16; one index_select per request instead of the per-token "
+                         "gather) and in fp32 (the truth); the reference rate is the sum of its forwards' times")
+    del model
+    torch.cuda.empty_cache()
+    return summary
 
 
 def run_linear(args):
@@ -513,56 +834,12 @@ def run_linear(args):
             del graph
         gbs = n * k * 2 / (res["nie_linear_rows"] * 1e-6) / 1e9
         out[name] = {"n": n, "k": k, "us": round(res["nie_linear_rows"], 2), "GBs": round(gbs, 1),
-                     "frac": round(gbs / 8000.0, 4), "torch_us": round(res["torch"], 2)}
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "torch_us": round(res["torch"], 2)}
         log(f"{name:15s} {n}x{k}: nie_linear_rows {res['nie_linear_rows']:.2f} us ({gbs:.0f} GB/s), "
             f"torch {res['torch']:.2f} us")
         del ws
         torch.cuda.empty_cache()
     return out
-
-
-def _measured_traffic():
-    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if present."""
-    path = os.path.join(REPO, "profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json")
-    try:
-        with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
-        return None
-
-
-def run_cpu_baseline(args):
-    """The oracle (reference algorithm, torch on CPU) on a bounded sample of the workload."""
-    import torch
-
-    from nano_infer_engine import workloads
-    from oracle import reference_ops
-
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    wl = workloads.decode_ragged(num_layers=1)
-    kc, vc = wl.pool(torch.bfloat16)
-    q, _, _ = wl.new_tokens(torch.bfloat16)
-    tables = tuple(tuple(t) for t in wl.tables)
-    lens = tuple(wl.seq_lens)
-    reference_ops.batched_paged_attention_reference(q, kc, vc, tables, lens, 0)  # warm-up
-    done, t0 = 0, time.perf_counter()
-    while True:
-        reference_ops.batched_paged_attention_reference(q, kc, vc, tables, lens, 0)
-        done += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    elapsed = time.perf_counter() - t0
-    gbs = workloads.decode_bytes(lens) * done / elapsed / 1e9
-    log(f"cpu baseline: {done} layer-steps in {elapsed:.1f} s on {threads} threads -> {gbs:.3f} GB/s")
-    return {
-        "value": round(gbs, 4),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{done} single-layer decode attention calls over the same 16 sequences "
-                  f"({sum(lens)} tokens), reference per-block loop in torch bf16 on CPU, {elapsed:.1f} s",
-    }
 
 
 def run_copy_calibration(mib: int):
@@ -587,32 +864,37 @@ def main():
     if args.copy_calibration:
         run_copy_calibration(args.copy_calibration)
         return
-    if args.e2e_only:
-        from nano_infer_engine import _native
+    from nano_infer_engine import _native
 
-        _native.load_library()
-        print(json.dumps({"e2e_llama1b_serving": run_e2e(args)}), flush=True)
+    _native.load_library()
+    only = {
+        "decode": ("decode", run_decode), "small": ("decode_small", run_decode_small),
+        "stress": ("stress_16x29600", lambda a: {"attention": run_stress(a), "full_model": run_stress_model(a)}),
+        "mixed": ("mixed_prefill_step", run_mixed), "e2e": ("e2e_llama1b_serving", run_e2e),
+        "linear": ("decode_projections", run_linear),
+        "reference": ("reference_path", lambda a: {**run_reference_path(a), "serving_lockstep": run_lockstep(a)}),
+    }
+    if args.only:
+        key, fn = only[args.only]
+        print(json.dumps({key: fn(args)}), flush=True)
         return
-    if args.mixed_only:
-        from nano_infer_engine import _native
-
-        _native.load_library()
-        print(json.dumps({"mixed_prefill_step": run_mixed(args)}), flush=True)
-        return
-    if args.linear_only:
-        from nano_infer_engine import _native
-
-        _native.load_library()
-        print(json.dumps({"decode_projections": run_linear(args)}), flush=True)
-        return
-    if args.stress_only:
-        from nano_infer_engine import _native
-
-        _native.load_library()
-        print(json.dumps({"stress_16x29600": run_stress(args)}), flush=True)
-        return
-    result = run_gpu(args)
-    result["cpu_baseline"] = None if args.skip_cpu else run_cpu_baseline(args)
+    skip = set(args.skip)
+    result = run_decode(args)
+    if "small" not in skip:
+        result["decode_small"] = run_decode_small(args)
+    if "stress" not in skip:
+        result["stress_16x29600"] = run_stress(args)
+        if "stress-model" not in skip:
+            result["stress_16x29600"]["full_model"] = run_stress_model(args)
+    if "mixed" not in skip:
+        result["mixed_prefill_step"] = run_mixed(args)
+    if "e2e" not in skip:
+        result["e2e_llama1b_serving"] = run_e2e(args)
+    if "reference" not in skip:
+        result["reference_path"] = run_reference_path(args)
+        if "lockstep" not in skip:
+            result["reference_path"]["serving_lockstep"] = run_lockstep(args)
+    result["cpu_baseline"] = None if "cpu" in skip else run_cpu_baseline(args)
     print(json.dumps(result), flush=True)
 
 

@@ -56,6 +56,42 @@ def batched_paged_attention_reference(query, key_cache, value_cache, block_table
     )
 
 
+def paged_attention_reference_matmul(query, key_cache, value_cache, block_table, sequence_length, layer_index):
+    """:func:`paged_attention_reference` with each ``einsum`` written as a
+    batched ``matmul`` over contiguous operands (head-major), for timing the
+    reference's per-block loop on a ROCm GPU, where a bf16 batched product
+    over a transposed operand (what einsum forms inside) has faulted.  The
+    loop, the repeat_interleave, the scale, the fp32 softmax and the casts
+    are the reference's (``layers/paged_attention.py:82-114``)."""
+    _, _, block_size, kv_heads, head_dim = key_cache.shape
+    group = query.shape[0] // kv_heads
+    blocks = -(-sequence_length // block_size)
+    scores, values = [], []
+    for logical, physical in enumerate(block_table[:blocks]):
+        valid = min(block_size, sequence_length - logical * block_size)
+        k_rows = key_cache[layer_index, physical, :valid].repeat_interleave(group, dim=1)
+        v_rows = value_cache[layer_index, physical, :valid].repeat_interleave(group, dim=1)
+        k_t = k_rows.permute(1, 2, 0).contiguous()  # (Hq, D, valid)
+        scores.append((query[:, None, :] @ k_t)[:, 0, :] * (head_dim**-0.5))
+        values.append(v_rows)
+    weights = torch.softmax(torch.cat(scores, dim=-1), dim=-1, dtype=torch.float32).to(query.dtype)
+    v_all = torch.cat(values, dim=0).transpose(0, 1).contiguous()  # (Hq, S, D)
+    return (weights[:, None, :] @ v_all)[:, 0, :]
+
+
+def batched_paged_attention_reference_matmul(query, key_cache, value_cache, block_tables, sequence_lengths,
+                                             layer_index):
+    """Per-sequence loop + stack of :func:`paged_attention_reference_matmul`."""
+    return torch.stack(
+        [
+            paged_attention_reference_matmul(query[b], key_cache, value_cache, block_tables[b], sequence_lengths[b],
+                                             layer_index)
+            for b in range(query.shape[0])
+        ],
+        dim=0,
+    )
+
+
 def write_tokens(keys, values, layer_index, table, block_size, start_position, new_keys, new_values) -> None:
     """Per-token scatter into the pool (``paged_cache.py:306-322``)."""
     for t in range(new_keys.shape[0]):
@@ -114,6 +150,34 @@ def ragged_attention_reference(
         q_pos = torch.arange(ctx, total, device=q.device)[:, None]
         k_pos = torch.arange(total, device=q.device)[None, :]
         scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
+        probs = torch.softmax(scores, dim=-1, dtype=torch.float32)
+        outputs.append((probs.to(vs.dtype) @ vs).transpose(0, 1))
+        start = end
+    return torch.cat(outputs, dim=0)
+
+
+def ragged_attention_reference_vectorized(q, k, v, keys, values, layer_index, tables, context_lens, query_lens,
+                                          scale: float) -> torch.Tensor:
+    """:func:`ragged_attention_reference` with the per-token write and gather
+    each done as one indexed copy over the request's flat slots (the same
+    elements, so the same values), for timing the reference's per-request
+    loop on a GPU without its per-token launches."""
+    block_size, hkv, d = keys.shape[2], keys.shape[3], keys.shape[4]
+    group = q.shape[1] // k.shape[1]
+    flat_k = keys[layer_index].view(-1, hkv, d)
+    flat_v = values[layer_index].view(-1, hkv, d)
+    outputs = []
+    start = 0
+    for table, ctx, n in zip(tables, context_lens, query_lens):
+        end, total = start + n, ctx + n
+        pos = torch.arange(total, device=q.device)
+        slots = torch.as_tensor(list(table), device=q.device)[pos // block_size] * block_size + pos % block_size
+        flat_k[slots[ctx:]] = k[start:end]
+        flat_v[slots[ctx:]] = v[start:end]
+        ks = flat_k.index_select(0, slots).repeat_interleave(group, dim=1).transpose(0, 1)
+        vs = flat_v.index_select(0, slots).repeat_interleave(group, dim=1).transpose(0, 1).contiguous()
+        scores = q[start:end].transpose(0, 1) @ ks.transpose(-1, -2).contiguous() * scale
+        scores = scores.masked_fill(pos[None, :] > pos[ctx:, None], float("-inf"))
         probs = torch.softmax(scores, dim=-1, dtype=torch.float32)
         outputs.append((probs.to(vs.dtype) @ vs).transpose(0, 1))
         start = end

@@ -188,6 +188,35 @@ def test_ragged_reference_matches_closed_form():
         start += n
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_timing_variants_of_the_oracle_agree_with_it(dtype):
+    """The GPU-timing variants (batched matmuls over contiguous operands
+    instead of einsum; indexed write / gather instead of per-token copies)
+    compute the same values: the vectorized ragged oracle bit for bit on the
+    CPU (same products on the same gathered tensors), the matmul decode loop
+    within fp32 reassociation / one bf16 rounding of the einsum loop, and the
+    closed form as a third witness."""
+    lengths = [1, 17, 64, 129]
+    kc, vc, tables, contig, q = _paged_layout(13, lengths, 16, 8, 2, 64, 40)
+    kc, vc, q = kc.to(dtype), vc.to(dtype), q.to(dtype)
+    a = reference_ops.batched_paged_attention_reference(q, kc, vc, tables, tuple(lengths), 1)
+    b = reference_ops.batched_paged_attention_reference_matmul(q, kc, vc, tables, tuple(lengths), 1)
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    assert (a.float() - b.float()).abs().max().item() <= tol
+    for i, (ks, vs) in enumerate(contig):
+        exact = closed_form.decode(q[i].float().numpy(), ks.to(dtype).float().numpy(), vs.to(dtype).float().numpy(),
+                                   64**-0.5)
+        assert np.abs(b[i].float().numpy() - exact).max() < (1e-5 if dtype == torch.float32 else 2e-2)
+    wl, kc, vc, q, k, v = _ragged_case(23, [0, 3, 40, 0], [9, 5, 1, 17], bs=4, dtype=dtype)
+    k1, v1, k2, v2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    want = reference_ops.ragged_attention_reference(q, k, v, k1, v1, 0, wl.tables, wl.context_lens, wl.query_lens,
+                                                    0.125)
+    got = reference_ops.ragged_attention_reference_vectorized(q, k, v, k2, v2, 0, wl.tables, wl.context_lens,
+                                                              wl.query_lens, 0.125)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(got, want)
+
+
 def test_ragged_chunked_equals_one_shot_and_decode_row_equals_decode():
     wl, kc, vc, q, k, v = _ragged_case(22, [0], [24], bs=4)
     one_k, one_v = kc.clone(), vc.clone()
