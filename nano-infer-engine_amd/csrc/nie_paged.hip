@@ -843,7 +843,8 @@ struct DecodeArgs {
   int64_t table_stride;
   const int32_t* seq_lens;
   int64_t batch;
-  int32_t tiles_per_split;  // 16-key tiles per work item
+  int32_t tiles_per_split;  // 16-key tiles per work item; 0: derived on the device from the lengths
+  int32_t split_slots;      // with tiles_per_split 0: workgroups the device plan aims to fill
   float scale;
   void* out;
   int64_t o_sb, o_sh;
@@ -876,14 +877,81 @@ struct DecodeItems {
   int32_t seq_first[kMaxDecodeSeqs];
 };
 
-__device__ __forceinline__ int64_t decode_splits_of(const DecodeArgs& a, int64_t b) {
-  const int64_t len = a.seq_lens[b];
-  return len > 0 ? cdiv(cdiv(len, kTileKeys), a.tiles_per_split) : (int64_t)0;
+// Split length of a call planned on the device: the smallest number of
+// 16-key tiles per work item (within [kDecodeMinTilesPerSplit,
+// kDecodeMaxTilesPerSplit]) whose items fit `slots` workgroups in one round.
+// With `tiles` = sum over the sequences of ceil(len / 16), a call then has
+// at most tiles / tps + batch <= slots - 1 items unless the upper clamp binds.
+constexpr int64_t kDecodeMinTilesPerSplit = 4;
+constexpr int64_t kDecodeMaxTilesPerSplit = 2 * kWave;  // the per-split block-table window
+
+__host__ __device__ inline int64_t decode_device_tps(int64_t tiles, int64_t batch, int64_t slots) {
+  const int64_t room = slots - batch - 1;
+  int64_t tps = room > 0 ? cdiv(tiles, room) : kDecodeMaxTilesPerSplit;
+  tps = tps < kDecodeMinTilesPerSplit ? kDecodeMinTilesPerSplit : tps;
+  return tps > kDecodeMaxTilesPerSplit ? kDecodeMaxTilesPerSplit : tps;
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t x) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// The split length of a decode call: the host's, or (tiles_per_split 0) the
+// device plan's from the lengths themselves; wave-uniform.  first_len gets
+// this lane's length of the first 64 sequences (those every caller reads).
+__device__ __forceinline__ int64_t decode_call_tps(const DecodeArgs& a, int* first_len) {
+  const int lane = lane_id();
+  *first_len = lane < a.batch ? a.seq_lens[lane] : 0;
+  if (a.tiles_per_split > 0) return a.tiles_per_split;
+  int64_t tiles = *first_len > 0 ? cdiv((int64_t)*first_len, (int64_t)kTileKeys) : 0;
+  for (int64_t b = kWave + lane; b < a.batch; b += kWave) {
+    const int64_t len = a.seq_lens[b];
+    tiles += len > 0 ? cdiv(len, (int64_t)kTileKeys) : 0;
+  }
+  return uniform64(decode_device_tps(wave_sum64(tiles), a.batch, a.split_slots));
+}
+
+// Items of sequence b of a call with split length tps (first_len: the
+// calling lane's length when b is that lane's sequence among the first 64).
+__device__ __forceinline__ int64_t decode_splits_of(const DecodeArgs& a, int64_t b, int64_t tps, int first_len) {
+  const int64_t len = b == lane_id() ? first_len : a.seq_lens[b];
+  return len > 0 ? cdiv(cdiv(len, (int64_t)kTileKeys), tps) : (int64_t)0;
 }
 
 // s_waitcnt immediate that waits until at most `n` vector-memory operations
 // are outstanding and leaves the export / LGKM counters alone (gfx9 encoding).
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+// Waits until at most `later` groups of kOps vector-memory operations are
+// outstanding: the DMA ops of the tiles (or key steps) a ring pipeline has
+// issued after the one about to be read.  `later` is wave-uniform and at
+// most kMaxLater; the ring issues only tiles that exist, so near the end of
+// an item fewer groups are in flight and the wait tightens with them.
+template <int kOps, int kMaxLater>
+__device__ __forceinline__ void wait_dma_groups(int later) {
+  static_assert(kMaxLater >= 0 && kMaxLater <= 3 && kMaxLater * kOps < 64, "vmcnt immediate range");
+  if constexpr (kMaxLater >= 3) {
+    if (later >= 3) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kOps));
+      return;
+    }
+  }
+  if constexpr (kMaxLater >= 2) {
+    if (later == 2) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kOps));
+      return;
+    }
+  }
+  if constexpr (kMaxLater >= 1) {
+    if (later == 1) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kOps));
+      return;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+}
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -1633,7 +1701,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   const int g = lane >> 4;
   const int row = lane & 15;
 
-  int64_t b, split, first_item, nsplit;
+  int64_t b, split, first_item, nsplit, tps;
   int seq_len;
   if (items.count > 0) {
     if ((int)blockIdx.x >= items.count) return;  // uniform over the workgroup
@@ -1642,21 +1710,27 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     split = it & 0xffffu;
     seq_len = items.seq_len[b];
     first_item = items.seq_first[b];
-    nsplit = cdiv(cdiv((int64_t)seq_len, (int64_t)kTileKeys), (int64_t)a.tiles_per_split);
+    tps = a.tiles_per_split;
+    nsplit = cdiv(cdiv((int64_t)seq_len, (int64_t)kTileKeys), tps);
   } else {
-    locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s); },
+    // the lengths are read once: the split length (planned on the device
+    // when the host sent none) and the item's sequence come out of them
+    int first_len;
+    tps = decode_call_tps(a, &first_len);
+    locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s, tps, first_len); },
                 &b, &split, &first_item, &nsplit);
     if (b < 0) return;  // uniform over the workgroup
     seq_len = a.seq_lens[b];
   }
   seq_len = __builtin_amdgcn_readfirstlane(seq_len);
+  const int tiles_per_split = (int)tps;
   const int h0 = (int)blockIdx.y * kHeads;  // first KV head of the group
   const int h = h0 + wave;
 
   const int32_t* table = a.tables + b * a.table_stride;
   const int tlen = (int)a.table_stride;
-  const int key_begin = (int)split * a.tiles_per_split * kTileKeys;
-  const int key_end = min(key_begin + a.tiles_per_split * kTileKeys, seq_len);
+  const int key_begin = (int)split * tiles_per_split * kTileKeys;
+  const int key_end = min(key_begin + tiles_per_split * kTileKeys, seq_len);
   const int last = key_end - 1;
 
   const T* kc = reinterpret_cast<const T*>(a.k_cache) + h0 * D;
@@ -1812,10 +1886,13 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   };
 
   const int ntiles = (key_end - key_begin + kTileKeys - 1) / kTileKeys;
-  const int last_key0 = key_begin + (ntiles - 1) * kTileKeys;
   constexpr int kAhead = kStages - 1;
+  // only tiles the split has are fetched: a tail shorter than the ring
+  // leaves stages unused instead of re-reading its last tile
 #pragma unroll
-  for (int j = 0; j < kAhead; ++j) issue(j, min(key_begin + j * kTileKeys, last_key0));
+  for (int j = 0; j < kAhead; ++j) {
+    if (j < ntiles) issue(j, key_begin + j * kTileKeys);
+  }
   if (rope) {
     // rotate q (vector j pairs with vector j + kVec/2: dims i and i + D/2)
     // while the first tiles are in flight
@@ -1846,13 +1923,15 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     for (int j = 0; j < kStages; ++j) {
       const int tt = t + j;
       if (tt >= ntiles) break;  // uniform over the workgroup
-      // this wave's ops for tile tt are done once at most the kAhead-1 later
-      // tiles' ops are outstanding; the barrier extends that to every wave
-      // and guarantees that every wave has finished reading tile tt-1
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm((kAhead - 1) * kOwnOps));
+      // this wave's ops for tile tt are done once at most the ops of the
+      // tiles issued after it (min(kAhead - 1, ntiles - 1 - tt) of them) are
+      // outstanding; the barrier extends that to every wave and guarantees
+      // that every wave has finished reading tile tt-1, whose stage the next
+      // fetch reuses
+      wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, ntiles - 1 - tt));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      issue((j + kAhead) % kStages, min(key_begin + (tt + kAhead) * kTileKeys, last_key0));
+      if (tt + kAhead < ntiles) issue((j + kAhead) % kStages, key_begin + (tt + kAhead) * kTileKeys);
       __builtin_amdgcn_sched_barrier(0);
       if (appender && tt == ntiles - 1) {
         const int pos = seq_len - 1;
@@ -1893,8 +1972,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     }
   }
 
-  // Drain the redundant prefetches issued past the last tile before this
-  // workgroup's LDS can be handed to another one.
+  // every fetch has been waited for (the last tile's wait is vmcnt(0))
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   if (carry) *reinterpret_cast<v4u*>(new_dst) = new_chunk;
   const float lsum = sum_over_groups(st.lsum);
@@ -1937,8 +2015,10 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
     nsplit = cdiv(cdiv((int64_t)items.seq_len[b], (int64_t)kTileKeys), (int64_t)a.tiles_per_split);
     first = items.seq_first[b];
   } else {
-    nsplit = decode_splits_of(a, b);
-    for (int64_t s = lane_id(); s < b; s += kWave) first += decode_splits_of(a, s);
+    int first_len;
+    const int64_t tps = decode_call_tps(a, &first_len);
+    nsplit = decode_splits_of(a, b, tps, first_len);
+    for (int64_t s = lane_id(); s < b; s += kWave) first += decode_splits_of(a, s, tps, first_len);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
   }
@@ -1981,8 +2061,7 @@ int64_t device_cus() {
   return n;
 }
 
-constexpr int64_t kDecodeMinTilesPerSplit = 4;
-constexpr int64_t kDecodeMaxTilesPerSplit = kTableWindow;
+static_assert(kDecodeMaxTilesPerSplit == kTableWindow, "a split's blocks fit the block-table window");
 constexpr int64_t kDecodeFixedTiles = 4;
 constexpr int64_t kDecodeMaxRounds = 8;
 
@@ -2004,9 +2083,10 @@ int64_t decode_tiles_override() {
 }
 
 struct DecodePlan {
-  int heads = 1;     // KV heads per workgroup (one wave each)
-  int resident = 1;  // workgroups resident on one CU
-  int64_t tps = kDecodeMinTilesPerSplit;
+  int heads = 1;      // KV heads per workgroup (one wave each)
+  int resident = 1;   // workgroups resident on one CU
+  int64_t slots = 1;  // workgroups of one round: CUs x resident / head groups
+  int64_t tps = 0;    // 16-key tiles per split; 0: chosen on the device (decode_device_tps)
   int64_t items = 0;  // grid.x: an upper bound on the number of work items
 };
 
@@ -2572,25 +2652,30 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 
   const int nsteps = (tile_end - tile_begin + kSub - 1) / kSub;
   constexpr int kAhead = kStages - 1;
+  // only steps the item has are fetched
 #pragma unroll
-  for (int j = 0; j < kAhead; ++j) issue(j, (tile_begin + j * kSub) * kTileKeys);
+  for (int j = 0; j < kAhead; ++j) {
+    if (j < nsteps) issue(j, (tile_begin + j * kSub) * kTileKeys);
+  }
   for (int s0 = 0; s0 < nsteps; s0 += kStages) {
 #pragma unroll
     for (int j = 0; j < kStages; ++j) {
       const int s = s0 + j;
       if (s >= nsteps) break;  // uniform over the workgroup
-      // this wave's ops for step s are done once at most the kAhead-1 later
-      // steps' ops are outstanding; the barrier extends that to every wave
-      // and guarantees that every wave has finished reading step s-1
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm((kAhead - 1) * kOwnOps));
+      // this wave's ops for step s are done once at most the ops of the
+      // steps issued after it (min(kAhead - 1, nsteps - 1 - s)) are
+      // outstanding; the barrier extends that to every wave and guarantees
+      // that every wave has finished reading step s-1, whose stage the next
+      // fetch reuses
+      wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1 - s));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
+      if (s + kAhead < nsteps) issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
       __builtin_amdgcn_sched_barrier(0);
       consume(j, (tile_begin + s * kSub) * kTileKeys);
     }
   }
-  // drain the redundant prefetches before the LDS is handed to another workgroup
+  // every fetch has been waited for (the last step's wait is vmcnt(0))
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 
 #pragma unroll
@@ -3045,6 +3130,13 @@ void launch_decode_u(const DecodeArgs& a, const DecodePlan& p, const DecodeItems
   }
 }
 
+// Without host copies of the lengths the split length is chosen on the
+// device, from the lengths themselves (decode_device_tps: the smallest that
+// fits one round of `slots` workgroups), so the launch needs no host
+// knowledge of them beyond an upper bound on their sum: the grid and the
+// workspace cover at most slots - 1 items, or tiles / cap + batch + 1 when
+// the split length reaches its cap.  A captured decode step replays with
+// the split length its lengths of the moment call for.
 template <typename T, int D>
 DecodePlan plan_decode_t(int64_t kv_heads, bool uniform, int64_t batch, int64_t total_seq_len) {
   DecodePlan p;
@@ -3052,25 +3144,15 @@ DecodePlan plan_decode_t(int64_t kv_heads, bool uniform, int64_t batch, int64_t 
   p.resident = uniform ? decode_resident_u<T, D, true>(p.heads) : decode_resident_u<T, D, false>(p.heads);
   const int64_t groups = kv_heads / p.heads;
   const int64_t cus = device_cus();
-  const int64_t slots = (cus * p.resident) / groups > 0 ? (cus * p.resident) / groups : 1;
-  const int64_t tiles = cdiv(total_seq_len, kTileKeys) + batch;  // >= sum_b ceil(len_b / 16)
-  p.tps = kDecodeMaxTilesPerSplit;
-  int64_t best = -1;
-  for (int64_t r = 1; r <= kDecodeMaxRounds; ++r) {
-    const int64_t room = r * slots - batch - 1;  // items <= tiles / tps + batch + 1
-    if (room <= 0) continue;
-    int64_t tps = cdiv(tiles, room);
-    tps = tps < kDecodeMinTilesPerSplit ? kDecodeMinTilesPerSplit : tps;
-    if (tps > kDecodeMaxTilesPerSplit) continue;
-    const int64_t cost = r * (kDecodeFixedTiles + tps);
-    if (best < 0 || cost < best) {
-      best = cost;
-      p.tps = tps;
-    }
-  }
+  p.slots = (cus * p.resident) / groups > 0 ? (cus * p.resident) / groups : 1;
+  p.tps = 0;
+  const int64_t capped = decode_max_items(batch, total_seq_len, kDecodeMaxTilesPerSplit);
+  p.items = capped > p.slots ? capped : p.slots;
   const int64_t forced = decode_tiles_override();
-  if (forced > 0) p.tps = forced < kDecodeMaxTilesPerSplit ? forced : kDecodeMaxTilesPerSplit;
-  p.items = decode_max_items(batch, total_seq_len, p.tps);
+  if (forced > 0) {
+    p.tps = forced < kDecodeMaxTilesPerSplit ? forced : kDecodeMaxTilesPerSplit;
+    p.items = decode_max_items(batch, total_seq_len, p.tps);
+  }
   return p;
 }
 
@@ -3085,10 +3167,9 @@ int64_t decode_items_exact(const int32_t* lens, int64_t batch, int64_t tps) {
 // smallest split length whose exact item count fits r rounds (the item count
 // only falls as the split length grows), then the r with the lowest
 // r * (kDecodeFixedTiles + tiles per split), as in plan_decode_t.
-DecodePlan plan_decode_exact(DecodePlan p, int64_t kv_heads, const int32_t* lens, int64_t batch) {
-  const int64_t groups = kv_heads / p.heads;
-  const int64_t cus = device_cus();
-  const int64_t slots = (cus * p.resident) / groups > 0 ? (cus * p.resident) / groups : 1;
+DecodePlan plan_decode_exact(DecodePlan p, const int32_t* lens, int64_t batch) {
+  const int64_t slots = p.slots;
+  p.tps = kDecodeMaxTilesPerSplit;
   int64_t best = -1;
   for (int64_t r = 1; r <= kDecodeMaxRounds; ++r) {
     if (decode_items_exact(lens, batch, kDecodeMaxTilesPerSplit) > r * slots) continue;
@@ -3122,7 +3203,7 @@ DecodePlan plan_decode(int dtype, int64_t head_dim, int64_t kv_heads, int64_t bl
     p = head_dim == 64 ? plan_decode_t<float, 64>(kv_heads, uniform, batch, total_seq_len)
                        : plan_decode_t<float, 128>(kv_heads, uniform, batch, total_seq_len);
   }
-  return host_lens != nullptr ? plan_decode_exact(p, kv_heads, host_lens, batch) : p;
+  return host_lens != nullptr ? plan_decode_exact(p, host_lens, batch) : p;
 }
 
 // The work-item table of a host-planned decode call (count 0 when the call
@@ -3680,9 +3761,9 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
     }
   }
   const DecodePlan plan = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
-  const int64_t tps = plan.tps;
+  const int64_t tps = plan.tps;  // 0: chosen on the device, at least kDecodeMinTilesPerSplit
   const int64_t items = plan.items;
-  const bool may_split = cdiv(max_seq_len, kTileKeys) > tps;
+  const bool may_split = cdiv(max_seq_len, kTileKeys) > (tps > 0 ? tps : kDecodeMinTilesPerSplit);
   const int64_t need = items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
   if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     if (static_scratch) {
@@ -3709,6 +3790,7 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   a.seq_lens = seq_lens;
   a.batch = batch;
   a.tiles_per_split = (int32_t)tps;
+  a.split_slots = (int32_t)plan.slots;
   a.scale = scale;
   a.out = out;
   a.o_sb = out_stride_b;
