@@ -178,6 +178,19 @@ __device__ __forceinline__ float max_over_groups(float x) {
   return score_max(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// The dispatcher hands workgroup i of a launch to XCD i % kXcds (round robin
+// over MI355X's eight XCDs, each with its own L2).  xcd_logical maps a 1-D
+// workgroup index to a logical index so that each XCD receives one contiguous
+// range of [0, n): workgroups that share inputs (the items of one KV head)
+// then share an L2.  Only placement depends on it, never correctness.
+constexpr int64_t kXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_logical(int64_t i, int64_t n) {
+  const int64_t x = i % kXcds, j = i / kXcds;
+  const int64_t q = n / kXcds, r = n % kXcds;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + j;
+}
+
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
@@ -2130,6 +2143,8 @@ struct PrefillArgs {
   float* ws_o;       // (ws_items, kv_heads, rows_per_item, head_dim)
   float* ws_ml;      // (ws_items, kv_heads, rows_per_item, 2)
   int64_t ws_items;  // item slots in the workspace
+  int32_t grid_items;   // prefill launch: items per KV head (1-D grid of grid_items * kv_heads)
+  int32_t merge_tiles;  // merge launch: query tiles per KV head
 };
 
 // Key tiles visible to query tile qt of request r (its last row's position + 1).
@@ -2377,7 +2392,10 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   const int row = lane & 15;
   const int tpt = a.tokens_per_tile;
   const int S = a.tiles_per_split;
-  const int h = (int)blockIdx.y;
+  // (item, KV head) of this workgroup, head-major over the XCDs
+  const int64_t logical = xcd_logical(blockIdx.x, (int64_t)a.grid_items * a.geom.kv_heads);
+  const int h = (int)(logical / a.grid_items);
+  const int wg_item = (int)(logical % a.grid_items);
 
   // This workgroup's item: request r, query tile from token t0, key tiles
   // [tile_begin, tile_cap), and the workspace slot of its partial (-1: the
@@ -2385,9 +2403,9 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   int64_t r, q_begin, slot;
   int q_len, ctx, t0, tile_begin, tile_cap;
   if (sc.count > 0) {
-    if ((int)blockIdx.x >= sc.count) return;  // uniform over the workgroup
-    const int k = sc.item_tile[blockIdx.x];
-    const int piece = sc.item_piece[blockIdx.x];
+    if (wg_item >= sc.count) return;  // uniform over the workgroup
+    const int k = sc.item_tile[wg_item];
+    const int piece = sc.item_piece[wg_item];
     r = sc.req[k];
     q_begin = sc.q_begin[k];
     q_len = sc.q_len[k];
@@ -2396,7 +2414,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     tile_begin = piece * S;
     slot = sc.nsplit[k] == 1 ? -1 : (int64_t)sc.first_item[k] + piece;
   } else {
-    const PrefillItem pit = prefill_locate(a, (int64_t)blockIdx.x);
+    const PrefillItem pit = prefill_locate(a, (int64_t)wg_item);
     if (pit.r < 0) return;  // uniform over the workgroup
     // (query tile, split) of this item; the loop is wave-uniform
     int qt = 0, split = (int)pit.local, nsplit = 0;
@@ -2746,11 +2764,17 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
   constexpr int kChunkPasses = D / 64;  // 4-dim chunks per lane
   constexpr int kBatch = 64 / (3 * kChunkPasses);  // splits per round trip (register budget)
   const int tpt = a.tokens_per_tile;
-  const int h = (int)blockIdx.y;
+  // (query tile, KV head, row group) of this workgroup, head-major over the
+  // XCDs like the prefill items whose partials it reads
+  constexpr int kGroups = kRows / kPrefillMergeRows;
+  const int64_t logical = xcd_logical(blockIdx.x, (int64_t)a.merge_tiles * a.geom.kv_heads * kGroups);
+  const int zg = (int)(logical % kGroups);
+  const int tile = (int)((logical / kGroups) % a.merge_tiles);
+  const int h = (int)(logical / kGroups / a.merge_tiles);
   int64_t first, row0;
   int nsplit, tokens;
   if (jobs.count > 0) {
-    const int j = (int)blockIdx.x;
+    const int j = tile;
     first = jobs.first_item[j];
     row0 = jobs.row0[j];
     nsplit = jobs.nsplit_tokens[j] >> 16;
@@ -2758,7 +2782,7 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
   } else {
     const int S = a.tiles_per_split;
     int64_t r, qt64, first_q, count_q;
-    locate_item((int64_t)blockIdx.x, a.num_seqs,
+    locate_item((int64_t)tile, a.num_seqs,
                 [&](int64_t b) { return (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + tpt - 1) / tpt; }, &r, &qt64,
                 &first_q, &count_q);
     if (r < 0) return;  // uniform over the workgroup
@@ -2777,7 +2801,7 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
   const int lane = lane_id();
   const int wave = (int)(threadIdx.x / kWave);
   const int chunk = lane & 15;
-  const int rr = (int)blockIdx.z * kPrefillMergeRows + wave * 4 + (lane >> 4);  // row within the item
+  const int rr = zg * kPrefillMergeRows + wave * 4 + (lane >> 4);  // row within the item
   const int tpb = 16 / a.group;
   const int tq = (rr / 16) * tpb + (rr % 16) / a.group;  // token within the tile
   const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;  // rows between consecutive items
@@ -3246,7 +3270,7 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& 
 
 template <typename T, int D, int NB, bool P2>
 void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc, hipStream_t stream) {
-  const dim3 grid((unsigned)p.items, (unsigned)a.geom.kv_heads);
+  const dim3 grid((unsigned)(p.items * a.geom.kv_heads));
   if (uniform_tiles(a.geom)) {
     hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a,
                        sc);
@@ -3272,9 +3296,10 @@ void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const Prefill
     launch_prefill_kernel<T, D, NB, false>(a, p, sc, stream);
   }
   if (merge) {
-    const unsigned tiles = (unsigned)(jobs.count > 0 ? jobs.count : p.qtiles);
-    const dim3 grid(tiles, (unsigned)a.geom.kv_heads, (unsigned)(prefill_rows_per_item<NB>() / kPrefillMergeRows));
-    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(kPrefillMergeWaves * kWave), 0, stream, a, jobs);
+    PrefillArgs m = a;
+    m.merge_tiles = (int32_t)(jobs.count > 0 ? jobs.count : p.qtiles);
+    const dim3 grid((unsigned)(m.merge_tiles * a.geom.kv_heads * (prefill_rows_per_item<NB>() / kPrefillMergeRows)));
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(kPrefillMergeWaves * kWave), 0, stream, m, jobs);
   }
 }
 
@@ -4012,7 +4037,10 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   const int group = (int)(q_heads / kv_heads);
   const PrefillPlan plan = plan_prefill(group, kv_heads, num_seqs, total_query_tokens, max_seq_len,
                                         host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr);
-  if (plan.items > 0x7fffffffLL || plan.qtiles > 0x7fffffffLL || total_query_tokens > 0x7fffffffLL) {
+  // 1-D grids: items x heads prefill workgroups, tiles x heads x row groups merge workgroups
+  if (plan.items * kv_heads > 0xffffffffLL / (kPrefillWaves * kWave) ||
+      plan.qtiles * kv_heads * (plan.rows / kPrefillMergeRows) > 0xffffffffLL / (kPrefillMergeWaves * kWave) ||
+      total_query_tokens > 0x7fffffffLL) {
     return fail(NIE_EINVAL, "grid too large");
   }
   if (plan.items == 0) return NIE_OK;
@@ -4035,6 +4063,8 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   a.group = group;
   a.tokens_per_tile = plan.tokens_per_tile;
   a.tiles_per_split = (int32_t)plan.tps;
+  a.grid_items = (int32_t)plan.items;
+  a.merge_tiles = 0;
   a.tables = block_tables;
   a.table_stride = table_stride;
   a.scale = scale;

@@ -168,6 +168,8 @@ def run_lockstep(model, prompts, cache_factory, *, max_new_tokens: int, max_batc
         torch.cuda.synchronize(device)
         report.product_seconds += time.perf_counter() - t0
         report.steps += 1
+        if report.steps % 50 == 0:
+            print(f"lockstep: {report.steps} steps, {len(report.rows)} sampled rows", flush=True)
         plan = sched.last_plan
         for ref_model, ref_cache in paths.values():  # mirror the product's releases
             for sid in list(ref_cache._block_tables):
