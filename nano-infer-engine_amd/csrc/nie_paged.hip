@@ -2357,6 +2357,27 @@ __device__ __forceinline__ void ring_read_tr_n(v2u (&r)[N], const uint32_t (&add
   }
 }
 
+// LDS reads of the ring at immediate offsets: read i (of N) is at
+// base[i % kBases] + (i / kBases) * kStride, so a step's reads need kBases
+// address registers.  Waited for by the caller (lgkmcnt), like ring_read_b128_n.
+template <int N, int kBases, int kStride, int I = 0>
+__device__ __forceinline__ void ring_read_at(v4u* r, const uint32_t* base) {
+  if constexpr (I < N) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r[I]) : "v"(base[I % kBases]), "i"((I / kBases) * kStride));
+    ring_read_at<N, kBases, kStride, I + 1>(r, base);
+  }
+}
+
+template <int N, int kBases, int kStride, int I = 0>
+__device__ __forceinline__ void ring_read_tr_at(v2u* r, const uint32_t* base) {
+  if constexpr (I < N) {
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                 : "=v"(r[I])
+                 : "v"(base[I % kBases]), "i"((I / kBases) * kStride));
+    ring_read_tr_at<N, kBases, kStride, I + 1>(r, base);
+  }
+}
+
 // One workgroup = one (request, query tile, key split) for one KV head.
 // Wave w owns kRowBlocks MFMA row blocks of 16 query rows (16/G consecutive
 // tokens x the G query heads of the KV head each).  The head's K and V rows
@@ -2543,23 +2564,78 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   // exp2 multiplier of the scores (see softmax_step)
   const float exp_c = kPow2Scale ? a.scale * kLog2e : kLog2e;
 
-  auto consume = [&](int slot, int key0) {
-    const unsigned char* stage = &ring[slot][0];
-    // every key of the step is visible to every row of this wave
-    const bool full = key0 + kSub * kTileKeys - 1 <= min(block_first[0], last);
-    v4f p[kRowBlocks][kSub];
-    if constexpr (Elt<T>::kIsBf16) {
-      const uint32_t sb = lds_off(stage);
-      // K slices of the step's tiles, one wait
-      constexpr int kK = kSub * F::kVec;
-      uint32_t ka[kK];
-      v4u kr[kK];
+  // Causal boundary or item end inside the step starting at key0: scores of
+  // keys a row may not see become -inf (key key0 + 16t + 4g + i is visible
+  // iff 16t + i <= lim).  With a false result every key of the step is
+  // visible to every row of this wave.
+  auto step_full = [&](int key0) { return key0 + kSub * kTileKeys - 1 <= min(block_first[0], last); };
+  auto mask_step = [&](v4f (&p)[kRowBlocks][kSub], int key0) {
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) {
+      const int lim = min(q_pos[nb], last) - (key0 + 4 * g);
 #pragma unroll
       for (int t = 0; t < kSub; ++t) {
 #pragma unroll
-        for (int j = 0; j < F::kVec; ++j) ka[t * F::kVec + j] = sb + t * kTileStride + koff[j];
+        for (int i = 0; i < 4; ++i) p[nb][t][i] = (t * kTileKeys + i <= lim) ? p[nb][t][i] : kNegInf;
       }
-      ring_read_b128_n<kK>(kr, ka);
+    }
+  };
+
+  const int nsteps = (tile_end - tile_begin + kSub - 1) / kSub;
+  constexpr int kAhead = kStages - 1;
+  // only steps the item has are fetched
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) {
+    if (j < nsteps) issue(j, (tile_begin + j * kSub) * kTileKeys);
+  }
+
+  if constexpr (Elt<T>::kIsBf16) {
+    // Software-pipelined steps.  Iteration s runs the softmax of step s on
+    // scores whose QK MFMAs were issued in iteration s-1, then issues the QK
+    // MFMAs of step s+1 and the P.V MFMAs of step s, so no instruction waits
+    // on an MFMA issued just before it, and a second wave on the SIMD fills
+    // the MFMA pipe while this one runs its softmax.  The row sums of P come
+    // from an MFMA with an all-ones A operand (the same bf16 P the P.V MFMAs
+    // consume), so the softmax has no per-score additions.  LDS reads use
+    // immediate offsets from two base addresses per stage.
+    constexpr int kKR = kSub * F::kVec;  // K reads per step
+    constexpr int kVT = kSub * (D / 16);  // V^T reads per step
+    static_assert(kKR % 4 == 0 && kVT % 4 == 0, "reads are waited for in groups of four");
+    const uint32_t ring0 = lds_off(&ring[0][0]);
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, v4u{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+    v4f rowsum[kRowBlocks];
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) rowsum[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4u kr[kKR];
+    v2u vt[kVT];
+    v4f sacc[kRowBlocks][kSub];
+
+    auto read_k = [&](int slot) {
+      const uint32_t sb = ring0 + slot * kStageBytes;
+      uint32_t base[F::kVec];
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) base[j] = sb + koff[j];
+      ring_read_at<kKR, F::kVec, kTileStride>(kr, base);
+    };
+    auto read_vt = [&](int slot) {
+      const uint32_t sb = ring0 + slot * kStageBytes;
+      uint32_t base[D / 16];
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) base[c] = sb + vtr[c];
+      ring_read_tr_at<kVT, D / 16, kTileStride>(vt, base);
+    };
+    // every LDS read issued so far has landed (results pass through the asm)
+    auto wait_reads = [&]() {
+#pragma unroll
+      for (int j = 0; j < kKR; j += 4) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kr[j]), "+v"(kr[j + 1]), "+v"(kr[j + 2]), "+v"(kr[j + 3]));
+      }
+#pragma unroll
+      for (int j = 0; j < kVT; j += 4) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[j]), "+v"(vt[j + 1]), "+v"(vt[j + 2]), "+v"(vt[j + 3]));
+      }
+    };
+    auto qk = [&]() {
 #pragma unroll
       for (int nb = 0; nb < kRowBlocks; ++nb) {
 #pragma unroll
@@ -2570,10 +2646,129 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[t * F::kVec + j]),
                                                           __builtin_bit_cast(bf16x8_t, qf[nb].v[j]), acc, 0, 0, 0);
           }
-          p[nb][t] = acc;
+          sacc[nb][t] = acc;
         }
       }
-    } else {
+    };
+
+    // prologue: step 0 landed, its scores issued
+    wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1));
+    __builtin_amdgcn_s_barrier();
+    read_k(0);
+    wait_reads();
+    qk();
+
+    for (int s0 = 0; s0 < nsteps; s0 += kStages) {
+#pragma unroll
+      for (int j = 0; j < kStages; ++j) {
+        const int s = s0 + j;
+        if (s >= nsteps) break;  // uniform over the workgroup
+        const bool more = s + 1 < nsteps;
+        if (more) {
+          // step s+1 has landed for every wave (this wave's ops: at most
+          // those of the steps issued after it remain), and every wave has
+          // finished step s-1, whose stage the next fetch reuses
+          wait_dma_groups<kOwnOps, kAhead - 2>(min(kAhead - 2, nsteps - 2 - s));
+          __builtin_amdgcn_s_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+          if (s + kAhead < nsteps) issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
+          read_k((j + 1) % kStages);
+        }
+        read_vt(j);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // softmax of step s: scores in the reference's rounding (the q.k sum
+        // rounded to bf16, times the scale, rounded again; the second
+        // rounding is exact and the scale moves into exp_c when the scale is
+        // a power of two)
+        const int key0 = (tile_begin + s * kSub) * kTileKeys;
+        v4f p[kRowBlocks][kSub];
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int t = 0; t < kSub; ++t) {
+            if constexpr (kPow2Scale) {
+              p[nb][t] = round_bf16x4(sacc[nb][t]);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) p[nb][t][i] = scaled_score<T>(sacc[nb][t][i], a.scale);
+            }
+          }
+        }
+        if (!step_full(key0)) mask_step(p, key0);
+        // The reference point m of a row moves only when one of its scores
+        // is more than kRescaleLog2 (in log2 units) above it, or it had none
+        // yet; each lane tests its own 16 scores, and only then is the row
+        // maximum formed across the lane groups (see softmax_step).
+        float lmax[kRowBlocks];
+        bool grow = false;
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+          float m0 = score_max(score_max(p[nb][0][0], p[nb][0][1]), p[nb][0][2]);
+          float m1 = score_max(score_max(p[nb][0][3], p[nb][1][0]), p[nb][1][1]);
+          m0 = score_max(score_max(m0, p[nb][1][2]), p[nb][1][3]);
+          m1 = score_max(score_max(m1, p[nb][2][0]), p[nb][2][1]);
+          m0 = score_max(score_max(m0, p[nb][2][2]), p[nb][2][3]);
+          m1 = score_max(score_max(m1, p[nb][3][0]), p[nb][3][1]);
+          m0 = score_max(score_max(m0, p[nb][3][2]), p[nb][3][3]);
+          lmax[nb] = score_max(m0, m1);
+          grow |= lmax[nb] != kNegInf && (st[nb].m == kNegInf || (lmax[nb] - st[nb].m) * exp_c > kRescaleLog2);
+        }
+        if (__ballot(grow)) {
+#pragma unroll
+          for (int nb = 0; nb < kRowBlocks; ++nb) {
+            const float m_new = score_max(st[nb].m, max_over_groups(lmax[nb]));
+            // alpha = 0 for a row without a reference yet (its O and sum are 0)
+            const float alpha = st[nb].m == kNegInf ? 0.f : fast_exp2((st[nb].m - m_new) * exp_c);
+            rowsum[nb] *= alpha;
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) st[nb].o[c] *= alpha;
+            st[nb].m = m_new;
+          }
+        }
+        bf16x8_t pp[kRowBlocks][kSub / 2];
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+          // a row with nothing unmasked so far keeps m = -inf; 0 as the
+          // reference point makes its exponentials exact zeros, not NaN
+          const float nref = (st[nb].m == kNegInf) ? 0.f : -st[nb].m * exp_c;
+#pragma unroll
+          for (int t = 0; t < kSub; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[nb][t][i] = fast_exp2(fmaf(p[nb][t][i], exp_c, nref));
+          }
+#pragma unroll
+          for (int t = 0; t < kSub; t += 2) {
+            pp[nb][t / 2] = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
+                                        pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
+                                                    p[nb][t + 1][3]));
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        wait_reads();
+        if (more) qk();  // scores of step s+1
+        // O^T += V^T . P^T and the row sums, two 16-key tiles per MFMA
+#pragma unroll
+        for (int t = 0; t < kSub; t += 2) {
+#pragma unroll
+          for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+              const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
+                                              __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
+              st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp[nb][t / 2], st[nb].o[c], 0, 0, 0);
+            }
+            rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) st[nb].lsum = rowsum[nb][0];
+  } else {
+    auto consume = [&](int slot, int key0) {
+      const unsigned char* stage = &ring[slot][0];
+      v4f p[kRowBlocks][kSub];
       F kf[kSub];
 #pragma unroll
       for (int t = 0; t < kSub; ++t) {
@@ -2585,70 +2780,14 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 #pragma unroll
       for (int nb = 0; nb < kRowBlocks; ++nb) {
 #pragma unroll
-        for (int t = 0; t < kSub; ++t) p[nb][t] = qk_mfma<T, D>(kf[t], qf[nb]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // V^T operands of the step (bf16), read while the QK MFMAs run: tile t,
-    // dims 16c.. -> vt[t * D/16 + c]
-    constexpr int kVt = Elt<T>::kIsBf16 ? kSub * (D / 16) : 4;
-    v2u vt[kVt];
-    if constexpr (Elt<T>::kIsBf16) {
-      const uint32_t sb = lds_off(stage);
-      uint32_t va[kVt];
-#pragma unroll
-      for (int t = 0; t < kSub; ++t) {
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) va[t * (D / 16) + c] = sb + t * kTileStride + vtr[c];
-      }
-      ring_read_tr_n<kVt>(vt, va);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // scores in the reference's rounding: the q.k sum rounded to the storage
-    // dtype, times the scale, rounded again (the second rounding is exact,
-    // and the scale moves into exp_c, when the scale is a power of two)
-#pragma unroll
-    for (int nb = 0; nb < kRowBlocks; ++nb) {
-#pragma unroll
-      for (int t = 0; t < kSub; ++t) {
-        if constexpr (kPow2Scale) {
-          p[nb][t] = round_bf16x4(p[nb][t]);
-        } else {
+        for (int t = 0; t < kSub; ++t) {
+          p[nb][t] = qk_mfma<T, D>(kf[t], qf[nb]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) p[nb][t][i] = scaled_score<T>(p[nb][t][i], a.scale);
         }
       }
-    }
-    if (!full) {  // causal boundary or item end inside the step
-#pragma unroll
-      for (int nb = 0; nb < kRowBlocks; ++nb) {
-        // key key0 + 16t + 4g + i is visible iff 16t + i <= lim
-        const int lim = min(q_pos[nb], last) - (key0 + 4 * g);
-#pragma unroll
-        for (int t = 0; t < kSub; ++t) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) p[nb][t][i] = (t * kTileKeys + i <= lim) ? p[nb][t][i] : kNegInf;
-        }
-      }
-    }
-    softmax_step<D, kRowBlocks, kSub>(st, p, exp_c);
-    if constexpr (Elt<T>::kIsBf16) {
-#pragma unroll
-      for (int t = 0; t < kSub; t += 2) {
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-          const bf16x8_t pp = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
-                                          pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
-                                                      p[nb][t + 1][3]));
-#pragma unroll
-          for (int c = 0; c < D / 16; ++c) {
-            const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
-                                            __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
-            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp, st[nb].o[c], 0, 0, 0);
-          }
-        }
-      }
-    } else {
+      if (!step_full(key0)) mask_step(p, key0);
+      softmax_step<D, kRowBlocks, kSub>(st, p, exp_c);
 #pragma unroll
       for (int t = 0; t < kSub; ++t) {
 #pragma unroll
@@ -2665,40 +2804,34 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
           }
         }
       }
-    }
-  };
-
-  const int nsteps = (tile_end - tile_begin + kSub - 1) / kSub;
-  constexpr int kAhead = kStages - 1;
-  // only steps the item has are fetched
+    };
+    for (int s0 = 0; s0 < nsteps; s0 += kStages) {
 #pragma unroll
-  for (int j = 0; j < kAhead; ++j) {
-    if (j < nsteps) issue(j, (tile_begin + j * kSub) * kTileKeys);
-  }
-  for (int s0 = 0; s0 < nsteps; s0 += kStages) {
-#pragma unroll
-    for (int j = 0; j < kStages; ++j) {
-      const int s = s0 + j;
-      if (s >= nsteps) break;  // uniform over the workgroup
-      // this wave's ops for step s are done once at most the ops of the
-      // steps issued after it (min(kAhead - 1, nsteps - 1 - s)) are
-      // outstanding; the barrier extends that to every wave and guarantees
-      // that every wave has finished reading step s-1, whose stage the next
-      // fetch reuses
-      wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1 - s));
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      if (s + kAhead < nsteps) issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
-      __builtin_amdgcn_sched_barrier(0);
-      consume(j, (tile_begin + s * kSub) * kTileKeys);
+      for (int j = 0; j < kStages; ++j) {
+        const int s = s0 + j;
+        if (s >= nsteps) break;  // uniform over the workgroup
+        // this wave's ops for step s are done once at most the ops of the
+        // steps issued after it (min(kAhead - 1, nsteps - 1 - s)) are
+        // outstanding; the barrier extends that to every wave and guarantees
+        // that every wave has finished reading step s-1, whose stage the next
+        // fetch reuses
+        wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1 - s));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + kAhead < nsteps) issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(j, (tile_begin + s * kSub) * kTileKeys);
+      }
     }
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) st[nb].lsum = sum_over_groups(st[nb].lsum);
   }
   // every fetch has been waited for (the last step's wait is vmcnt(0))
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 
 #pragma unroll
   for (int nb = 0; nb < kRowBlocks; ++nb) {
-    const float lsum = sum_over_groups(st[nb].lsum);
+    const float lsum = st[nb].lsum;
     const int tq = t0 + (wave * kRowBlocks + nb) * tpb + row / a.group;
     if (tq >= t_end) continue;
     const int qh = h * a.group + row % a.group;
