@@ -10,7 +10,10 @@ length bucket) and replayed:
 
 * the step's inputs live in static device buffers: token IDs, block tables
   (width = bucket / block_size), context and sequence lengths, slot mapping
-  and positions; one host-to-device copy refreshes the metadata per step;
+  and positions; their pinned host staging persists with the capture, its
+  tables updated in place (:class:`~nano_infer_engine.paged_batch.TableMirror`:
+  only a sequence's new blocks, or a row that changed hands), and one
+  host-to-device copy per buffer refreshes the device side per step;
 * the decode launch inside the graph is planned for the bucket
   (:func:`~nano_infer_engine.paged_batch.decode_plan_bound`), exactly as the
   eager step plans it, so a replay computes the same values as the eager
@@ -31,7 +34,7 @@ import numpy as np
 import torch
 
 from nano_infer_engine import _native
-from nano_infer_engine.paged_batch import RaggedBatch, decode_plan_bound
+from nano_infer_engine.paged_batch import RaggedBatch, TableMirror, decode_plan_bound
 from nano_infer_engine.paged_cache import PagedKVCache
 
 
@@ -48,6 +51,7 @@ class _CapturedStep:
     copied: torch.cuda.Event  # recorded after the staging copies of the last step
     logits: torch.Tensor  # (B, vocab) output of the last replay
     next_ids: torch.Tensor  # (B,) int64 argmax of ``logits``
+    mirror: TableMirror  # the staged tables, updated in place from step to step
 
 
 class DecodeGraphRunner:
@@ -140,6 +144,7 @@ class DecodeGraphRunner:
             copied=torch.cuda.Event(),
             logits=logits,
             next_ids=next_ids,
+            mirror=TableMirror(),
         )
 
     # ------------------------------------------------------------------ step
@@ -185,11 +190,10 @@ class DecodeGraphRunner:
         ints = step.ints_host.numpy()
         longs = step.longs_host.numpy()
         tables = ints[: b * width].reshape(b, width)
-        tables[:] = 0
+        # only the table entries that changed since this capture's last
+        # replay are rewritten (a new block per sequence every block_size steps)
+        step.mirror.fill(tables, [cache._row(s) for s in sequence_ids])
         ctx = np.asarray(context, dtype=np.int64)
-        for r, s in enumerate(sequence_ids):
-            row = cache._table(s)[:width]
-            tables[r, : len(row)] = row
         ints[b * width : b * width + b] = ctx
         ints[b * width + b :] = ctx + 1
         longs[:b] = tables[np.arange(b), ctx // bs].astype(np.int64) * bs + ctx % bs

@@ -108,6 +108,103 @@ class RaggedBatch:
         return found
 
 
+class TableMirror:
+    """Block-table rows of consecutive steps' batches, maintained in place.
+
+    ``fill`` writes the tables of a batch into an (R, W) staging array that
+    it wrote the previous batch into as well.  Row r remembers which
+    sequence's table it holds and how many entries of it are written: a
+    sequence that kept its row only gets the blocks it gained since (at most
+    one per row and step in decoding), a row that changed hands is rewritten
+    and its stale tail zeroed.  A change of width or of staging memory
+    rewrites everything.  The reference builds these tables anew, as
+    tuples, in every layer (``layers/attention.py:258-261``).
+    """
+
+    def __init__(self) -> None:
+        self._owner: list = []  # per row: the BlockRow written there (None: unknown)
+        self._count: list[int] = []  # entries of it written
+        self._key: tuple = ()  # (staging address, width) the rows refer to
+        self.rewritten = 0  # entries written by the last fill (for tests and measurement)
+
+    def fill(self, view: np.ndarray, rows: list) -> None:
+        nrows, width = view.shape
+        key = (view.__array_interface__["data"][0], width)
+        if key != self._key:
+            view[:] = 0
+            self._owner, self._count, self._key = [], [], key
+        if len(self._owner) < nrows:
+            grow = nrows - len(self._owner)
+            self._owner.extend([None] * grow)
+            self._count.extend([width] * grow)  # unknown content: rewrite the whole row
+        written = 0
+        for r, row in enumerate(rows):
+            n = row.n if row.n < width else width
+            k = self._count[r]
+            if self._owner[r] is row and k <= n:
+                if n > k:
+                    view[r, k:n] = row.ids[k:n]
+                    written += n - k
+            else:
+                view[r, :n] = row.ids[:n]
+                if k > n:
+                    view[r, n:k] = 0
+                written += n
+                self._owner[r] = row
+            self._count[r] = n
+        self.rewritten = written
+
+
+class _Staging:
+    """Host staging of a cache's step metadata, reused from step to step:
+    int32 [tables (rows x width) | context lens (rows) | sequence lens
+    (rows)] and int64 [slots | positions | cu_seqlens].  Pinned when the
+    cache is on a GPU, so the two uploads are asynchronous; an event recorded
+    after them keeps the next step from rewriting the staging under a copy
+    still in flight."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.pinned = device.type == "cuda"
+        self.ints = np.zeros(0, dtype=np.int32)
+        self.longs = np.zeros(0, dtype=np.int64)
+        self._ints_t = self._longs_t = None
+        self.rows = self.width = 0
+        self.mirror = TableMirror()
+        self.uploaded = torch.cuda.Event() if self.pinned else None
+
+    def _buffer(self, size: int, dtype: torch.dtype) -> tuple[torch.Tensor, np.ndarray]:
+        t = torch.zeros(size, dtype=dtype, pin_memory=self.pinned)
+        return t, t.numpy()
+
+    def layout(self, rows: int, width: int, tokens: int) -> None:
+        if self.uploaded is not None:
+            self.uploaded.synchronize()
+        if rows > self.rows or width != self.width:
+            self.rows, self.width = max(rows, self.rows), width
+            self._ints_t, self.ints = self._buffer(self.rows * width + 2 * self.rows, torch.int32)
+        if 2 * tokens + rows + 1 > self.longs.shape[0]:
+            self._longs_t, self.longs = self._buffer(2 * max(2 * tokens + rows + 1, 64), torch.int64)
+
+    def upload(self, tokens: int, rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+        n_ints, n_longs = self.rows * self.width + 2 * self.rows, 2 * tokens + rows + 1
+        ints = torch.empty(n_ints, dtype=torch.int32, device=self.device)
+        longs = torch.empty(n_longs, dtype=torch.int64, device=self.device)
+        ints.copy_(self._ints_t[:n_ints], non_blocking=True)
+        longs.copy_(self._longs_t[:n_longs], non_blocking=True)
+        if self.uploaded is not None:
+            self.uploaded.record()
+        return ints, longs
+
+
+def _staging(cache: PagedKVCache) -> _Staging:
+    st = getattr(cache, "_step_staging", None)
+    if st is None:
+        st = _Staging(cache.keys.device)
+        cache._step_staging = st
+    return st
+
+
 def build_ragged_batch(
     cache: PagedKVCache,
     sequence_ids: tuple[str, ...],
@@ -117,59 +214,69 @@ def build_ragged_batch(
     """Metadata for appending ``query_lens[r]`` tokens to each sequence.
 
     Capacity must already be allocated (``ensure_capacity``).  Context lengths
-    default to the cached lengths.
+    default to the cached lengths.  The block tables go through the cache's
+    :class:`TableMirror`, so a step rewrites only the table entries that
+    changed since the previous one; the rest is vectorised over the batch.
     """
     if context_lens is None:
         context_lens = tuple(cache.get_sequence_length(s) for s in sequence_ids)
     bs = cache.block_size
-    for sequence_id, ctx, q in zip(sequence_ids, context_lens, query_lens):
-        # every new token must already be backed by a block (same error as a write)
-        cache._resolve_position(sequence_id, ctx + q - 1)
-    tables = [cache._table(s) for s in sequence_ids]
+    rows = [cache._row(s) for s in sequence_ids]
     num_requests = len(sequence_ids)
-    num_tokens = int(sum(query_lens))
+    ctx = np.asarray(context_lens, dtype=np.int64)
+    qlen = np.asarray(query_lens, dtype=np.int64)
+    last = ctx + qlen - 1
+    capacity = np.fromiter((row.n for row in rows), dtype=np.int64, count=num_requests) * bs
+    bad = np.flatnonzero((last >= capacity) | (last < 0))
+    if bad.size:
+        # every new token must already be backed by a block (same error as a write)
+        r = int(bad[0])
+        cache._resolve_position(sequence_ids[r], int(last[r]))
+    num_tokens = int(qlen.sum())
     decode_from = num_requests
     while decode_from > 0 and query_lens[decode_from - 1] == 1:
         decode_from -= 1
     decode_bound = 0
     if decode_from < num_requests:
-        decode_bound = decode_plan_bound(max(c + 1 for c in context_lens[decode_from:]))
+        decode_bound = decode_plan_bound(int(ctx[decode_from:].max()) + 1)
     # rows cover the decode plan's bound, as the decode launch requires
-    width = max(1, max(len(t) for t in tables), -(-decode_bound // bs))
+    width = max(1, max(row.n for row in rows), -(-decode_bound // bs))
 
-    ints = np.zeros(num_requests * width + 2 * num_requests, dtype=np.int32)
-    table_view = ints[: num_requests * width].reshape(num_requests, width)
-    longs = np.empty(2 * num_tokens + num_requests + 1, dtype=np.int64)
-    slots = longs[:num_tokens]
-    positions = longs[num_tokens : 2 * num_tokens]
-    cu = longs[2 * num_tokens :]
+    st = _staging(cache)
+    st.layout(num_requests, width, num_tokens)
+    table_view = st.ints[: st.rows * width].reshape(st.rows, width)[:num_requests]
+    st.mirror.fill(table_view, rows)
+    base = st.rows * width
+    st.ints[base : base + num_requests] = ctx
+    st.ints[base + st.rows : base + st.rows + num_requests] = ctx + qlen
+    slots = st.longs[:num_tokens]
+    positions = st.longs[num_tokens : 2 * num_tokens]
+    cu = st.longs[2 * num_tokens : 2 * num_tokens + num_requests + 1]
     cu[0] = 0
-    cursor = 0
-    for r, (table, ctx, q) in enumerate(zip(tables, context_lens, query_lens)):
-        table_view[r, : len(table)] = table
-        pos = np.arange(ctx, ctx + q, dtype=np.int64)
-        positions[cursor : cursor + q] = pos
-        slots[cursor : cursor + q] = table_view[r, pos // bs].astype(np.int64) * bs + pos % bs
-        cursor += q
-        cu[r + 1] = cursor
-    ints[num_requests * width : num_requests * width + num_requests] = context_lens
-    ints[num_requests * width + num_requests :] = np.asarray(context_lens) + np.asarray(query_lens)
+    np.cumsum(qlen, out=cu[1:])
+    if num_tokens == num_requests:  # one token per request: vectorised
+        positions[:] = ctx
+    else:
+        positions[:] = np.repeat(ctx - cu[:-1], qlen) + np.arange(num_tokens, dtype=np.int64)
+    owner = np.repeat(np.arange(num_requests), qlen)
+    slots[:] = table_view[owner, positions // bs].astype(np.int64) * bs + positions % bs
 
-    device = cache.keys.device
-    ints_t = torch.from_numpy(ints).to(device, non_blocking=True)
-    longs_t = torch.from_numpy(longs).to(device, non_blocking=True)
-
+    ints_t, longs_t = st.upload(num_tokens, num_requests)
+    tables_t, ctx_t, seq_t = ints_t.split([st.rows * width, st.rows, st.rows])
+    slots_t, positions_t, cu_t = longs_t.split([num_tokens, num_tokens, num_requests + 1])
+    if st.rows > num_requests:
+        ctx_t, seq_t = ctx_t[:num_requests], seq_t[:num_requests]
     return RaggedBatch(
         sequence_ids=tuple(sequence_ids),
         query_lens=tuple(query_lens),
         context_lens=tuple(context_lens),
         num_tokens=num_tokens,
-        block_tables=ints_t[: num_requests * width].view(num_requests, width),
-        context_lens_t=ints_t[num_requests * width : num_requests * width + num_requests],
-        seq_lens_t=ints_t[num_requests * width + num_requests :],
-        cu_seqlens=longs_t[2 * num_tokens :],
-        slot_mapping=longs_t[:num_tokens],
-        positions=longs_t[num_tokens : 2 * num_tokens],
+        block_tables=tables_t.view(st.rows, width)[:num_requests],
+        context_lens_t=ctx_t,
+        seq_lens_t=seq_t,
+        cu_seqlens=cu_t,
+        slot_mapping=slots_t,
+        positions=positions_t,
         decode_from=decode_from,
         decode_bound=decode_bound,
     )

@@ -39,6 +39,33 @@ def _check_positive_int(value: object, name: str) -> None:
         raise ValueError(f"{name} must be positive")
 
 
+class BlockRow:
+    """One sequence's block table: physical block IDs in logical order, kept
+    in an int32 array with spare capacity, so appending a block is amortised
+    O(1) and copying a row into a launch's table is a memcpy, not a
+    Python-list conversion.  ``ids[:n]`` are valid; the object lives as long
+    as the sequence does (a released and re-created ID gets a new one)."""
+
+    __slots__ = ("ids", "n")
+
+    def __init__(self, blocks: list[int]) -> None:
+        self.ids = np.empty(max(8, 2 * len(blocks)), dtype=np.int32)
+        self.ids[: len(blocks)] = blocks
+        self.n = len(blocks)
+
+    def extend(self, blocks: list[int]) -> None:
+        need = self.n + len(blocks)
+        if need > self.ids.shape[0]:
+            grown = np.empty(max(need, 2 * self.ids.shape[0]), dtype=np.int32)
+            grown[: self.n] = self.ids[: self.n]
+            self.ids = grown
+        self.ids[self.n : need] = blocks
+        self.n = need
+
+    def view(self) -> np.ndarray:
+        return self.ids[: self.n]
+
+
 @dataclass(frozen=True)
 class PagedKVTransfer:
     """Logical-block snapshot of one sequence, independent of physical IDs.
@@ -84,7 +111,7 @@ class PagedKVCache:
         self.head_dim = head_dim
 
         # sequence ID -> physical block IDs in logical order, and cached length
-        self._block_tables: dict[str, list[int]] = {}
+        self._block_tables: dict[str, BlockRow] = {}
         self._sequence_lengths: dict[str, int] = {}
 
         shape = (num_layers, num_blocks, block_size, kv_head_num, head_dim)
@@ -107,7 +134,7 @@ class PagedKVCache:
         _check_sequence_id(sequence_id)
         _check_positive_int(required_tokens, "required_tokens")
         table = self._block_tables.get(sequence_id)
-        have = 0 if table is None else len(table)
+        have = 0 if table is None else table.n
         missing = self.blocks_for(required_tokens) - have
         if missing <= 0:
             return
@@ -115,7 +142,7 @@ class PagedKVCache:
         # only once the allocation succeeded.
         new_blocks = self.allocator.allocate(missing)
         if table is None:
-            self._block_tables[sequence_id] = new_blocks
+            self._block_tables[sequence_id] = BlockRow(new_blocks)
             self._sequence_lengths[sequence_id] = 0
         else:
             table.extend(new_blocks)
@@ -135,13 +162,17 @@ class PagedKVCache:
     def get_block_table(self, sequence_id: str) -> tuple[int, ...]:
         """Immutable snapshot of a sequence's block table."""
         _check_sequence_id(sequence_id)
-        return tuple(self._block_tables[sequence_id])
+        return tuple(self._block_tables[sequence_id].view().tolist())
 
     def has_sequence(self, sequence_id: str) -> bool:
         return sequence_id in self._block_tables
 
-    def _table(self, sequence_id: str) -> list[int]:
-        """Live block table (no copy); KeyError if unknown."""
+    def _table(self, sequence_id: str) -> np.ndarray:
+        """Live block table (an int32 view, valid until the sequence grows); KeyError if unknown."""
+        return self._block_tables[sequence_id].view()
+
+    def _row(self, sequence_id: str) -> BlockRow:
+        """The sequence's table object; KeyError if unknown."""
         return self._block_tables[sequence_id]
 
     def _resolve_position(self, sequence_id: str, token_position: int) -> tuple[int, int]:
@@ -150,15 +181,16 @@ class PagedKVCache:
             raise TypeError("token_position must be an integer")
         if token_position < 0:
             raise ValueError("token_position must be non-negative")
-        table = self.get_block_table(sequence_id)
+        _check_sequence_id(sequence_id)
+        row = self._block_tables[sequence_id]
         logical, offset = divmod(token_position, self.block_size)
-        if logical >= len(table):
+        if logical >= row.n:
             raise IndexError("token position exceeds allocated capacity")
-        return table[logical], offset
+        return int(row.ids[logical]), offset
 
     def slots_for(self, sequence_id: str, start_position: int, token_count: int) -> np.ndarray:
         """Flat slots (phys * block_size + offset) of positions start .. start+count-1."""
-        table = np.asarray(self._block_tables[sequence_id], dtype=np.int64)
+        table = self._block_tables[sequence_id].view().astype(np.int64)
         positions = np.arange(start_position, start_position + token_count, dtype=np.int64)
         return table[positions // self.block_size] * self.block_size + positions % self.block_size
 
@@ -166,7 +198,7 @@ class PagedKVCache:
         """Return every block of a sequence to the allocator."""
         _check_sequence_id(sequence_id)
         blocks = self._block_tables[sequence_id]
-        self.allocator.free(blocks)
+        self.allocator.free(blocks.view().tolist())
         del self._block_tables[sequence_id]
         del self._sequence_lengths[sequence_id]
 
@@ -227,10 +259,10 @@ class PagedKVCache:
 
     def table_tensor(self, sequence_id: str, blocks: int | None = None) -> torch.Tensor:
         """Device int32 copy of (a prefix of) a sequence's block table."""
-        table = self._block_tables[sequence_id]
+        table = self._block_tables[sequence_id].view()
         if blocks is not None:
             table = table[:blocks]
-        return torch.tensor(table, dtype=torch.int32).to(self.keys.device, non_blocking=True)
+        return torch.from_numpy(table.copy()).to(self.keys.device, non_blocking=True)
 
     def export_sequence(self, sequence_id: str) -> PagedKVTransfer:
         """Snapshot of a sequence in logical block order (unused tail zeroed)."""

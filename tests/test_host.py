@@ -250,6 +250,76 @@ def test_ragged_batch_metadata_matches_closed_form():
         build_ragged_batch(c, ("d1",), (3,))
 
 
+def test_ragged_batch_metadata_over_changing_steps():
+    """Steps whose batches grow, shrink, reorder and replace sequences (with
+    prefill pieces and decode rows) reuse the cache's staging; every step's
+    metadata still equals the closed form of that step alone."""
+    rng = np.random.default_rng(7)
+    c = _cache(num_blocks=400, block_size=4)
+    live: dict[str, int] = {}
+    serial = 0
+    for step in range(60):
+        # retire and admit a few sequences
+        for sid in list(live):
+            if rng.random() < 0.15:
+                if c.has_sequence(sid):
+                    c.release(sid)
+                del live[sid]
+        while len(live) < 6 and rng.random() < 0.8:
+            live[f"s{serial}"] = 0
+            serial += 1
+        ids = list(live)
+        rng.shuffle(ids)
+        ids = tuple(ids[: int(rng.integers(1, len(ids) + 1))]) if ids else ()
+        if not ids:
+            continue
+        # prefill pieces first, then single-token rows
+        qlen = [int(rng.integers(2, 9)) if live[s] < 8 else 1 for s in ids]
+        order = sorted(range(len(ids)), key=lambda r: qlen[r] == 1)
+        ids = tuple(ids[r] for r in order)
+        qlen = tuple(qlen[r] for r in order)
+        for s, n in zip(ids, qlen):
+            c.ensure_capacity(s, live[s] + n)
+        batch = build_ragged_batch(c, ids, qlen)
+        ctx = [live[s] for s in ids]
+        tables = [c.get_block_table(s) for s in ids]
+        assert batch.slot_mapping.tolist() == slots.slot_mapping(tables, ctx, list(qlen), 4).tolist()
+        assert batch.positions.tolist() == [p for cx, n in zip(ctx, qlen) for p in range(cx, cx + n)]
+        assert batch.cu_seqlens.tolist() == np.concatenate([[0], np.cumsum(qlen)]).tolist()
+        assert batch.context_lens_t.tolist() == ctx
+        assert batch.seq_lens_t.tolist() == [cx + n for cx, n in zip(ctx, qlen)]
+        width = batch.block_tables.shape[1]
+        for r, t in enumerate(tables):
+            assert batch.block_tables[r].tolist() == list(t[:width]) + [0] * (width - min(len(t), width)), (step, r)
+        for s, n in zip(ids, qlen):
+            c.advance(s, n)
+            live[s] += n
+
+
+def test_table_mirror_rewrites_only_what_changed():
+    from nano_infer_engine.paged_batch import TableMirror
+
+    c = _cache(num_blocks=64, block_size=4)
+    for sid, n in (("a", 9), ("b", 4), ("c", 13)):
+        c.ensure_capacity(sid, n)
+    view = np.full((3, 8), -1, dtype=np.int32)
+    m = TableMirror()
+    rows = [c._row(s) for s in ("a", "b", "c")]
+    m.fill(view, rows)
+    assert m.rewritten == 3 + 1 + 4
+    assert view[0, :3].tolist() == list(c.get_block_table("a")) and view[0, 3:].tolist() == [0] * 5
+    m.fill(view, rows)  # nothing changed
+    assert m.rewritten == 0
+    c.ensure_capacity("b", 5)  # b gains one block
+    m.fill(view, rows)
+    assert m.rewritten == 1 and view[1, :2].tolist() == list(c.get_block_table("b"))
+    # another sequence takes row 2: the row is rewritten and its stale tail zeroed
+    c.ensure_capacity("d", 2)
+    m.fill(view, [rows[0], rows[1], c._row("d")])
+    assert m.rewritten == 1
+    assert view[2].tolist() == list(c.get_block_table("d")) + [0] * 7
+
+
 # ---------------------------------------------------------------------------
 # the C ABI library (loads and exports; no compute without a GPU)
 # ---------------------------------------------------------------------------
