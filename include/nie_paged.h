@@ -16,8 +16,13 @@
  *  - A "slot" is phys_block * block_size + offset_in_block
  *    (src/nano_infer_engine/paged_cache.py:240-262).
  *  - dtype is NIE_DTYPE_F32 or NIE_DTYPE_BF16; everything in one call shares it.
- *  - head_dim must be 64 or 128; q_heads must be a multiple of kv_heads with
- *    q_heads / kv_heads in {1, 2, 4, 8, 16}.  block_size may be any positive
+ *  - Attention shapes: q_heads a positive multiple of kv_heads and head_dim
+ *    in [1, 256].  head_dim 64 or 128 with q_heads / kv_heads in
+ *    {1, 2, 4, 8, 16} runs on the MFMA kernels, which need 16-byte aligned
+ *    q/out/new-row pointers and strides; every other shape runs on a generic
+ *    kernel (one wave per query row and head: the same results at a far
+ *    lower rate), which needs element alignment only and no workspace (its
+ *    *_workspace_bytes query returns 0).  block_size may be any positive
  *    value.
  *  - Block IDs read from block tables are clamped into [0, num_blocks) on the
  *    device, so a bad table cannot address memory outside the pool; callers
@@ -41,7 +46,7 @@ extern "C" {
 
 #define NIE_OK 0
 #define NIE_EINVAL (-1)       /* bad argument (null pointer, bad size, bad workspace) */
-#define NIE_EUNSUPPORTED (-2) /* dtype / head_dim / GQA group size not built */
+#define NIE_EUNSUPPORTED (-2) /* dtype or shape not built (e.g. head_dim > 256) */
 #define NIE_ELAUNCH (-3)      /* HIP reported an error at launch */
 
 #define NIE_DTYPE_F32 0
@@ -129,7 +134,7 @@ int nie_kv_copy_blocks(int dtype,
  * Rotate-half with every product and sum rounded to the storage dtype, so
  * the output is bit-identical to the reference's elementwise torch ops fed
  * the same sin/cos rows; the K/V writes are bit-exact copies of those rows.
- * head_dim must be 64 or 128.
+ * head_dim must be even (rotate-half splits it in two).
  * Replaces: the RoPE of q and k (src/nano_infer_engine/layers/rope.py:6-23,
  *           called at src/nano_infer_engine/layers/attention.py:238-239 and
  *           :375-376) followed by PagedKVCache.write of the new K/V

@@ -37,6 +37,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <atomic>
+#include <initializer_list>
 #include <mutex>
 #include <type_traits>
 
@@ -2111,6 +2112,256 @@ int64_t decode_max_items(int64_t batch, int64_t total_seq_len, int64_t tps) {
 }
 
 // ---------------------------------------------------------------------------
+// Attention for shapes the MFMA kernels are not built for (any head_dim up to
+// kGenericMaxDim, any GQA group): one wave per (query row, query head), the
+// lanes over the head dims.  Two passes over the keys keep the reference's
+// rounding points exactly: pass 1 forms the running maximum and the fp32
+// softmax denominator of the scores (q.k rounded to the storage dtype, times
+// the scale, rounded again: layers/paged_attention.py:97-98,
+// layers/attention.py:400); pass 2 recomputes each score and accumulates
+// round(exp(s - m) / l) * v in fp32 (the probabilities cast to the storage
+// dtype before P.V, :109-114 and :410-411), rounding once at the end.  The
+// work per key is a wave reduction, so these shapes run far below the tuned
+// kernels' rate; they exist so that every shape the reference accepts runs.
+// ---------------------------------------------------------------------------
+constexpr int kGenericMaxDim = 256;
+constexpr int kGenericWaves = 4;
+
+struct GenericAttnArgs {
+  const void* q;
+  int64_t q_sr, q_sh;  // query row / head strides (elements)
+  void* out;
+  int64_t o_sr, o_sh;
+  const void* k_cache;
+  const void* v_cache;
+  CacheGeom geom;
+  int32_t head_dim;
+  int32_t q_heads;
+  int32_t group;
+  const int32_t* tables;
+  int64_t table_stride;
+  float scale;
+  int64_t rows;  // query rows
+  // decode: row b is sequence b over its first seq_lens[b] keys
+  const int32_t* seq_lens;
+  // varlen (seq_lens == nullptr): row t of request r (cu_seqlens[r] <= t <
+  // cu_seqlens[r + 1]) sees keys [0, context_lens[r] + t - cu_seqlens[r]]
+  const int64_t* cu_seqlens;
+  const int32_t* context_lens;
+  int64_t num_seqs;
+  // decode only: RoPE of q at position seq_len - 1 (cos / sin tables
+  // (rope_rows, head_dim / 2)); nullptr: none
+  const void* rope_cos;
+  const void* rope_sin;
+  int64_t rope_rows;
+};
+
+__device__ __forceinline__ float wave_sum_f32(float x) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kGenericWaves* kWave) void attention_generic_kernel(GenericAttnArgs a) {
+  constexpr int kPer = kGenericMaxDim / kWave;
+  const int lane = lane_id();
+  const int64_t w = (int64_t)blockIdx.x * kGenericWaves + threadIdx.x / kWave;
+  if (w >= a.rows * a.q_heads) return;  // uniform over the wave
+  const int64_t row = w / a.q_heads;
+  const int h = (int)(w - row * a.q_heads);
+  const int D = a.head_dim;
+  int64_t seq;
+  int nkeys;
+  if (a.seq_lens != nullptr) {
+    seq = row;
+    nkeys = a.seq_lens[row];
+  } else {
+    int64_t lo = 0, hi = a.num_seqs - 1;  // the last request whose first row is <= row
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (a.cu_seqlens[mid] <= row) lo = mid;
+      else hi = mid - 1;
+    }
+    seq = lo;
+    nkeys = a.context_lens[lo] + (int)(row - a.cu_seqlens[lo]) + 1;
+  }
+  nkeys = __builtin_amdgcn_readfirstlane(nkeys);
+  seq = uniform64(seq);
+  T* orow = reinterpret_cast<T*>(a.out) + row * a.o_sr + (int64_t)h * a.o_sh;
+  if (nkeys <= 0) {  // nothing to attend: zeros, not garbage
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (lane + kWave * i < D) store_elt<T>(orow + lane + kWave * i, 0.f);
+    }
+    return;
+  }
+  // this lane's dims of q (rotated first when RoPE tables are given)
+  const T* qrow = reinterpret_cast<const T*>(a.q) + row * a.q_sr + (int64_t)h * a.q_sh;
+  float q[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = lane + kWave * i;
+    q[i] = d < D ? load_elt<T>(qrow, d) : 0.f;
+    if (a.rope_cos != nullptr && d < D) {
+      const int half = D / 2;
+      int64_t pos = nkeys - 1;
+      pos = pos >= a.rope_rows ? a.rope_rows - 1 : pos;
+      const int j = d < half ? d : d - half;
+      const float c = load_elt<T>(a.rope_cos, pos * half + j);
+      const float sn = load_elt<T>(a.rope_sin, pos * half + j);
+      const float other = load_elt<T>(qrow, d < half ? d + half : d - half);
+      q[i] = d < half ? sub_t<T>(mul_t<T>(q[i], c), mul_t<T>(other, sn))
+                      : add_t<T>(mul_t<T>(q[i], c), mul_t<T>(other, sn));
+    }
+  }
+  const int32_t* table = a.tables + seq * a.table_stride;
+  const int tlen = (int)a.table_stride;
+  const int kvh = h / a.group;
+  const T* kc = reinterpret_cast<const T*>(a.k_cache) + (int64_t)kvh * D;
+  const T* vc = reinterpret_cast<const T*>(a.v_cache) + (int64_t)kvh * D;
+  auto score = [&](int64_t off) {
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int d = lane + kWave * i;
+      if (d < D) part = fmaf(q[i], load_elt<T>(kc + off, d), part);
+    }
+    return scaled_score<T>(wave_sum_f32(part), a.scale);
+  };
+  float m = kNegInf, l = 0.f;
+  for (int k = 0; k < nkeys; ++k) {
+    const float sc = score(token_offset(a.geom, table, tlen, k));
+    const float m_new = score_max(m, sc);
+    l = (m == kNegInf ? 0.f : l * expf(m - m_new)) + expf(sc - m_new);
+    m = m_new;
+  }
+  float o[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) o[i] = 0.f;
+  const float inv_l = 1.f / l;
+  for (int k = 0; k < nkeys; ++k) {
+    const int64_t off = token_offset(a.geom, table, tlen, k);
+    const float p = round_storage<T>(expf(score(off) - m) * inv_l);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int d = lane + kWave * i;
+      if (d < D) o[i] = fmaf(p, load_elt<T>(vc + off, d), o[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    if (lane + kWave * i < D) store_elt<T>(orow + lane + kWave * i, o[i]);
+  }
+}
+
+// The fused decode step's cache write for the shapes above: sequence b's new
+// K (rotated at position seq_lens[b] - 1 when RoPE tables are given, as
+// rope_kv_append_kernel rotates it) and V rows into the slot its table gives;
+// a table entry outside the pool skips the write.  One thread per
+// (sequence, KV head, dim).
+struct GenericAppendArgs {
+  const void* k_new;
+  int64_t kn_s;
+  const void* v_new;
+  int64_t vn_s;
+  void* k_cache;
+  void* v_cache;
+  CacheGeom geom;
+  int32_t head_dim;
+  const int32_t* tables;
+  int64_t table_stride;
+  const int32_t* seq_lens;
+  int64_t batch;
+  const void* rope_cos;
+  const void* rope_sin;
+  int64_t rope_rows;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void decode_append_generic_kernel(GenericAppendArgs a) {
+  const int D = a.head_dim;
+  const int64_t per_seq = (int64_t)a.geom.kv_heads * D;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.batch * per_seq) return;
+  const int64_t b = i / per_seq;
+  const int64_t e = i - b * per_seq;  // element (kv head * D + dim) of the row
+  const int d = (int)(e % D);
+  const int pos = a.seq_lens[b] - 1;
+  if (pos < 0) return;
+  int lb, off;
+  if (a.geom.bs_shift >= 0) {
+    lb = pos >> a.geom.bs_shift;
+    off = pos & (a.geom.block_size - 1);
+  } else {
+    lb = pos / a.geom.block_size;
+    off = pos - lb * a.geom.block_size;
+  }
+  if (lb >= a.table_stride) return;
+  const int phys = a.tables[b * a.table_stride + lb];
+  if (phys < 0 || phys >= a.geom.num_blocks) return;
+  const int64_t dst = a.geom.layer_offset + ((int64_t)phys * a.geom.block_size + off) * a.geom.row_elems + e;
+  const T* krow = reinterpret_cast<const T*>(a.k_new) + b * a.kn_s;
+  const T* vrow = reinterpret_cast<const T*>(a.v_new) + b * a.vn_s;
+  float kv = load_elt<T>(krow, e);
+  if (a.rope_cos != nullptr) {
+    const int half = D / 2;
+    int64_t rp = pos >= a.rope_rows ? a.rope_rows - 1 : pos;
+    const int j = d < half ? d : d - half;
+    const float c = load_elt<T>(a.rope_cos, rp * half + j);
+    const float sn = load_elt<T>(a.rope_sin, rp * half + j);
+    const float other = load_elt<T>(krow, d < half ? e + half : e - half);
+    kv = d < half ? sub_t<T>(mul_t<T>(kv, c), mul_t<T>(other, sn)) : add_t<T>(mul_t<T>(kv, c), mul_t<T>(other, sn));
+  }
+  store_elt<T>(reinterpret_cast<T*>(a.k_cache) + dst, kv);
+  reinterpret_cast<T*>(a.v_cache)[dst] = reinterpret_cast<const T*>(vrow)[e];
+}
+
+// rope_kv_append_kernel for an even head_dim the kernel is not built for:
+// one thread per (token, head, pair index), the same per-op rounding.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kv_append_generic_kernel(RopeAppendArgs a, int head_dim) {
+  const int half = head_dim / 2;
+  const int heads = a.q_heads + 2 * a.kv_heads;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.num_tokens * heads * half) return;
+  const int64_t r = idx / half;
+  const int i = (int)(idx - r * half);
+  const int64_t t = r / heads;
+  const int j = (int)(r - t * heads);
+  int64_t pos = a.positions[t];
+  pos = pos < 0 ? 0 : (pos >= a.table_rows ? a.table_rows - 1 : pos);
+  const float c = load_elt<T>(a.cos_table, pos * half + i);
+  const float s = load_elt<T>(a.sin_table, pos * half + i);
+  if (j < a.q_heads) {
+    T* x = reinterpret_cast<T*>(a.q) + t * a.q_st + (int64_t)j * a.q_sh;
+    const float x1 = load_elt<T>(x, i);
+    const float x2 = load_elt<T>(x, i + half);
+    store_elt<T>(x + i, sub_t<T>(mul_t<T>(x1, c), mul_t<T>(x2, s)));
+    store_elt<T>(x + i + half, add_t<T>(mul_t<T>(x2, c), mul_t<T>(x1, s)));
+    return;
+  }
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.pool_slots) return;
+  const bool is_k = j < a.q_heads + a.kv_heads;
+  const int h = is_k ? j - a.q_heads : j - a.q_heads - a.kv_heads;
+  const int64_t dst_off = a.layer_offset + (slot * a.kv_heads + h) * head_dim;
+  if (is_k) {
+    const T* x = reinterpret_cast<const T*>(a.k) + t * a.k_st + (int64_t)h * a.k_sh;
+    const float x1 = load_elt<T>(x, i);
+    const float x2 = load_elt<T>(x, i + half);
+    T* dst = reinterpret_cast<T*>(a.k_cache) + dst_off;
+    store_elt<T>(dst + i, sub_t<T>(mul_t<T>(x1, c), mul_t<T>(x2, s)));
+    store_elt<T>(dst + i + half, add_t<T>(mul_t<T>(x2, c), mul_t<T>(x1, s)));
+  } else {
+    const T* x = reinterpret_cast<const T*>(a.v) + t * a.v_st + (int64_t)h * a.v_sh;
+    T* dst = reinterpret_cast<T*>(a.v_cache) + dst_off;
+    dst[i] = x[i];
+    dst[i + half] = x[i + half];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Varlen prefill
 // ---------------------------------------------------------------------------
 constexpr int kPrefillWaves = 4;
@@ -3182,18 +3433,21 @@ int check_geometry(int64_t num_layers, int64_t layer_index, int64_t num_blocks,
   return NIE_OK;
 }
 
+// Shapes the MFMA decode / prefill kernels are built for; every other shape
+// of check_attention_shape runs on attention_generic_kernel.
+bool tuned_attention(int64_t head_dim, int64_t q_heads, int64_t kv_heads) {
+  const int64_t group = q_heads / kv_heads;
+  return (head_dim == 64 || head_dim == 128) && (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
+}
+
 int check_attention_shape(int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                           int64_t num_blocks, int64_t block_size) {
-  if (head_dim != 64 && head_dim != 128) {
-    return fail(NIE_EUNSUPPORTED, "head_dim %lld not supported (64 or 128)", (long long)head_dim);
+  if (head_dim <= 0 || head_dim > kGenericMaxDim) {
+    return fail(NIE_EUNSUPPORTED, "head_dim %lld not supported (1 to %d)", (long long)head_dim, kGenericMaxDim);
   }
   if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0) {
     return fail(NIE_EINVAL, "q_heads (%lld) must be a positive multiple of kv_heads (%lld)",
                 (long long)q_heads, (long long)kv_heads);
-  }
-  const int64_t group = q_heads / kv_heads;
-  if (group != 1 && group != 2 && group != 4 && group != 8 && group != 16) {
-    return fail(NIE_EUNSUPPORTED, "GQA group size %lld not supported", (long long)group);
   }
   if (num_blocks > 0x7fffffffLL || block_size > 0x7fffffffLL / 16 || kv_heads > 65535) {
     return fail(NIE_EINVAL, "pool dimensions exceed the supported range");
@@ -3443,6 +3697,28 @@ void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, const PrefillSch
   else launch_prefill_nb<T, D, 2>(a, p, sc, jobs, stream, merge);
 }
 
+// Element alignment of the generic path's pointers.
+bool elt_aligned(int64_t es, std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs) {
+    if (p != nullptr && ((uintptr_t)p % es) != 0) return false;
+  }
+  return true;
+}
+
+template <typename T>
+void launch_generic_attention(const GenericAttnArgs& a, hipStream_t stream) {
+  const int64_t waves = a.rows * a.q_heads;
+  hipLaunchKernelGGL((attention_generic_kernel<T>), dim3((unsigned)cdiv(waves, (int64_t)kGenericWaves)),
+                     dim3(kGenericWaves * kWave), 0, stream, a);
+}
+
+int generic_attention(int dtype, const GenericAttnArgs& a, hipStream_t stream) {
+  if (a.rows * a.q_heads > 0xffffffffLL) return fail(NIE_EINVAL, "too many query rows");
+  if (dtype == NIE_DTYPE_BF16) launch_generic_attention<bf16_t>(a, stream);
+  else launch_generic_attention<float>(a, stream);
+  return launched("attention_generic");
+}
+
 int check_aligned(const void* p, int64_t stride_a, int64_t stride_b, int64_t es) {
   return ((uintptr_t)p % 16) == 0 && ((stride_a * es) % 16) == 0 && ((stride_b * es) % 16) == 0;
 }
@@ -3562,7 +3838,7 @@ NIE_API int nie_rope_kv_append(int dtype, void* q, int64_t q_stride_t, int64_t q
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
   if (rc) return rc;
-  if (head_dim != 64 && head_dim != 128) return fail(NIE_EUNSUPPORTED, "head_dim %lld not built", (long long)head_dim);
+  if (head_dim % 2 != 0) return fail(NIE_EINVAL, "RoPE needs an even head_dim, got %lld", (long long)head_dim);
   if (num_tokens < 0 || q_heads < 0) return fail(NIE_EINVAL, "num_tokens and q_heads must be non-negative");
   if (num_tokens == 0) return NIE_OK;
   if (!q || !k_new || !v_new || !positions || !slot_mapping || !cos_table || !sin_table || !k_cache || !v_cache) {
@@ -3570,7 +3846,7 @@ NIE_API int nie_rope_kv_append(int dtype, void* q, int64_t q_stride_t, int64_t q
   }
   if (table_rows <= 0) return fail(NIE_EINVAL, "the sin/cos table must have at least one row");
   const int64_t heads = q_heads + 2 * kv_heads;
-  const int rows_per_block = 256 / (int)(head_dim / 2);
+  const int rows_per_block = (head_dim == 64 || head_dim == 128) ? 256 / (int)(head_dim / 2) : 1;
   const int64_t blocks = cdiv(num_tokens * heads, rows_per_block);
   if (heads > 0x7fffffffLL || blocks > 0x7fffffffLL) return fail(NIE_EINVAL, "too many tokens");
   RopeAppendArgs a;
@@ -3596,6 +3872,15 @@ NIE_API int nie_rope_kv_append(int dtype, void* q, int64_t q_stride_t, int64_t q
   a.q_heads = (int32_t)q_heads;
   a.kv_heads = (int32_t)kv_heads;
   hipStream_t s = (hipStream_t)stream;
+  if (head_dim != 64 && head_dim != 128) {
+    // other even head_dims: one thread per (token, head, pair)
+    const int64_t threads = num_tokens * heads * (head_dim / 2);
+    if (cdiv(threads, (int64_t)256) > 0x7fffffffLL) return fail(NIE_EINVAL, "too many tokens");
+    const dim3 ggrid((unsigned)cdiv(threads, (int64_t)256));
+    if (dtype == NIE_DTYPE_BF16) hipLaunchKernelGGL((rope_kv_append_generic_kernel<bf16_t>), ggrid, dim3(256), 0, s, a, (int)head_dim);
+    else hipLaunchKernelGGL((rope_kv_append_generic_kernel<float>), ggrid, dim3(256), 0, s, a, (int)head_dim);
+    return launched("rope_kv_append");
+  }
   const dim3 grid((unsigned)blocks);
   if (dtype == NIE_DTYPE_BF16) {
     if (head_dim == 64) hipLaunchKernelGGL((rope_kv_append_kernel<bf16_t, 64>), grid, dim3(256), 0, s, a);
@@ -3850,6 +4135,7 @@ NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64
     return 0;
   }
   if (host_seq_lens != nullptr && !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) return 0;
+  if (!tuned_attention(head_dim, q_heads, kv_heads)) return 0;  // the generic kernel needs no workspace
   const DecodePlan p = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
   return p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
 }
@@ -3895,6 +4181,72 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
                 (long long)table_stride, (long long)max_seq_len);
   }
   const int64_t es = elt_bytes(dtype);
+  if (!tuned_attention(head_dim, q_heads, kv_heads)) {
+    // other shapes: the generic kernels (no workspace; element alignment)
+    if (!elt_aligned(es, {q, out, k_cache, v_cache, append.k_new, append.v_new, append.cos_table, append.sin_table})) {
+      return fail(NIE_EINVAL, "pointers must be aligned to the element size");
+    }
+    if (append.k_new != nullptr || append.v_new != nullptr) {
+      if (!append.k_new || !append.v_new) return fail(NIE_EINVAL, "null pointer argument");
+      if (append.k_stride < kv_heads * head_dim || append.v_stride < kv_heads * head_dim) {
+        return fail(NIE_EINVAL, "new K/V rows must be (batch, kv_heads, head_dim) rows");
+      }
+      if (append.cos_table != nullptr || append.sin_table != nullptr) {
+        if (!append.cos_table || !append.sin_table || append.table_rows <= 0) {
+          return fail(NIE_EINVAL, "RoPE needs both tables and at least one row");
+        }
+        if (head_dim % 2) return fail(NIE_EINVAL, "RoPE needs an even head_dim");
+      }
+    }
+    if (batch > 0x7fffffffLL) return fail(NIE_EINVAL, "batch too large");
+    const CacheGeom geom = make_geom(layer_index, num_blocks, block_size, kv_heads, head_dim);
+    hipStream_t s = (hipStream_t)stream;
+    if (append.k_new != nullptr) {
+      GenericAppendArgs g;
+      g.k_new = append.k_new;
+      g.kn_s = append.k_stride;
+      g.v_new = append.v_new;
+      g.vn_s = append.v_stride;
+      g.k_cache = const_cast<void*>(k_cache);
+      g.v_cache = const_cast<void*>(v_cache);
+      g.geom = geom;
+      g.head_dim = (int32_t)head_dim;
+      g.tables = block_tables;
+      g.table_stride = table_stride;
+      g.seq_lens = seq_lens;
+      g.batch = batch;
+      g.rope_cos = append.cos_table;
+      g.rope_sin = append.sin_table;
+      g.rope_rows = append.table_rows;
+      const dim3 grid((unsigned)cdiv(batch * kv_heads * head_dim, (int64_t)256));
+      if (dtype == NIE_DTYPE_BF16) hipLaunchKernelGGL((decode_append_generic_kernel<bf16_t>), grid, dim3(256), 0, s, g);
+      else hipLaunchKernelGGL((decode_append_generic_kernel<float>), grid, dim3(256), 0, s, g);
+      rc = launched("decode_append_generic");
+      if (rc) return rc;
+    }
+    GenericAttnArgs ga{};
+    ga.q = q;
+    ga.q_sr = q_stride_b;
+    ga.q_sh = q_stride_h;
+    ga.out = out;
+    ga.o_sr = out_stride_b;
+    ga.o_sh = out_stride_h;
+    ga.k_cache = k_cache;
+    ga.v_cache = v_cache;
+    ga.geom = geom;
+    ga.head_dim = (int32_t)head_dim;
+    ga.q_heads = (int32_t)q_heads;
+    ga.group = (int32_t)(q_heads / kv_heads);
+    ga.tables = block_tables;
+    ga.table_stride = table_stride;
+    ga.scale = scale;
+    ga.rows = batch;
+    ga.seq_lens = seq_lens;
+    ga.rope_cos = append.k_new != nullptr ? append.cos_table : nullptr;
+    ga.rope_sin = append.k_new != nullptr ? append.sin_table : nullptr;
+    ga.rope_rows = append.table_rows;
+    return generic_attention(dtype, ga, s);
+  }
   if (!check_aligned(q, q_stride_b, q_stride_h, es) || !check_aligned(out, out_stride_b, out_stride_h, es) ||
       ((uintptr_t)k_cache % 16) || ((uintptr_t)v_cache % 16)) {
     return fail(NIE_EINVAL, "q/out/cache pointers and strides must be 16-byte aligned");
@@ -4122,6 +4474,7 @@ NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t tot
                                 max_seq_len)) {
     return 0;
   }
+  if (!tuned_attention(head_dim, q_heads, kv_heads)) return 0;  // the generic kernel needs no workspace
   const PrefillPlan p = plan_prefill(q_heads / kv_heads, kv_heads, num_seqs, total_query_tokens, max_seq_len,
                                      host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr);
   if (!p.split) return 0;  // no query tile is split
@@ -4158,6 +4511,31 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
     return fail(NIE_EINVAL, "block table row does not cover max_seq_len");
   }
   const int64_t es = elt_bytes(dtype);
+  if (!tuned_attention(head_dim, q_heads, kv_heads)) {
+    // other shapes: the generic kernel (no workspace; element alignment)
+    if (!elt_aligned(es, {q, out, k_cache, v_cache})) return fail(NIE_EINVAL, "pointers must be aligned to the element size");
+    GenericAttnArgs ga{};
+    ga.q = q;
+    ga.q_sr = q_stride_t;
+    ga.q_sh = q_stride_h;
+    ga.out = out;
+    ga.o_sr = out_stride_t;
+    ga.o_sh = out_stride_h;
+    ga.k_cache = k_cache;
+    ga.v_cache = v_cache;
+    ga.geom = make_geom(layer_index, num_blocks, block_size, kv_heads, head_dim);
+    ga.head_dim = (int32_t)head_dim;
+    ga.q_heads = (int32_t)q_heads;
+    ga.group = (int32_t)(q_heads / kv_heads);
+    ga.tables = block_tables;
+    ga.table_stride = table_stride;
+    ga.scale = scale;
+    ga.rows = total_query_tokens;
+    ga.cu_seqlens = cu_seqlens_q;
+    ga.context_lens = context_lens;
+    ga.num_seqs = num_seqs;
+    return generic_attention(dtype, ga, (hipStream_t)stream);
+  }
   if (!check_aligned(q, q_stride_t, q_stride_h, es) || !check_aligned(out, out_stride_t, out_stride_h, es) ||
       ((uintptr_t)k_cache % 16) || ((uintptr_t)v_cache % 16)) {
     return fail(NIE_EINVAL, "q/out/cache pointers and strides must be 16-byte aligned");

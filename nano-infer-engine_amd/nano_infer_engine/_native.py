@@ -23,8 +23,22 @@ NIE_DTYPE_BF16 = 1
 _DTYPE_CODES = {torch.float32: NIE_DTYPE_F32, torch.bfloat16: NIE_DTYPE_BF16}
 
 #: Head dims and GQA group sizes the attention kernels are built for.
+#: Shapes the MFMA decode / prefill kernels are built for ("tuned"); every
+#: other head_dim up to GENERIC_MAX_HEAD_DIM and every GQA group runs on the
+#: library's generic attention kernel (same results, far lower rate).
 SUPPORTED_HEAD_DIMS = (64, 128)
 SUPPORTED_GROUP_SIZES = (1, 2, 4, 8, 16)
+GENERIC_MAX_HEAD_DIM = 256
+
+
+def tuned_attention(q_heads: int, kv_heads: int, head_dim: int) -> bool:
+    """Whether the shape runs on the MFMA kernels (which need 16-byte aligned rows)."""
+    return head_dim in SUPPORTED_HEAD_DIMS and q_heads % kv_heads == 0 and q_heads // kv_heads in SUPPORTED_GROUP_SIZES
+
+
+def _row_align(q_heads: int, kv_heads: int, head_dim: int) -> int:
+    """Byte alignment the launch needs of its row pointers and strides."""
+    return 16 if tuned_attention(q_heads, kv_heads, head_dim) else 1
 
 #: Every symbol the library exports (checked by the CPU test suite).
 EXPORTED_SYMBOLS = (
@@ -675,12 +689,10 @@ def kv_copy_blocks(
 
 
 def _check_attention_shapes(q_heads: int, kv_heads: int, head_dim: int) -> None:
-    if head_dim not in SUPPORTED_HEAD_DIMS:
-        raise RuntimeError(f"HIP attention supports head_dim in {SUPPORTED_HEAD_DIMS}, not {head_dim}")
-    if q_heads % kv_heads != 0 or q_heads // kv_heads not in SUPPORTED_GROUP_SIZES:
-        raise RuntimeError(
-            f"HIP attention supports GQA group sizes {SUPPORTED_GROUP_SIZES}; got {q_heads}/{kv_heads}"
-        )
+    if not 0 < head_dim <= GENERIC_MAX_HEAD_DIM:
+        raise RuntimeError(f"HIP attention supports head_dim 1 to {GENERIC_MAX_HEAD_DIM}, not {head_dim}")
+    if q_heads <= 0 or kv_heads <= 0 or q_heads % kv_heads != 0:
+        raise RuntimeError(f"q_heads must be a positive multiple of kv_heads; got {q_heads}/{kv_heads}")
 
 
 def paged_decode(
@@ -744,8 +756,9 @@ def paged_decode(
     if rope_tables is not None and new_kv is None:
         raise ValueError("rope_tables applies to the fused append (new_kv)")
     if new_kv is not None:
-        keys, values = _check_new_rows(new_kv, batch, kv_heads, head_dim, query.dtype, query.device)
-        cos, sin, rows = _check_rope_tables(rope_tables, head_dim, query.dtype, query.device)
+        align = _row_align(q_heads, kv_heads, head_dim)
+        keys, values = _check_new_rows(new_kv, batch, kv_heads, head_dim, query.dtype, query.device, align)
+        cos, sin, rows = _check_rope_tables(rope_tables, head_dim, query.dtype, query.device, align)
         rc = lib.nie_paged_decode_append(
             dtype_code(query.dtype),
             query.data_ptr(), query.stride(0), query.stride(1),
@@ -782,26 +795,28 @@ def paged_decode(
     return out
 
 
-def _check_rope_tables(rope_tables, head_dim: int, dtype, device):
+def _check_rope_tables(rope_tables, head_dim: int, dtype, device, align: int = 16):
     """(cos pointer, sin pointer, rows) of optional RoPE tables, (rows, head_dim/2) each; (None, None, 0) without."""
     if rope_tables is None:
         return None, None, 0
+    if head_dim % 2:
+        raise ValueError("RoPE needs an even head_dim")
     cos, sin = rope_tables
     for t in (cos, sin):
         if (t.dtype != dtype or t.device != device or t.ndim != 2 or t.shape[1] != head_dim // 2
-                or not t.is_contiguous() or t.data_ptr() % 16 or t.shape[0] == 0):
+                or not t.is_contiguous() or t.data_ptr() % align or t.shape[0] == 0):
             raise ValueError("RoPE tables must be contiguous, aligned (rows, head_dim / 2) tensors of the query dtype")
     if cos.shape != sin.shape:
         raise ValueError("RoPE cos and sin tables must have the same shape")
     return cos.data_ptr(), sin.data_ptr(), cos.shape[0]
 
 
-def _check_new_rows(new_kv, batch: int, kv_heads: int, head_dim: int, dtype, device):
-    """The (keys, values) rows of a fused decode step: (batch, kv_heads, head_dim), 16-byte aligned."""
+def _check_new_rows(new_kv, batch: int, kv_heads: int, head_dim: int, dtype, device, align: int = 16):
+    """The (keys, values) rows of a fused decode step: (batch, kv_heads, head_dim), rows aligned to ``align`` bytes."""
     keys, values = new_kv
     for t in (keys, values):
         if (t.dtype != dtype or t.device != device or t.shape != (batch, kv_heads, head_dim) or t.stride(2) != 1
-                or t.stride(1) != head_dim or t.data_ptr() % 16 or (t.stride(0) * t.element_size()) % 16):
+                or t.stride(1) != head_dim or t.data_ptr() % align or (t.stride(0) * t.element_size()) % align):
             raise ValueError("new keys/values must be aligned (batch, kv_heads, head_dim) rows matching the query")
     return keys, values
 
@@ -960,7 +975,8 @@ class PreparedRopeAppend:
 class PreparedDecode:
     """``paged_decode`` for one batch of sequences (tables, lengths), any layer."""
 
-    __slots__ = ("_fn", "_fn_append", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep", "_kv_shape")
+    __slots__ = ("_fn", "_fn_append", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep", "_kv_shape",
+                 "_align")
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, total_seq_len: int, q_heads: int, scale: float,
@@ -987,6 +1003,7 @@ class PreparedDecode:
         self._device = k_cache.device
         self._shape = (batch, q_heads, head_dim)
         self._kv_shape = (batch, kv_heads, head_dim)
+        self._align = _row_align(q_heads, kv_heads, head_dim)
         self._keep = (block_tables, seq_lens, workspace, host_lens)
         self._pre = (code,)
         self._mid = (k_cache.data_ptr(), v_cache.data_ptr(), num_layers)
@@ -997,7 +1014,7 @@ class PreparedDecode:
     def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
         for t in (query, out):
             if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
-                    or t.data_ptr() % 16):
+                    or t.data_ptr() % self._align):
                 raise ValueError("query/out must be aligned (batch, q_heads, head_dim) tensors matching the batch")
         kptr, vptr, num_layers = self._mid
         (num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch, max_len, total_len,
@@ -1019,10 +1036,10 @@ class PreparedDecode:
         """
         for t in (query, out):
             if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
-                    or t.data_ptr() % 16):
+                    or t.data_ptr() % self._align):
                 raise ValueError("query/out must be aligned (batch, q_heads, head_dim) tensors matching the batch")
-        _check_new_rows((keys, values), *self._kv_shape, self._dtype, self._device)
-        cos, sin, rows = _check_rope_tables(rope_tables, self._kv_shape[2], self._dtype, self._device)
+        _check_new_rows((keys, values), *self._kv_shape, self._dtype, self._device, self._align)
+        cos, sin, rows = _check_rope_tables(rope_tables, self._kv_shape[2], self._dtype, self._device, self._align)
         kptr, vptr, num_layers = self._mid
         (num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch, max_len, total_len,
          scale, (ws, ws_bytes, hlens, stream)) = self._post
@@ -1040,7 +1057,7 @@ class PreparedDecode:
 class PreparedPrefill:
     """``varlen_prefill`` for one packed ragged batch, any layer."""
 
-    __slots__ = ("_fn", "_args", "_shape", "_dtype", "_device", "_keep")
+    __slots__ = ("_fn", "_args", "_shape", "_dtype", "_device", "_keep", "_align")
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, cu_seqlens: torch.Tensor,
                  context_lens: torch.Tensor, block_tables: torch.Tensor, total_tokens: int, max_query_len: int,
@@ -1067,6 +1084,7 @@ class PreparedPrefill:
         self._dtype = k_cache.dtype
         self._device = k_cache.device
         self._shape = (total_tokens, q_heads, head_dim)
+        self._align = _row_align(q_heads, kv_heads, head_dim)
         self._keep = (cu_seqlens, context_lens, block_tables, workspace, host_cu, host_ctx)
         self._args = (dtype_code(k_cache.dtype), cu_seqlens.data_ptr(), context_lens.data_ptr(), num_seqs,
                       total_tokens, max_query_len, max_seq_len, k_cache.data_ptr(), v_cache.data_ptr(), num_layers,
@@ -1078,7 +1096,7 @@ class PreparedPrefill:
     def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
         for t in (query, out):
             if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
-                    or t.data_ptr() % 16):
+                    or t.data_ptr() % self._align):
                 raise ValueError("query/out must be aligned (tokens, q_heads, head_dim) tensors matching the batch")
         (code, cu, ctx, num_seqs, total, max_q, max_s, kptr, vptr, num_layers, num_blocks, block_size, q_heads,
          kv_heads, head_dim, tables, tstride, scale, (ws, ws_bytes), (hcu, hctx), stream) = self._args

@@ -353,7 +353,13 @@ def test_library_workspace_queries():
     assert big >= 16 * 15 * 32 * 66 * 4
     assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1, None) == 0
     assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710, None) == 0  # bad dtype
-    assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710, None) == 0  # head_dim 96
+    # head_dim 96 and GQA group 3 run on the generic kernel, which needs no workspace
+    assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 96, 16, 500, 710, None) == 0
+    assert lib.nie_paged_decode_workspace_bytes(1, 4, 24, 8, 64, 16, 500, 710, None) == 0
+    assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 3, None, None) == 0
+    assert lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 512, 16, 500, 710, None) == 0  # beyond 256
+    assert _native.tuned_attention(32, 8, 64) and not _native.tuned_attention(32, 8, 3)
+    assert not _native.tuned_attention(24, 8, 64)
     # prefill, planned from bounds
     assert lib.nie_varlen_prefill_workspace_bytes(4, 512, 128, 4128, 32, 8, 64, None, None) > 0
 
