@@ -1,4 +1,4 @@
-"""End-to-end serving numerics of the Llama-3.2-1B-shaped model against the reference path.
+"""End-to-end serving numerics of the Llama-3.2-1B-shaped model against the reference path (bf16 and fp32).
 
 The product runs as shipped: the continuous-batching scheduler with chunked
 prefill (chunk 128, 512 prefill tokens per step, batch 16, block size 16),
@@ -60,6 +60,33 @@ def test_serving_tokens_against_reference_path():
     assert s["err_product_truth"]["median"] <= 1.05 * s["err_reference_truth"]["median"]
     assert s["err_product_truth"]["p99"] <= 1.10 * s["err_reference_truth"]["p99"]
     # every disagreement is a near-tie inside the measured row difference
+    for row in report.rows:
+        if row.product != row.reference:
+            assert row.reference_margin <= 2 * row.err_product_reference, row
+
+
+def test_serving_tokens_against_reference_path_fp32():
+    """The same serving run in fp32 (the bf16 model's weights upcast): the
+    product's greedy tokens equal the reference path's.  Teacher forcing with
+    every sampled row agreeing is free-running identity, by induction over
+    the steps.  Logit error here is ~1e-5, so only an exact tie could flip a
+    row; any flip must be such a near-tie."""
+    print("serving lockstep fp32: llama-1b shape, 16 requests x 256 tokens, chunk 128 / 512, batch 16", flush=True)
+    model = workloads.serving_model(DEV).float()
+    cfg = model.config
+    prompts = workloads.serving_prompts(DEV, cfg.vocab_size, count=16)
+    blocks = workloads.serving_cache_blocks(prompts, 256)
+
+    def cache(dtype):
+        return PagedKVCache(blocks, 16, cfg.num_layers, cfg.kv_head_num, cfg.head_dim, dtype, DEV)
+
+    report = lockstep.run_lockstep(model, prompts, cache, max_new_tokens=256, max_batch_size=16, chunk=128,
+                                   budget=512, truth=False)
+    s = report.summary()
+    print(json.dumps({k: v for k, v in s.items() if k != "first_divergence"}), flush=True)
+    assert s["requests"] == 16 and s["sampled_rows"] == 16 * 256
+    assert s["err_product_reference"]["max"] <= 1e-3
+    assert s["top1_agreement_product_reference"] >= 0.999
     for row in report.rows:
         if row.product != row.reference:
             assert row.reference_margin <= 2 * row.err_product_reference, row
