@@ -36,9 +36,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <atomic>
 #include <initializer_list>
 #include <mutex>
+#include <vector>
 #include <type_traits>
 
 #include "nie_paged.h"
@@ -2474,18 +2476,21 @@ __device__ __forceinline__ PrefillItem prefill_locate(const PrefillArgs& a, int6
 }
 
 // Work items of a prefill call planned from host metadata, passed by value
-// as a kernel argument: item i (one workgroup per KV head) is piece
-// item_piece[i] (key tiles [piece*S, (piece+1)*S), S = tiles_per_split) of
-// query tile item_tile[i], whose request, rows and context are listed per
-// tile.  Without the table each workgroup locates its item from the device
-// copies of cu_seqlens / context_lens, one memory round trip more.
+// as a kernel argument: item i (one workgroup per KV head) is the
+// item_piece[i]-th piece of query tile item_tile[i], key tiles
+// [item_begin[i], item_begin[i] + item_len[i]); the tile's request, rows and
+// context are listed per tile.  Without the table each workgroup locates
+// its item from the device copies of cu_seqlens / context_lens (one memory
+// round trip more), with pieces of tiles_per_split tiles.
 constexpr int kMaxSchedTiles = 64;
-constexpr int kMaxSchedItems = 512;
+constexpr int kMaxSchedItems = 320;
 
 struct PrefillSchedule {
   int32_t count = 0;  // items; 0: located on the device
   uint8_t item_tile[kMaxSchedItems];
   uint8_t item_piece[kMaxSchedItems];
+  uint8_t item_len[kMaxSchedItems];
+  uint16_t item_begin[kMaxSchedItems];
   int32_t first_item[kMaxSchedTiles];  // the tile's first item (its partials' first workspace slot)
   int32_t nsplit[kMaxSchedTiles];      // the tile's items; 1: the rows are written out
   int32_t req[kMaxSchedTiles];         // request of the tile
@@ -2494,6 +2499,8 @@ struct PrefillSchedule {
   int32_t ctx[kMaxSchedTiles];         // the request's cached tokens
   int32_t t0[kMaxSchedTiles];          // the tile's first query token within the request
 };
+
+static_assert(sizeof(PrefillArgs) + sizeof(PrefillSchedule) <= 4096, "prefill kernel arguments fit 4 KiB");
 
 // Key steps of kPrefillStepTiles 16-key tiles (64 keys) stream through an LDS
 // ring of prefill_stages() steps.
@@ -2683,7 +2690,8 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     q_len = sc.q_len[k];
     ctx = sc.ctx[k];
     t0 = sc.t0[k];
-    tile_begin = piece * S;
+    tile_begin = sc.item_begin[wg_item];
+    tile_cap = tile_begin + sc.item_len[wg_item];
     slot = sc.nsplit[k] == 1 ? -1 : (int64_t)sc.first_item[k] + piece;
   } else {
     const PrefillItem pit = prefill_locate(a, (int64_t)wg_item);
@@ -2702,6 +2710,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     ctx = pit.ctx;
     t0 = qt * tpt;
     tile_begin = split * S;
+    tile_cap = tile_begin + S;
     slot = nsplit == 1 ? -1 : pit.first + pit.local;
   }
   r = uniform64(r);
@@ -2711,7 +2720,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   ctx = __builtin_amdgcn_readfirstlane(ctx);
   t0 = __builtin_amdgcn_readfirstlane(t0);
   tile_begin = __builtin_amdgcn_readfirstlane(tile_begin);
-  tile_cap = tile_begin + S;
+  tile_cap = __builtin_amdgcn_readfirstlane(tile_cap);
   const int t_end = min(t0 + tpt, q_len);
   const int key_end = ctx + t_end;
   const int tile_end = min(tile_cap, (key_end + kTileKeys - 1) / kTileKeys);
@@ -3098,13 +3107,18 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
       const int64_t wrow = (slot * a.geom.kv_heads + h) * kRows + (wave * kRowBlocks + nb) * 16 + row;
       float* dst = a.ws_o + wrow * D + 4 * g;
 #pragma unroll
+      // streaming stores: the partials drain to memory while other items
+      // still run, instead of in the L2 writeback at the end of the kernel
+      // (mixed chunked-prefill step: 26.4 -> 25.6 us per call)
       for (int c = 0; c < D / 16; ++c) {
-        *reinterpret_cast<float4*>(dst + 16 * c) =
-            make_float4(st[nb].o[c][0], st[nb].o[c][1], st[nb].o[c][2], st[nb].o[c][3]);
+        __builtin_nontemporal_store(st[nb].o[c], reinterpret_cast<v4f*>(dst + 16 * c));
       }
       // the merge expects the maximum of the scaled scores
       const float m = kPow2Scale ? st[nb].m * a.scale : st[nb].m;
-      if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + wrow * 2) = make_float2(m, lsum);
+      if (g == 0) {
+        __builtin_nontemporal_store(m, a.ws_ml + wrow * 2);
+        __builtin_nontemporal_store(lsum, a.ws_ml + wrow * 2 + 1);
+      }
     }
   }
 }
@@ -3255,23 +3269,38 @@ constexpr int64_t kPrefillTargetItems = 2048;
 constexpr int64_t kPrefillMinTilesPerSplit = 8;
 constexpr int64_t kPrefillMaxTilesPerSplit = 64;
 
-struct PrefillPlan;
-void fill_merge_jobs(const PrefillPlan& p, int64_t num_seqs, const int64_t* host_cu, const int32_t* host_ctx,
-                     PrefillMergeJobs* jobs);
+// A query tile of a host-planned prefill call (tiles in request order) and
+// its pieces' workspace slots [first, first + pieces).
+struct PrefillTile {
+  int64_t r;       // request
+  int64_t qt;      // query tile within the request
+  int64_t ktiles;  // 16-key tiles it sees
+  int64_t pieces;
+  int64_t first;
+};
+
+// One work item: key tiles [begin, begin + len) of query tile `tile`, its
+// `piece`-th piece.
+struct PrefillPiece {
+  int32_t tile, piece, begin, len;
+};
 
 struct PrefillPlan {
   int row_blocks = 2;  // MFMA row blocks per wave
   int tokens_per_tile = 64;
-  int64_t tps = kPrefillMaxTilesPerSplit;
-  int64_t items = 0;   // prefill grid.x: the item count (exact from host metadata, else a bound)
+  int64_t tps = kPrefillMaxTilesPerSplit;  // piece length of the device-located plan
+  int64_t items = 0;   // prefill grid.x per KV head: the item count (exact from host metadata, else a bound)
   int64_t qtiles = 0;  // merge grid.x: the query-tile count (exact, else a bound)
   int64_t rows = 0;    // rows per item
   bool split = false;  // some query tile is split over several items
+  // host metadata: the query tiles and the items in dispatch order
+  std::vector<PrefillTile> tiles;
+  std::vector<PrefillPiece> order;
 };
 
-// Workgroups a prefill call aims for with host metadata: the split length is
-// chosen so the items fill the GPU about once (two workgroups fit a CU at
-// head_dim 64; 1.5 per CU measured fastest on the mixed chunked-prefill step).
+// Workgroups a prefill call aims for with host metadata when its pieces are
+// uniform: the split length is chosen so the items fill the GPU about once
+// (two workgroups fit a CU at head_dim 64; 1.5 per CU measured fastest).
 inline int64_t prefill_slots() { return 3 * device_cus() / 2; }
 
 // Key tiles visible to query tile qt of a request with n query tokens after
@@ -3279,6 +3308,70 @@ inline int64_t prefill_slots() { return 3 * device_cus() / 2; }
 int64_t host_key_tiles(int64_t ctx, int64_t n, int64_t tpt, int64_t qt) {
   const int64_t t_end = (qt + 1) * tpt < n ? (qt + 1) * tpt : n;
   return cdiv(ctx + t_end, (int64_t)kTileKeys);
+}
+
+// Balanced pieces for a call whose KV heads each fill one XCD (kv_heads ==
+// kXcds, the grid is head-major over the XCDs): every query tile is cut into
+// pieces of about half a CU's share of the head's 64-key steps, and the
+// pieces are ordered so that the dispatcher, which places the k-th and the
+// (k + CUs)-th workgroup of an XCD on one CU, pairs the smallest of the
+// large pieces with the largest of the small ones.  False (uniform pieces
+// instead) when the call is too small to fill the XCD twice or its pieces
+// would not fit the kernel-argument tables.
+bool plan_balanced(PrefillPlan& p, int64_t kv_heads) {
+  const int64_t ncu = device_cus() / kXcds;
+  if (kv_heads != kXcds || ncu < 2 || p.tiles.size() > (size_t)kMaxSchedTiles) return false;
+  const int64_t slots = 2 * ncu;
+  int64_t total = 0;
+  for (const PrefillTile& t : p.tiles) total += cdiv(t.ktiles, (int64_t)kPrefillStepTiles);
+  if (total < slots) return false;
+  double half = (double)total / (double)slots;  // steps per piece
+  std::vector<int64_t> n(p.tiles.size());
+  for (int attempt = 0;; ++attempt) {
+    int64_t count = 0;
+    for (size_t i = 0; i < p.tiles.size(); ++i) {
+      const int64_t steps = cdiv(p.tiles[i].ktiles, (int64_t)kPrefillStepTiles);
+      int64_t k = (int64_t)std::llround((double)steps / half);
+      const int64_t min_k = cdiv(p.tiles[i].ktiles, kPrefillMaxTilesPerSplit);
+      k = k < min_k ? min_k : (k > steps ? steps : k);
+      n[i] = k < 1 ? 1 : k;
+      count += n[i];
+    }
+    if (count <= slots) break;
+    if (attempt == 64) return false;
+    half *= 1.05;
+  }
+  std::vector<PrefillPiece> pieces;
+  int64_t first = 0, splits = 0;
+  for (size_t i = 0; i < p.tiles.size(); ++i) {
+    PrefillTile& t = p.tiles[i];
+    const int64_t steps = cdiv(t.ktiles, (int64_t)kPrefillStepTiles);
+    t.pieces = n[i];
+    t.first = first;
+    first += n[i];
+    splits += n[i] > 1;
+    int64_t done = 0;  // steps before this piece
+    for (int64_t j = 0; j < n[i]; ++j) {
+      const int64_t size = steps / n[i] + (j < steps % n[i] ? 1 : 0);
+      const int64_t begin = done * kPrefillStepTiles;
+      const int64_t len = std::min(size * kPrefillStepTiles, t.ktiles - begin);
+      if (begin > 0xffff || len > 255) return false;
+      pieces.push_back(PrefillPiece{(int32_t)i, (int32_t)j, (int32_t)begin, (int32_t)len});
+      done += size;
+    }
+  }
+  if (pieces.size() > (size_t)kMaxSchedItems || splits > kMaxMergeJobs) return false;
+  // the ncu largest in ascending order, then the rest in descending order:
+  // dispatch position k < ncu and k + ncu share a CU
+  std::vector<PrefillPiece> by_size(pieces);
+  std::stable_sort(by_size.begin(), by_size.end(),
+                   [](const PrefillPiece& x, const PrefillPiece& y) { return x.len > y.len; });
+  const size_t big = std::min((size_t)ncu, by_size.size());
+  p.order.assign(by_size.rbegin() + (by_size.size() - big), by_size.rend());
+  p.order.insert(p.order.end(), by_size.begin() + big, by_size.end());
+  p.items = (int64_t)pieces.size();
+  p.split = splits > 0;
+  return true;
 }
 
 // host_cu / host_ctx: optional host copies of cu_seqlens / context_lens,
@@ -3299,26 +3392,35 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
     return cdiv(tps, (int64_t)kPrefillStepTiles) * kPrefillStepTiles;  // whole key steps
   };
   if (host_cu != nullptr && host_ctx != nullptr) {
-    int64_t work = 0, qtiles = 0, max_kt = 0;
+    int64_t work = 0;
     for (int64_t r = 0; r < num_seqs; ++r) {
       const int64_t n = host_cu[r + 1] - host_cu[r];
-      const int64_t nqt = cdiv(n, tpt);
-      qtiles += nqt;
-      for (int64_t qt = 0; qt < nqt; ++qt) {
+      for (int64_t qt = 0; qt < cdiv(n, tpt); ++qt) {
         const int64_t kt = host_key_tiles(host_ctx[r], n, tpt, qt);
+        p.tiles.push_back(PrefillTile{r, qt, kt, 0, 0});
         work += kt;
-        max_kt = kt > max_kt ? kt : max_kt;
       }
     }
+    p.qtiles = (int64_t)p.tiles.size();
+    static const int balanced_off = env_int("NIE_PREFILL_UNIFORM");
+    if (forced <= 0 && balanced_off <= 0 && plan_balanced(p, kv_heads)) return p;
+    // uniform pieces of tps tiles, in request order
     p.tps = clamp_tps(cdiv(work * kv_heads, prefill_slots()));
-    int64_t items = 0;
-    for (int64_t r = 0; r < num_seqs; ++r) {
-      const int64_t n = host_cu[r + 1] - host_cu[r];
-      for (int64_t qt = 0; qt < cdiv(n, tpt); ++qt) items += cdiv(host_key_tiles(host_ctx[r], n, tpt, qt), p.tps);
+    p.order.clear();
+    int64_t first = 0;
+    for (size_t i = 0; i < p.tiles.size(); ++i) {
+      PrefillTile& t = p.tiles[i];
+      t.pieces = cdiv(t.ktiles, p.tps);
+      t.first = first;
+      first += t.pieces;
+      p.split |= t.pieces > 1;
+      for (int64_t j = 0; j < t.pieces; ++j) {
+        const int64_t begin = j * p.tps;
+        p.order.push_back(PrefillPiece{(int32_t)i, (int32_t)j, (int32_t)begin,
+                                       (int32_t)std::min(p.tps, t.ktiles - begin)});
+      }
     }
-    p.items = items;
-    p.qtiles = qtiles;
-    p.split = max_kt > p.tps;
+    p.items = first;
     return p;
   }
   const int64_t qtiles = total_tokens / tpt + num_seqs;  // >= sum_r ceil(len_r / tpt)
@@ -3332,69 +3434,67 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
 }
 
 // The split query tiles of a host-planned call as merge jobs (count 0 when
-// there are more than kMaxMergeJobs: the merge then locates them itself).
+// there are more than kMaxMergeJobs: the merge then locates them itself,
+// which needs the uniform pieces of the device-located plan).
 void fill_merge_jobs(const PrefillPlan& p, int64_t num_seqs, const int64_t* host_cu, const int32_t* host_ctx,
                      PrefillMergeJobs* jobs) {
+  (void)num_seqs;
+  (void)host_ctx;
   jobs->count = 0;
-  if (host_cu == nullptr || host_ctx == nullptr) return;
+  if (host_cu == nullptr || p.tiles.empty()) return;
   const int64_t tpt = p.tokens_per_tile;
-  int64_t item = 0;
   int n = 0;
-  for (int64_t r = 0; r < num_seqs; ++r) {
-    const int64_t len = host_cu[r + 1] - host_cu[r];
-    for (int64_t qt = 0; qt < cdiv(len, tpt); ++qt) {
-      const int64_t nsplit = cdiv(host_key_tiles(host_ctx[r], len, tpt, qt), p.tps);
-      if (nsplit > 1) {
-        if (n == kMaxMergeJobs || item > 0x7fffffffLL || host_cu[r] + qt * tpt > 0x7fffffffLL || nsplit > 0x7fff) {
-          jobs->count = 0;
-          return;
-        }
-        jobs->first_item[n] = (int32_t)item;
-        jobs->row0[n] = (int32_t)(host_cu[r] + qt * tpt);
-        const int64_t tokens = len - qt * tpt < tpt ? len - qt * tpt : tpt;
-        jobs->nsplit_tokens[n] = (int32_t)((nsplit << 16) | tokens);
-        ++n;
-      }
-      item += nsplit;
+  for (const PrefillTile& t : p.tiles) {
+    if (t.pieces <= 1) continue;
+    const int64_t len = host_cu[t.r + 1] - host_cu[t.r];
+    const int64_t row0 = host_cu[t.r] + t.qt * tpt;
+    if (n == kMaxMergeJobs || t.first > 0x7fffffffLL || row0 > 0x7fffffffLL || t.pieces > 0x7fff) {
+      jobs->count = 0;
+      return;
     }
+    jobs->first_item[n] = (int32_t)t.first;
+    jobs->row0[n] = (int32_t)row0;
+    const int64_t tokens = len - t.qt * tpt < tpt ? len - t.qt * tpt : tpt;
+    jobs->nsplit_tokens[n] = (int32_t)((t.pieces << 16) | tokens);
+    ++n;
   }
   jobs->count = n;
 }
 
-// The item table of a host-planned call (see PrefillSchedule), in the order
-// of the device-side enumeration: requests in order, query tiles in order,
-// pieces in order, so item indices, workspace slots and merge jobs are the
-// same either way.  False when the call has more query tiles or items than
-// the table holds (the workgroups then locate their items).
+// The item table of a host-planned call (see PrefillSchedule), in the plan's
+// dispatch order.  False when the call has more query tiles or items than
+// the table holds (the workgroups then locate their items, which needs the
+// uniform pieces of the device-located plan).
 bool build_prefill_schedule(const PrefillPlan& p, int64_t num_seqs, const int64_t* host_cu,
                             const int32_t* host_ctx, PrefillSchedule* sc) {
+  (void)num_seqs;
   sc->count = 0;
-  const int64_t tpt = p.tokens_per_tile;
-  int64_t k = 0, items = 0;
-  for (int64_t r = 0; r < num_seqs; ++r) {
-    const int64_t n = host_cu[r + 1] - host_cu[r];
-    for (int64_t qt = 0; qt < cdiv(n, tpt); ++qt) {
-      const int64_t nsplit = cdiv(host_key_tiles(host_ctx[r], n, tpt, qt), p.tps);
-      if (k == kMaxSchedTiles || items + nsplit > kMaxSchedItems || nsplit > 255 || host_cu[r] > 0x7fffffffLL ||
-          n > 0x7fffffffLL) {
-        return false;
-      }
-      sc->first_item[k] = (int32_t)items;
-      sc->nsplit[k] = (int32_t)nsplit;
-      sc->req[k] = (int32_t)r;
-      sc->q_begin[k] = (int32_t)host_cu[r];
-      sc->q_len[k] = (int32_t)n;
-      sc->ctx[k] = host_ctx[r];
-      sc->t0[k] = (int32_t)(qt * tpt);
-      for (int64_t j = 0; j < nsplit; ++j, ++items) {
-        sc->item_tile[items] = (uint8_t)k;
-        sc->item_piece[items] = (uint8_t)j;
-      }
-      ++k;
-    }
+  if (p.tiles.empty() || p.tiles.size() > (size_t)kMaxSchedTiles || p.order.size() > (size_t)kMaxSchedItems ||
+      (int64_t)p.order.size() != p.items) {
+    return false;
   }
-  if (items != p.items) return false;  // the plan counts the same items
-  sc->count = (int32_t)items;
+  const int64_t tpt = p.tokens_per_tile;
+  for (size_t k = 0; k < p.tiles.size(); ++k) {
+    const PrefillTile& t = p.tiles[k];
+    const int64_t n = host_cu[t.r + 1] - host_cu[t.r];
+    if (t.pieces > 255 || host_cu[t.r] > 0x7fffffffLL || n > 0x7fffffffLL) return false;
+    sc->first_item[k] = (int32_t)t.first;
+    sc->nsplit[k] = (int32_t)t.pieces;
+    sc->req[k] = (int32_t)t.r;
+    sc->q_begin[k] = (int32_t)host_cu[t.r];
+    sc->q_len[k] = (int32_t)n;
+    sc->ctx[k] = host_ctx[t.r];
+    sc->t0[k] = (int32_t)(t.qt * tpt);
+  }
+  for (size_t i = 0; i < p.order.size(); ++i) {
+    const PrefillPiece& q = p.order[i];
+    if (q.begin > 0xffff || q.len > 255) return false;
+    sc->item_tile[i] = (uint8_t)q.tile;
+    sc->item_piece[i] = (uint8_t)q.piece;
+    sc->item_begin[i] = (uint16_t)q.begin;
+    sc->item_len[i] = (uint8_t)q.len;
+  }
+  sc->count = (int32_t)p.order.size();
   return true;
 }
 
