@@ -133,6 +133,13 @@ __device__ __forceinline__ v4f round_bf16x4(v4f v) {
              __uint_as_float(hi & 0xffff0000u)};
 }
 
+// Rounds x to bf16 (round to nearest even) and returns the rounded value as
+// a float in one instruction: v_cvt_pk_bf16_f32 with 0 for the low half
+// leaves bf16(x) in the high half, which read as a float is the value itself.
+__device__ __forceinline__ float round_bf16_in_f32(float x) {
+  return __uint_as_float(pack_bf16x2(0.f, x));
+}
+
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Four floats -> the bf16 MFMA operand (element i = x[i]).
@@ -182,11 +189,19 @@ __device__ __forceinline__ float max_over_groups(float x) {
 }
 
 // The dispatcher hands workgroup i of a launch to XCD i % kXcds (round robin
-// over MI355X's eight XCDs, each with its own L2).  xcd_logical maps a 1-D
+// over MI355X's eight XCDs, each with its own L2).  xcd_logical (and
+// xcd_logical32, the same in 32-bit arithmetic) maps a 1-D
 // workgroup index to a logical index so that each XCD receives one contiguous
 // range of [0, n): workgroups that share inputs (the items of one KV head)
 // then share an L2.  Only placement depends on it, never correctness.
 constexpr int64_t kXcds = 8;
+
+__device__ __forceinline__ uint32_t xcd_logical32(uint32_t i, uint32_t n) {
+  constexpr uint32_t kX = (uint32_t)kXcds;
+  const uint32_t x = i % kX, j = i / kX;
+  const uint32_t q = n / kX, r = n % kX;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + j;
+}
 
 __device__ __forceinline__ int64_t xcd_logical(int64_t i, int64_t n) {
   const int64_t x = i % kXcds, j = i / kXcds;
@@ -281,13 +296,16 @@ constexpr int kTableWindow = 2 * kWave;
 
 struct TableCache {
   int base;        // first cached logical block (wave-uniform)
-  int entries[2];  // lane i: table[base + i], table[base + 64 + i]; 0 past the end of the table row
+  int entries[2];  // lane i: table[base + i], table[base + 64 + i] (the row's last entry past its end)
 
+  // The reads are clamped to the row's last entry (table_len >= 1), so they
+  // need neither a branch nor a wait where they are issued; every lookup
+  // asks for a block inside the row, so the entries past it are never used.
   __device__ __forceinline__ void load(const int32_t* table, int table_len, int first) {
     base = __builtin_amdgcn_readfirstlane(first);
     const int i = base + lane_id();
-    entries[0] = i < table_len ? table[i] : 0;
-    entries[1] = i + kWave < table_len ? table[i + kWave] : 0;
+    entries[0] = table[min(i, table_len - 1)];
+    entries[1] = table[min(i + kWave, table_len - 1)];
   }
   // Physical block of logical block `lb` (wave-uniform).  With kRefill the
   // window moves when `lb` leaves it; without, the caller guarantees
@@ -2476,28 +2494,25 @@ __device__ __forceinline__ PrefillItem prefill_locate(const PrefillArgs& a, int6
 }
 
 // Work items of a prefill call planned from host metadata, passed by value
-// as a kernel argument: item i (one workgroup per KV head) is the
-// item_piece[i]-th piece of query tile item_tile[i], key tiles
-// [item_begin[i], item_begin[i] + item_len[i]); the tile's request, rows and
-// context are listed per tile.  Without the table each workgroup locates
-// its item from the device copies of cu_seqlens / context_lens (one memory
-// round trip more), with pieces of tiles_per_split tiles.
+// as a kernel argument: item i (one workgroup per KV head) is piece p of
+// query tile k, key tiles [item_begin[i], item_begin[i] + len), with
+// item[i] = k | p << 8 | len << 16; the tile's request, rows and context are
+// listed per tile.  Every field is a 32-bit word, so a workgroup reads its
+// item and then its tile with scalar loads.  Without the table each workgroup locates its item from the
+// device copies of cu_seqlens / context_lens, with pieces of tiles_per_split
+// tiles.
 constexpr int kMaxSchedTiles = 64;
 constexpr int kMaxSchedItems = 320;
 
 struct PrefillSchedule {
   int32_t count = 0;  // items; 0: located on the device
-  uint8_t item_tile[kMaxSchedItems];
-  uint8_t item_piece[kMaxSchedItems];
-  uint8_t item_len[kMaxSchedItems];
-  uint16_t item_begin[kMaxSchedItems];
-  int32_t first_item[kMaxSchedTiles];  // the tile's first item (its partials' first workspace slot)
-  int32_t nsplit[kMaxSchedTiles];      // the tile's items; 1: the rows are written out
-  int32_t req[kMaxSchedTiles];         // request of the tile
-  int32_t q_begin[kMaxSchedTiles];     // the request's first packed query row
-  int32_t q_len[kMaxSchedTiles];       // the request's query tokens
-  int32_t ctx[kMaxSchedTiles];         // the request's cached tokens
-  int32_t t0[kMaxSchedTiles];          // the tile's first query token within the request
+  uint32_t item[kMaxSchedItems];        // tile | piece << 8 | len << 16
+  uint32_t item_begin[kMaxSchedItems];  // first key tile of the piece
+  uint32_t tile[kMaxSchedTiles];        // request | pieces << 8 | first item << 16 (pieces 1: rows written out)
+  int32_t q_begin[kMaxSchedTiles];      // the request's first packed query row
+  int32_t q_len[kMaxSchedTiles];        // the request's query tokens
+  int32_t ctx[kMaxSchedTiles];          // the request's cached tokens
+  int32_t t0[kMaxSchedTiles];           // the tile's first query token within the request
 };
 
 static_assert(sizeof(PrefillArgs) + sizeof(PrefillSchedule) <= 4096, "prefill kernel arguments fit 4 KiB");
@@ -2671,10 +2686,11 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   const int row = lane & 15;
   const int tpt = a.tokens_per_tile;
   const int S = a.tiles_per_split;
-  // (item, KV head) of this workgroup, head-major over the XCDs
-  const int64_t logical = xcd_logical(blockIdx.x, (int64_t)a.grid_items * a.geom.kv_heads);
-  const int h = (int)(logical / a.grid_items);
-  const int wg_item = (int)(logical % a.grid_items);
+  // (item, KV head) of this workgroup, head-major over the XCDs; 32-bit
+  // and scalar, so the schedule below is read with scalar loads
+  const uint32_t logical = xcd_logical32(blockIdx.x, (uint32_t)a.grid_items * (uint32_t)a.geom.kv_heads);
+  const int h = __builtin_amdgcn_readfirstlane((int)(logical / (uint32_t)a.grid_items));
+  const int wg_item = __builtin_amdgcn_readfirstlane((int)(logical - (uint32_t)h * (uint32_t)a.grid_items));
 
   // This workgroup's item: request r, query tile from token t0, key tiles
   // [tile_begin, tile_cap), and the workspace slot of its partial (-1: the
@@ -2683,16 +2699,17 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   int q_len, ctx, t0, tile_begin, tile_cap;
   if (sc.count > 0) {
     if (wg_item >= sc.count) return;  // uniform over the workgroup
-    const int k = sc.item_tile[wg_item];
-    const int piece = sc.item_piece[wg_item];
-    r = sc.req[k];
+    const uint32_t it = sc.item[wg_item];
+    const int k = (int)(it & 0xff);
+    const uint32_t tl = sc.tile[k];
+    r = (int64_t)(tl & 0xff);
+    tile_begin = (int)sc.item_begin[wg_item];
+    tile_cap = tile_begin + (int)(it >> 16);
     q_begin = sc.q_begin[k];
     q_len = sc.q_len[k];
     ctx = sc.ctx[k];
     t0 = sc.t0[k];
-    tile_begin = sc.item_begin[wg_item];
-    tile_cap = tile_begin + sc.item_len[wg_item];
-    slot = sc.nsplit[k] == 1 ? -1 : (int64_t)sc.first_item[k] + piece;
+    slot = ((tl >> 8) & 0xff) == 1 ? -1 : (int64_t)(tl >> 16) + (int64_t)((it >> 8) & 0xff);
   } else {
     const PrefillItem pit = prefill_locate(a, (int64_t)wg_item);
     if (pit.r < 0) return;  // uniform over the workgroup
@@ -2731,6 +2748,11 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   const T* kc = reinterpret_cast<const T*>(a.k_cache) + h * D;
   const T* vc = reinterpret_cast<const T*>(a.v_cache) + h * D;
 
+  // the block-table window first: the first K/V fetch waits for it, the Q
+  // rows only the first scores
+  TableCache tc;
+  if constexpr (kUniform) tc.load(table, tlen, (tile_begin * kTileKeys) >> a.geom.bs_shift);
+
   // Rows: block nb of this wave = tokens t0 + (wave*kRowBlocks + nb)*(16/G) + row/G, head row%G.
   const int tpb = 16 / a.group;  // tokens per row block
   F qf[kRowBlocks];
@@ -2741,12 +2763,10 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     const int tq = t0 + (wave * kRowBlocks + nb) * tpb + row / a.group;
     const int qh = h * a.group + row % a.group;
     q_pos[nb] = tq < t_end ? ctx + tq : -1;  // -1: no keys visible (padding row)
-    if (tq < t_end) {
-      load_slice<T, D>(qf[nb], reinterpret_cast<const T*>(a.q) + (q_begin + tq) * a.q_st + qh * a.q_sh);
-    } else {
-#pragma unroll
-      for (int i = 0; i < F::kVec; ++i) qf[nb].v[i] = uint4{0u, 0u, 0u, 0u};
-    }
+    // a padding row reads the tile's last row (no branch around the loads);
+    // it has its own MFMA column and is never written
+    const int tq_read = min(tq, t_end - 1);
+    load_slice<T, D>(qf[nb], reinterpret_cast<const T*>(a.q) + (q_begin + tq_read) * a.q_st + qh * a.q_sh);
     st[nb].init();
   }
   // first and last position of each row block (wave-uniform): steps past
@@ -2758,8 +2778,6 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     block_last[nb] = min(ctx + t0 + (wave * kRowBlocks + nb + 1) * tpb, key_end) - 1;
   }
 
-  TableCache tc;
-  if constexpr (kUniform) tc.load(table, tlen, (tile_begin * kTileKeys) >> a.geom.bs_shift);
 
   // This wave's DMA ops of the step starting at key0: the K ops then the V
   // ops of the step's tile `wave` (op = wave*kOwnOps + i, the tile's LDS
@@ -2918,111 +2936,125 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     wait_reads();
     qk();
 
-    for (int s0 = 0; s0 < nsteps; s0 += kStages) {
+    // A row's reference point moves when one of its scores is more than
+    // kRescaleLog2 (log2 units) above it, i.e. more than grow_thr in score
+    // units; nref = -m * exp_c is kept with it (0 while m = -inf, so that a
+    // row with nothing unmasked yet gets exact zeros, not NaN).
+    const float grow_thr = kRescaleLog2 / exp_c;
+    float nref[kRowBlocks];
 #pragma unroll
-      for (int j = 0; j < kStages; ++j) {
-        const int s = s0 + j;
-        if (s >= nsteps) break;  // uniform over the workgroup
-        const bool more = s + 1 < nsteps;
-        if (more) {
-          // step s+1 has landed for every wave (this wave's ops: at most
-          // those of the steps issued after it remain), and every wave has
-          // finished step s-1, whose stage the next fetch reuses
-          wait_dma_groups<kOwnOps, kAhead - 2>(min(kAhead - 2, nsteps - 2 - s));
-          __builtin_amdgcn_s_barrier();
-          __builtin_amdgcn_sched_barrier(0);
-          if (s + kAhead < nsteps) issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
-          read_k((j + 1) % kStages);
-        }
-        read_vt(j);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int nb = 0; nb < kRowBlocks; ++nb) nref[nb] = 0.f;
 
-        // softmax of step s: scores in the reference's rounding (the q.k sum
-        // rounded to bf16, times the scale, rounded again; the second
-        // rounding is exact and the scale moves into exp_c when the scale is
-        // a power of two)
-        const int key0 = (tile_begin + s * kSub) * kTileKeys;
-        v4f p[kRowBlocks][kSub];
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-#pragma unroll
-          for (int t = 0; t < kSub; ++t) {
-            if constexpr (kPow2Scale) {
-              p[nb][t] = round_bf16x4(sacc[nb][t]);
-            } else {
-#pragma unroll
-              for (int i = 0; i < 4; ++i) p[nb][t][i] = scaled_score<T>(sacc[nb][t][i], a.scale);
-            }
-          }
-        }
-        if (!step_full(key0)) mask_step(p, key0);
-        // The reference point m of a row moves only when one of its scores
-        // is more than kRescaleLog2 (in log2 units) above it, or it had none
-        // yet; each lane tests its own 16 scores, and only then is the row
-        // maximum formed across the lane groups (see softmax_step).
-        float lmax[kRowBlocks];
-        bool grow = false;
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-          float m0 = score_max(score_max(p[nb][0][0], p[nb][0][1]), p[nb][0][2]);
-          float m1 = score_max(score_max(p[nb][0][3], p[nb][1][0]), p[nb][1][1]);
-          m0 = score_max(score_max(m0, p[nb][1][2]), p[nb][1][3]);
-          m1 = score_max(score_max(m1, p[nb][2][0]), p[nb][2][1]);
-          m0 = score_max(score_max(m0, p[nb][2][2]), p[nb][2][3]);
-          m1 = score_max(score_max(m1, p[nb][3][0]), p[nb][3][1]);
-          m0 = score_max(score_max(m0, p[nb][3][2]), p[nb][3][3]);
-          lmax[nb] = score_max(m0, m1);
-          grow |= lmax[nb] != kNegInf && (st[nb].m == kNegInf || (lmax[nb] - st[nb].m) * exp_c > kRescaleLog2);
-        }
-        if (__ballot(grow)) {
-#pragma unroll
-          for (int nb = 0; nb < kRowBlocks; ++nb) {
-            const float m_new = score_max(st[nb].m, max_over_groups(lmax[nb]));
-            // alpha = 0 for a row without a reference yet (its O and sum are 0)
-            const float alpha = st[nb].m == kNegInf ? 0.f : fast_exp2((st[nb].m - m_new) * exp_c);
-            rowsum[nb] *= alpha;
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c) st[nb].o[c] *= alpha;
-            st[nb].m = m_new;
-          }
-        }
-        bf16x8_t pp[kRowBlocks][kSub / 2];
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-          // a row with nothing unmasked so far keeps m = -inf; 0 as the
-          // reference point makes its exponentials exact zeros, not NaN
-          const float nref = (st[nb].m == kNegInf) ? 0.f : -st[nb].m * exp_c;
-#pragma unroll
-          for (int t = 0; t < kSub; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) p[nb][t][i] = fast_exp2(fmaf(p[nb][t][i], exp_c, nref));
-          }
-#pragma unroll
-          for (int t = 0; t < kSub; t += 2) {
-            pp[nb][t / 2] = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
-                                        pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
-                                                    p[nb][t + 1][3]));
-          }
-        }
+    // Iteration s.  more: a step s+1 exists (its scores are issued here).
+    // Called with a literal `more`, so each call site is one straight-line
+    // tail in which the QK MFMAs of step s+1 and the P.V MFMAs of step s
+    // interleave with the exponentials of step s.
+    auto step = [&](int slot, int s, bool more) {
+      if (more) {
+        // step s+1 has landed for every wave (this wave's ops: at most
+        // those of the steps issued after it remain), and every wave has
+        // finished step s-1, whose stage the next fetch reuses
+        wait_dma_groups<kOwnOps, kAhead - 2>(min(kAhead - 2, nsteps - 2 - s));
+        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        wait_reads();
-        if (more) qk();  // scores of step s+1
-        // O^T += V^T . P^T and the row sums, two 16-key tiles per MFMA
+        if (s + kAhead < nsteps) issue((slot + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
+        read_k((slot + 1) % kStages);
+      }
+      read_vt(slot);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // softmax of step s: scores in the reference's rounding (the q.k sum
+      // rounded to bf16, times the scale, rounded again; the second rounding
+      // is exact and the scale moves into exp_c when the scale is a power of
+      // two)
+      const int key0 = (tile_begin + s * kSub) * kTileKeys;
+      v4f p[kRowBlocks][kSub];
 #pragma unroll
-        for (int t = 0; t < kSub; t += 2) {
+      for (int nb = 0; nb < kRowBlocks; ++nb) {
 #pragma unroll
-          for (int nb = 0; nb < kRowBlocks; ++nb) {
+        for (int t = 0; t < kSub; ++t) {
 #pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-              const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
-                                              __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
-              st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp[nb][t / 2], st[nb].o[c], 0, 0, 0);
-            }
-            rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
+          for (int i = 0; i < 4; ++i) {
+            p[nb][t][i] = kPow2Scale ? round_bf16_in_f32(sacc[nb][t][i]) : scaled_score<T>(sacc[nb][t][i], a.scale);
           }
         }
       }
+      if (!step_full(key0)) mask_step(p, key0);
+      // each lane tests its own 16 scores of a row; only when one of them
+      // moves the row's reference point is the row maximum formed across
+      // the lane groups (see softmax_step).  m = -inf gives +inf (a finite
+      // score grows it), a fully masked lane gives -inf or NaN (no growth).
+      float lmax[kRowBlocks];
+      bool grow = false;
+#pragma unroll
+      for (int nb = 0; nb < kRowBlocks; ++nb) {
+        float m0 = score_max(score_max(p[nb][0][0], p[nb][0][1]), p[nb][0][2]);
+        float m1 = score_max(score_max(p[nb][0][3], p[nb][1][0]), p[nb][1][1]);
+        m0 = score_max(score_max(m0, p[nb][1][2]), p[nb][1][3]);
+        m1 = score_max(score_max(m1, p[nb][2][0]), p[nb][2][1]);
+        m0 = score_max(score_max(m0, p[nb][2][2]), p[nb][2][3]);
+        m1 = score_max(score_max(m1, p[nb][3][0]), p[nb][3][1]);
+        m0 = score_max(score_max(m0, p[nb][3][2]), p[nb][3][3]);
+        lmax[nb] = score_max(m0, m1);
+        grow |= lmax[nb] - st[nb].m > grow_thr;
+      }
+      if (__ballot(grow)) {
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+          const float m_new = score_max(st[nb].m, max_over_groups(lmax[nb]));
+          // alpha = 0 for a row without a reference yet (its O and sum are 0)
+          const float alpha = st[nb].m == kNegInf ? 0.f : fast_exp2((st[nb].m - m_new) * exp_c);
+          rowsum[nb] *= alpha;
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) st[nb].o[c] *= alpha;
+          st[nb].m = m_new;
+          nref[nb] = m_new == kNegInf ? 0.f : -m_new * exp_c;
+        }
+      }
+      bf16x8_t pp[kRowBlocks][kSub / 2];
+#pragma unroll
+      for (int t = 0; t < kSub; t += 2) {
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int u = t; u < t + 2; ++u) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[nb][u][i] = fast_exp2(fmaf(p[nb][u][i], exp_c, nref[nb]));
+          }
+          pp[nb][t / 2] = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
+                                      pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
+                                                  p[nb][t + 1][3]));
+        }
+      }
+      wait_reads();
+      if (more) qk();  // scores of step s+1
+      // O^T += V^T . P^T and the row sums, two 16-key tiles per MFMA
+#pragma unroll
+      for (int t = 0; t < kSub; t += 2) {
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) {
+            const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
+                                            __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
+            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp[nb][t / 2], st[nb].o[c], 0, 0, 0);
+          }
+          rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
+        }
+      }
+    };
+
+    // every step but the last has a successor; the ring stage of the last
+    // is known only at run time (the reads take it from their base address)
+    for (int s0 = 0; s0 < nsteps - 1; s0 += kStages) {
+#pragma unroll
+      for (int j = 0; j < kStages; ++j) {
+        const int s = s0 + j;
+        if (s >= nsteps - 1) break;  // uniform over the workgroup
+        step(j, s, true);
+      }
     }
+    if (nsteps > 0) step((nsteps - 1) % kStages, nsteps - 1, false);
 #pragma unroll
     for (int nb = 0; nb < kRowBlocks; ++nb) st[nb].lsum = rowsum[nb][0];
   } else {
@@ -3477,10 +3509,10 @@ bool build_prefill_schedule(const PrefillPlan& p, int64_t num_seqs, const int64_
   for (size_t k = 0; k < p.tiles.size(); ++k) {
     const PrefillTile& t = p.tiles[k];
     const int64_t n = host_cu[t.r + 1] - host_cu[t.r];
-    if (t.pieces > 255 || host_cu[t.r] > 0x7fffffffLL || n > 0x7fffffffLL) return false;
-    sc->first_item[k] = (int32_t)t.first;
-    sc->nsplit[k] = (int32_t)t.pieces;
-    sc->req[k] = (int32_t)t.r;
+    if (t.r > 255 || t.pieces > 255 || t.first > 0xffff || host_cu[t.r] > 0x7fffffffLL || n > 0x7fffffffLL) {
+      return false;
+    }
+    sc->tile[k] = (uint32_t)t.r | (uint32_t)t.pieces << 8 | (uint32_t)t.first << 16;
     sc->q_begin[k] = (int32_t)host_cu[t.r];
     sc->q_len[k] = (int32_t)n;
     sc->ctx[k] = host_ctx[t.r];
@@ -3488,11 +3520,9 @@ bool build_prefill_schedule(const PrefillPlan& p, int64_t num_seqs, const int64_
   }
   for (size_t i = 0; i < p.order.size(); ++i) {
     const PrefillPiece& q = p.order[i];
-    if (q.begin > 0xffff || q.len > 255) return false;
-    sc->item_tile[i] = (uint8_t)q.tile;
-    sc->item_piece[i] = (uint8_t)q.piece;
-    sc->item_begin[i] = (uint16_t)q.begin;
-    sc->item_len[i] = (uint8_t)q.len;
+    if (q.tile > 255 || q.piece > 255 || q.len > 0xffff || q.begin < 0) return false;
+    sc->item[i] = (uint32_t)q.tile | (uint32_t)q.piece << 8 | (uint32_t)q.len << 16;
+    sc->item_begin[i] = (uint32_t)q.begin;
   }
   sc->count = (int32_t)p.order.size();
   return true;
