@@ -124,15 +124,6 @@ __device__ __forceinline__ float round_to_bf16(float x) {
   return (float)(__bf16)x;
 }
 
-// Rounds four floats to bf16 (round to nearest even): one v_cvt_pk_bf16_f32
-// per pair, then each half widened back.
-__device__ __forceinline__ v4f round_bf16x4(v4f v) {
-  const uint32_t lo = pack_bf16x2(v[0], v[1]);
-  const uint32_t hi = pack_bf16x2(v[2], v[3]);
-  return v4f{__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u), __uint_as_float(hi << 16),
-             __uint_as_float(hi & 0xffff0000u)};
-}
-
 // Rounds x to bf16 (round to nearest even) and returns the rounded value as
 // a float in one instruction: v_cvt_pk_bf16_f32 with 0 for the low half
 // leaves bf16(x) in the high half, which read as a float is the value itself.
@@ -1754,7 +1745,8 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s, tps, first_len); },
                 &b, &split, &first_item, &nsplit);
     if (b < 0) return;  // uniform over the workgroup
-    seq_len = a.seq_lens[b];
+    // lane b already holds the length of one of the first 64 sequences
+    seq_len = b < kWave ? __shfl(first_len, (int)b) : a.seq_lens[b];
   }
   seq_len = __builtin_amdgcn_readfirstlane(seq_len);
   const int tiles_per_split = (int)tps;
@@ -2051,7 +2043,9 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
   } else {
     int first_len;
     const int64_t tps = decode_call_tps(a, &first_len);
-    nsplit = decode_splits_of(a, b, tps, first_len);
+    // lane b already holds the length of one of the first 64 sequences
+    const int64_t len_b = b < kWave ? __shfl(first_len, (int)b) : a.seq_lens[b];
+    nsplit = len_b > 0 ? cdiv(cdiv(len_b, (int64_t)kTileKeys), tps) : (int64_t)0;
     for (int64_t s = lane_id(); s < b; s += kWave) first += decode_splits_of(a, s, tps, first_len);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) first += __shfl_xor(first, off);
