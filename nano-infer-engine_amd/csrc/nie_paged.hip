@@ -2520,10 +2520,14 @@ constexpr int prefill_stage_bytes() {
   return kPrefillStepTiles * 2 * GroupTile<T, D, 1>::kBytes;
 }
 
+// bf16 keeps a step's V in the ring one iteration longer than it fetches
+// ahead (the step's P.V runs in the next iteration), so it takes one stage
+// more: five at head_dim 64 (80 KiB, two workgroups per CU), four at 128.
 template <typename T, int D>
 constexpr int prefill_stages() {
   constexpr int fit = kPrefillLdsBudget / prefill_stage_bytes<T, D>();
-  return fit >= 4 ? 4 : (fit >= 2 ? fit : 2);
+  constexpr int want = Elt<T>::kIsBf16 ? 5 : 4;
+  return fit >= want ? want : (fit >= 2 ? fit : 2);
 }
 
 // Two 4-element bf16 operands (sub-tile a's keys, then sub-tile b's) as one
@@ -2854,7 +2858,10 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   };
 
   const int nsteps = (tile_end - tile_begin + kSub - 1) / kSub;
-  constexpr int kAhead = kStages - 1;
+  // steps fetched ahead of the one being consumed; bf16 holds one stage more
+  // for the V of the step whose P.V is still to run (see below)
+  constexpr int kAhead = Elt<T>::kIsBf16 ? kStages - 2 : kStages - 1;
+  static_assert(kAhead >= 1, "at least one step in flight");
   // only steps the item has are fetched
 #pragma unroll
   for (int j = 0; j < kAhead; ++j) {
@@ -2863,16 +2870,19 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 
   if constexpr (Elt<T>::kIsBf16) {
     // Software-pipelined steps.  Iteration s runs the softmax of step s on
-    // scores whose QK MFMAs were issued in iteration s-1, then issues the QK
-    // MFMAs of step s+1 and the P.V MFMAs of step s, so no instruction waits
-    // on an MFMA issued just before it, and a second wave on the SIMD fills
-    // the MFMA pipe while this one runs its softmax.  The row sums of P come
-    // from an MFMA with an all-ones A operand (the same bf16 P the P.V MFMAs
-    // consume), so the softmax has no per-score additions.  LDS reads use
-    // immediate offsets from two base addresses per stage.
+    // scores whose QK MFMAs were issued in iteration s-1.  The P.V MFMAs of
+    // step s-1 (its P kept from the previous iteration, its V still in the
+    // ring) run beside the rounding of step s, and the QK MFMAs of step s+1
+    // beside the exponentials of step s, so both VALU phases of a step have
+    // this wave's own MFMAs to overlap with and no MFMA waits on an
+    // instruction just before it.  The row sums of P come from an MFMA with
+    // an all-ones A operand (the same bf16 P the P.V MFMAs consume), so the
+    // softmax has no per-score additions.  LDS reads use immediate offsets
+    // from two base addresses per stage.
     constexpr int kKR = kSub * F::kVec;  // K reads per step
     constexpr int kVT = kSub * (D / 16);  // V^T reads per step
     static_assert(kKR % 4 == 0 && kVT % 4 == 0, "reads are waited for in groups of four");
+    static_assert(kStages >= kAhead + 2, "a step's V stays in the ring until its P.V has run");
     const uint32_t ring0 = lds_off(&ring[0][0]);
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, v4u{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
     v4f rowsum[kRowBlocks];
@@ -2896,12 +2906,16 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
       for (int c = 0; c < D / 16; ++c) base[c] = sb + vtr[c];
       ring_read_tr_at<kVT, D / 16, kTileStride>(vt, base);
     };
-    // every LDS read issued so far has landed (results pass through the asm)
-    auto wait_reads = [&]() {
+    // every LDS read issued so far has landed; the K (or V^T) operands pass
+    // through the asm, so nothing reads them before it and the other set's
+    // registers stay free to be reused
+    auto wait_k = [&]() {
 #pragma unroll
       for (int j = 0; j < kKR; j += 4) {
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kr[j]), "+v"(kr[j + 1]), "+v"(kr[j + 2]), "+v"(kr[j + 3]));
       }
+    };
+    auto wait_vt = [&]() {
 #pragma unroll
       for (int j = 0; j < kVT; j += 4) {
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[j]), "+v"(vt[j + 1]), "+v"(vt[j + 2]), "+v"(vt[j + 3]));
@@ -2927,7 +2941,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1));
     __builtin_amdgcn_s_barrier();
     read_k(0);
-    wait_reads();
+    wait_k();
     qk();
 
     // A row's reference point moves when one of its scores is more than
@@ -2939,22 +2953,40 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 #pragma unroll
     for (int nb = 0; nb < kRowBlocks; ++nb) nref[nb] = 0.f;
 
-    // Iteration s.  more: a step s+1 exists (its scores are issued here).
-    // Called with a literal `more`, so each call site is one straight-line
-    // tail in which the QK MFMAs of step s+1 and the P.V MFMAs of step s
-    // interleave with the exponentials of step s.
-    auto step = [&](int slot, int s, bool more) {
+    // O^T += V^T . P^T and the row sums for the P of one step (pp) and its
+    // V^T operands (vt), two 16-key tiles per MFMA
+    auto pv = [&](const bf16x8_t (&pp)[kRowBlocks][kSub / 2]) {
+#pragma unroll
+      for (int t = 0; t < kSub; t += 2) {
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) {
+            const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
+                                            __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
+            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp[nb][t / 2], st[nb].o[c], 0, 0, 0);
+          }
+          rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
+        }
+      }
+    };
+    bf16x8_t pp_prev[kRowBlocks][kSub / 2];  // P of the step whose P.V is still to run
+
+    // Iteration s in ring stage `slot`.  more: a step s+1 exists (its scores
+    // are issued here); prev: a step s-1 exists (its P.V runs here).  Both
+    // are literals at every call site, so each call is straight-line code.
+    auto step = [&](int slot, int s, bool more, bool prev) {
       if (more) {
         // step s+1 has landed for every wave (this wave's ops: at most
         // those of the steps issued after it remain), and every wave has
-        // finished step s-1, whose stage the next fetch reuses
+        // finished iteration s-1, so the stage the next fetch reuses (last
+        // read for step s-2's V) is free
         wait_dma_groups<kOwnOps, kAhead - 2>(min(kAhead - 2, nsteps - 2 - s));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         if (s + kAhead < nsteps) issue((slot + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
-        read_k((slot + 1) % kStages);
       }
-      read_vt(slot);
+      if (prev) read_vt((slot + kStages - 1) % kStages);
       __builtin_amdgcn_sched_barrier(0);
 
       // softmax of step s: scores in the reference's rounding (the q.k sum
@@ -2973,6 +3005,13 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
           }
         }
       }
+      if (prev) {
+        wait_vt();
+        pv(pp_prev);  // step s-1, against the reference points its P was formed with
+      }
+      // K of step s+1 (landed: waited for above), read only now so its
+      // registers are not held across the P.V of step s-1
+      if (more) read_k((slot + 1) % kStages);
       if (!step_full(key0)) mask_step(p, key0);
       // each lane tests its own 16 scores of a row; only when one of them
       // moves the row's reference point is the row maximum formed across
@@ -2993,6 +3032,8 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
         grow |= lmax[nb] - st[nb].m > grow_thr;
       }
       if (__ballot(grow)) {
+        // O and the sums hold every step up to s-1 (relative to the old
+        // reference points); they move to the new ones together
 #pragma unroll
         for (int nb = 0; nb < kRowBlocks; ++nb) {
           const float m_new = score_max(st[nb].m, max_over_groups(lmax[nb]));
@@ -3005,7 +3046,6 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
           nref[nb] = m_new == kNegInf ? 0.f : -m_new * exp_c;
         }
       }
-      bf16x8_t pp[kRowBlocks][kSub / 2];
 #pragma unroll
       for (int t = 0; t < kSub; t += 2) {
 #pragma unroll
@@ -3015,40 +3055,40 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) p[nb][u][i] = fast_exp2(fmaf(p[nb][u][i], exp_c, nref[nb]));
           }
-          pp[nb][t / 2] = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
-                                      pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
-                                                  p[nb][t + 1][3]));
+          pp_prev[nb][t / 2] = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
+                                           pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
+                                                       p[nb][t + 1][3]));
         }
       }
-      wait_reads();
-      if (more) qk();  // scores of step s+1
-      // O^T += V^T . P^T and the row sums, two 16-key tiles per MFMA
-#pragma unroll
-      for (int t = 0; t < kSub; t += 2) {
-#pragma unroll
-        for (int nb = 0; nb < kRowBlocks; ++nb) {
-#pragma unroll
-          for (int c = 0; c < D / 16; ++c) {
-            const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[t * (D / 16) + c]),
-                                            __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
-            st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp[nb][t / 2], st[nb].o[c], 0, 0, 0);
-          }
-          rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
-        }
+      if (more) {
+        wait_k();
+        qk();  // scores of step s+1
       }
     };
 
-    // every step but the last has a successor; the ring stage of the last
-    // is known only at run time (the reads take it from their base address)
-    for (int s0 = 0; s0 < nsteps - 1; s0 += kStages) {
+    // Step 0 has no predecessor and the last step no successor (its ring
+    // stage is known only at run time: the reads take it from their base
+    // address); the steps between run unrolled over the ring's stages.
+    if (nsteps > 1) step(0, 0, true, false);
+    for (int s0 = 1; s0 < nsteps - 1; s0 += kStages) {
 #pragma unroll
       for (int j = 0; j < kStages; ++j) {
         const int s = s0 + j;
         if (s >= nsteps - 1) break;  // uniform over the workgroup
-        step(j, s, true);
+        step((1 + j) % kStages, s, true, true);
       }
     }
-    if (nsteps > 0) step((nsteps - 1) % kStages, nsteps - 1, false);
+    if (nsteps == 1) {
+      step(0, 0, false, false);
+    } else if (nsteps > 1) {
+      step((nsteps - 1) % kStages, nsteps - 1, false, true);
+    }
+    // P.V of the last step
+    if (nsteps > 0) {
+      read_vt((nsteps - 1) % kStages);
+      wait_vt();
+      pv(pp_prev);
+    }
 #pragma unroll
     for (int nb = 0; nb < kRowBlocks; ++nb) st[nb].lsum = rowsum[nb][0];
   } else {
