@@ -2878,7 +2878,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     // instruction just before it.  The row sums of P come from an MFMA with
     // an all-ones A operand (the same bf16 P the P.V MFMAs consume), so the
     // softmax has no per-score additions.  LDS reads use immediate offsets
-    // from two base addresses per stage.
+    // from one base address per K vector and per 16-dim V^T chunk.
     constexpr int kKR = kSub * F::kVec;  // K reads per step
     constexpr int kVT = kSub * (D / 16);  // V^T reads per step
     static_assert(kKR % 4 == 0 && kVT % 4 == 0, "reads are waited for in groups of four");
