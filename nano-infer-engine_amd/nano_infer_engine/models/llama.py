@@ -20,6 +20,7 @@ from dataclasses import dataclass, field
 import torch
 from torch import nn
 
+from nano_infer_engine import _native
 from nano_infer_engine.layers import linear as _linear
 from nano_infer_engine.layers.decoder import Llama3Decoder
 from nano_infer_engine.layers.rms_norm import RmsNorm
@@ -137,8 +138,12 @@ class Llama3_2(nn.Module):
         x = self.embed(input_ids)
         # each block's output stays an unsummed pair (ffn_out, h); the next
         # norm adds it (one kernel for the add and the norm on the GPU)
+        lean = self._lean_stream(x)
         for layer_index, decoder in enumerate(self.decoders):
-            x = decoder.forward_tokens_unsummed(x, cache, layer_index, batch)
+            if lean is not None:
+                x = decoder.forward_tokens_lean(x, cache, layer_index, batch, lean)
+            else:
+                x = decoder.forward_tokens_unsummed(x, cache, layer_index, batch)
         if not isinstance(x, tuple):  # no layers
             x = (x, torch.zeros_like(x))
         ffn_out, h = x
@@ -151,6 +156,18 @@ class Llama3_2(nn.Module):
             if r is not None:
                 return r[1]
         return _linear.apply(self.lm_head, self.final_rms.forward_add(ffn_out, h)[1])
+
+    def _lean_stream(self, x: torch.Tensor) -> int | None:
+        """The current stream when every block can run ``forward_tokens_lean``
+        on x's rows, else None: a packed batch of more than the decode-step
+        GEMM's rows (a prefill step's; fewer rows keep the fused decode-step
+        kernels), on the GPU, without autograd."""
+        if (not x.is_cuda or x.dim() != 2 or x.shape[0] <= _native.LINEAR_MAX_ROWS or not x.is_contiguous()
+                or torch.is_grad_enabled()):
+            return None
+        if not all(decoder.lean_weights(x) for decoder in self.decoders):
+            return None
+        return _native._stream(x.device)
 
     def _new_cache_for(self, batch_size: int, seq_len: int, device: torch.device) -> tuple[PagedKVCache, tuple[str, ...]]:
         block_size = 16

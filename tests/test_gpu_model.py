@@ -468,3 +468,57 @@ def test_bf16_batched_decode_projections_match_torch_gemm():
     assert 0 < err <= 5e-2
     assert decisive.float().mean().item() >= 0.5
     assert torch.equal(hip.argmax(-1)[decisive], ref.argmax(-1)[decisive])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lean_prefill_blocks_match_generic_blocks(monkeypatch, dtype):
+    """A packed forward of more than 16 rows (two prefill chunks on cached
+    context plus a decode row) runs each block through forward_tokens_lean:
+    the norms, SiLU product and attention on this library's kernels, the
+    projections on torch's GEMM with stacked [q; k; v] and [gate; up]
+    weights.  The same call through the generic blocks (which stack the same
+    weights and call the same kernels through the module layer) gives the
+    same logits and cache bit for bit."""
+    _log(f"lean prefill blocks == generic blocks ({dtype})")
+    from nano_infer_engine.layers.decoder import Llama3Decoder
+    model = _model(dtype=dtype, hidden=512, q_heads=8, kv_heads=2, layers=3, vocab=256, max_seq_len=128, seed=6)
+    gen = torch.Generator().manual_seed(6)
+    ids = ("request-a", "request-b", "request-c")
+    prompts = [torch.randint(0, 256, (1, n), generator=gen).to(DEV) for n in (40, 21, 9)]
+    lengths = (24, 31, 1)
+    flat = torch.randint(0, 256, (sum(lengths),), generator=gen).to(DEV)
+    bounds = torch.tensor([0, 24, 55, 56], device=DEV)
+
+    lean_calls = []
+    original = Llama3Decoder.forward_tokens_lean
+
+    def spy(self, *args, **kwargs):
+        lean_calls.append(1)
+        return original(self, *args, **kwargs)
+
+    monkeypatch.setattr(Llama3Decoder, "forward_tokens_lean", spy)
+
+    def run():
+        cache = _cache_for(model, 24, block_size=8)
+        with torch.inference_mode():
+            for p, sid in zip(prompts, ids):
+                model(p, kv_cache=cache, sequence_ids=(sid,))
+            lean_calls.clear()
+            logits = model.forward_ragged(flat, kv_cache=cache, sequence_ids=ids, query_start_loc=bounds)
+        torch.cuda.synchronize()
+        return logits, cache
+
+    lean_logits, lean_cache = run()
+    assert len(lean_calls) == model.config.num_layers
+    with monkeypatch.context() as m:
+        m.setattr(Llama3_2, "_lean_stream", lambda self, x: None)
+        generic_logits, generic_cache = run()
+    assert not lean_calls
+    assert torch.equal(lean_logits, generic_logits)
+    for sid in ids:
+        n = lean_cache.get_sequence_length(sid)
+        assert n == generic_cache.get_sequence_length(sid)
+        for layer in range(model.config.num_layers):
+            lk, lv = lean_cache.gather(layer, sid, n)
+            gk, gv = generic_cache.gather(layer, sid, n)
+            assert torch.equal(lk, gk) and torch.equal(lv, gv)
