@@ -3216,7 +3216,11 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 // ... for larger head_dim) of row l/16.  Every split's loads of a batch of
 // up to kBatch splits are issued before any is used, so the usual merge is
 // one memory round trip; batches combine through a running maximum per row
-// (exact log-sum-exp weights, splits in order).
+// (exact log-sum-exp weights, splits in order).  kBatch is the launch's
+// largest split count rounded up to 4, 8 or 16: the batch's registers set
+// how many merge workgroups a CU holds (234 VGPRs for 21 splits at head_dim
+// 64 allow one, so the 384 to 544 workgroups of a serving step's prefill
+// merge ran in two or three rounds: 9-12 us against 4-5 us in one).
 constexpr int kPrefillMergeWaves = 8;
 constexpr int kPrefillMergeRows = kPrefillMergeWaves * 4;
 
@@ -3241,12 +3245,12 @@ struct PrefillMergeJobs {
   int32_t nsplit_tokens[kMaxMergeJobs];  // nsplit << 16 | tokens
 };
 
-template <typename T, int D, int kRowBlocks>
+template <typename T, int D, int kRowBlocks, int kBatch>
 __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a,
                                                                                  PrefillMergeJobs jobs) {
   constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
   constexpr int kChunkPasses = D / 64;  // 4-dim chunks per lane
-  constexpr int kBatch = 64 / (3 * kChunkPasses);  // splits per round trip (register budget)
+  static_assert(kBatch >= 1, "splits per round trip");
   const int tpt = a.tokens_per_tile;
   // (query tile, KV head, row group) of this workgroup, head-major over the
   // XCDs like the prefill items whose partials it reads
@@ -3289,7 +3293,14 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
   const int tpb = 16 / a.group;
   const int tq = (rr / 16) * tpb + (rr % 16) / a.group;  // token within the tile
   const int64_t split_stride = (int64_t)a.geom.kv_heads * kRows;  // rows between consecutive items
-  const int64_t slot0 = (first * a.geom.kv_heads + h) * kRows + rr;
+  // split s of this row: the uniform base of slot (first + s, h) plus a
+  // lane offset shared by every split, so each load needs no address
+  // registers of its own (scalar base, 32-bit vector offset)
+  const int64_t row0_first = (first * a.geom.kv_heads + h) * kRows;
+  const float* o_first = a.ws_o + row0_first * D;
+  const float* ml_first = a.ws_ml + row0_first * 2;
+  const uint32_t o_lane = (uint32_t)(rr * D + 4 * chunk);
+  const uint32_t ml_lane = (uint32_t)(rr * 2);
 
   float run_max = kNegInf, denom = 0.f;
   float4 acc[kChunkPasses];
@@ -3301,12 +3312,12 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       const bool in = s0 + b < nsplit;
-      const int64_t slot = slot0 + (s0 + b) * split_stride;
-      ml[b] = in ? *reinterpret_cast<const float2*>(a.ws_ml + slot * 2) : make_float2(kNegInf, 0.f);
+      const int64_t split_row = (int64_t)(s0 + b) * split_stride;  // uniform
+      const float* ob = o_first + split_row * D;
+      ml[b] = in ? *reinterpret_cast<const float2*>(ml_first + split_row * 2 + ml_lane) : make_float2(kNegInf, 0.f);
 #pragma unroll
       for (int c = 0; c < kChunkPasses; ++c) {
-        v[b][c] = in ? *reinterpret_cast<const float4*>(a.ws_o + slot * D + 4 * (chunk + 16 * c))
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[b][c] = in ? *reinterpret_cast<const float4*>(ob + o_lane + 64 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
     float bmax = ml[0].x;
@@ -3379,6 +3390,7 @@ struct PrefillPlan {
   int64_t qtiles = 0;  // merge grid.x: the query-tile count (exact, else a bound)
   int64_t rows = 0;    // rows per item
   bool split = false;  // some query tile is split over several items
+  int64_t max_split = 0;  // items of the most-split query tile (a bound without host metadata)
   // host metadata: the query tiles and the items in dispatch order
   std::vector<PrefillTile> tiles;
   std::vector<PrefillPiece> order;
@@ -3447,6 +3459,7 @@ bool plan_balanced(PrefillPlan& p, int64_t kv_heads) {
     }
   }
   if (pieces.size() > (size_t)kMaxSchedItems || splits > kMaxMergeJobs) return false;
+  p.max_split = *std::max_element(n.begin(), n.end());
   // the ncu largest in ascending order, then the rest in descending order:
   // dispatch position k < ncu and k + ncu share a CU
   std::vector<PrefillPiece> by_size(pieces);
@@ -3500,6 +3513,7 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
       t.first = first;
       first += t.pieces;
       p.split |= t.pieces > 1;
+      p.max_split = std::max(p.max_split, t.pieces);
       for (int64_t j = 0; j < t.pieces; ++j) {
         const int64_t begin = j * p.tps;
         p.order.push_back(PrefillPiece{(int32_t)i, (int32_t)j, (int32_t)begin,
@@ -3516,6 +3530,7 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
   p.items = work / p.tps + qtiles + 1;  // sum ceil(n / tps) <= sum n / tps + count
   p.qtiles = qtiles;
   p.split = ktiles > p.tps;
+  p.max_split = cdiv(ktiles, p.tps);
   return p;
 }
 
@@ -3870,7 +3885,18 @@ void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const Prefill
     PrefillArgs m = a;
     m.merge_tiles = (int32_t)(jobs.count > 0 ? jobs.count : p.qtiles);
     const dim3 grid((unsigned)(m.merge_tiles * a.geom.kv_heads * (prefill_rows_per_item<NB>() / kPrefillMergeRows)));
-    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB>), grid, dim3(kPrefillMergeWaves * kWave), 0, stream, m, jobs);
+    const dim3 block(kPrefillMergeWaves * kWave);
+    // splits per round trip: the call's largest split count, in steps of
+    // 4, 8, 16 (8 at head_dim 128); more splits take several round trips
+    if (p.max_split <= 4) {
+      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 4>), grid, block, 0, stream, m, jobs);
+    } else if constexpr (D > 64) {
+      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 8>), grid, block, 0, stream, m, jobs);
+    } else if (p.max_split <= 8) {
+      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 8>), grid, block, 0, stream, m, jobs);
+    } else {
+      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 16>), grid, block, 0, stream, m, jobs);
+    }
   }
 }
 
