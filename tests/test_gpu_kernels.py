@@ -486,6 +486,23 @@ def test_varlen_prefill_mixed_batch(dtype, host_plan):
     assert err <= TOL[dtype]
 
 
+@pytest.mark.parametrize("context,query", [(300, 16), (600, 8), (1000, 40), (20000, 16)])
+@pytest.mark.parametrize("host_plan", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_varlen_prefill_merge_batches(dtype, host_plan, context, query):
+    """One request over one KV head, its keys split into about 3, 5, 9 and
+    157 pieces (8 key tiles each): the merge loads its splits in batches of
+    4, 8 or 16 chosen from the call's largest split count, and 157 splits
+    take ten batches of 16 combined through the running maximum."""
+    _log(f"varlen merge batches ctx={context} q={query} {dtype} host_plan={host_plan}")
+    wl = workloads.ragged([context], [query], seed=31, pool_factor=1.2, q_heads=4, kv_heads=1, head_dim=64,
+                          block_size=16)
+    got, want = _prefill_case(wl, dtype, host_plan)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
 @pytest.mark.parametrize(
     "q_heads,kv_heads,head_dim,block_size",
     [(4, 4, 64, 16), (4, 2, 64, 2), (8, 1, 64, 4), (16, 1, 64, 16), (32, 2, 128, 32), (8, 4, 128, 5)],
