@@ -68,18 +68,35 @@ class Llama3Decoder(nn.Module):
         return ((a.q_proj, a.k_proj, a.v_proj, a.o_proj, f.gate_proj, f.up_proj, f.down_proj),
                 (self.pre_norm, self.post_norm))
 
+    def _lean_key(self, x: torch.Tensor) -> tuple:
+        """What the cached lean weights depend on: x's dtype and device and,
+        per projection and norm, its weight's identity, storage and version,
+        whether it has a bias, and the norms' eps.  Read from the module and
+        parameter dicts (every prefill-sized forward checks all blocks, and
+        nn.Module attribute lookups would cost more than the check)."""
+        mods = self._modules
+        attn, ffn = mods["attn"]._modules, mods["ffn"]._modules
+        pre, post = mods["pre_norm"], mods["post_norm"]
+        key = [x.dtype, x.device, pre.eps, post.eps]
+        for m in (attn["q_proj"], attn["k_proj"], attn["v_proj"], attn["o_proj"], ffn["gate_proj"], ffn["up_proj"],
+                  ffn["down_proj"], pre, post):
+            params = m._parameters
+            w = params.get("weight")
+            key += (None, 0, 0) if w is None else (id(w), w.data_ptr(), w._version)
+            key.append(params.get("bias") is not None)
+        return tuple(key)
+
     def lean_weights(self, x: torch.Tensor) -> bool:
         """Whether ``forward_tokens_lean`` takes x's rows: bias-free projections
         and weighted norms of x's dtype on x's device, in shapes the norm and
         SiLU-product kernels take.  Rebuilds the cached weights when one of
         the block's parameters was replaced or modified since."""
-        linears, norms = self._lean_params()
-        key = (x.dtype, x.device) + tuple((m.weight.data_ptr(), m.weight._version) for m in linears + norms) + \
-            tuple(n.eps for n in norms)
+        key = self._lean_key(x)
         cached = self._lean
         if cached is not None and cached.key == key:
             return True
         self._lean = None
+        linears, norms = self._lean_params()
         if any(m.bias is not None for m in linears) or any(n.weight is None for n in norms):
             return False
         ws = [m.weight for m in linears] + [n.weight for n in norms]

@@ -522,3 +522,33 @@ def test_lean_prefill_blocks_match_generic_blocks(monkeypatch, dtype):
             lk, lv = lean_cache.gather(layer, sid, n)
             gk, gv = generic_cache.gather(layer, sid, n)
             assert torch.equal(lk, gk) and torch.equal(lv, gv)
+
+
+def test_lean_prefill_blocks_follow_weight_changes(monkeypatch):
+    """The lean blocks' cached weights follow the parameters: after an
+    in-place change of one projection and after a projection's weight is
+    replaced, a 40-row forward gives the generic blocks' logits bit for bit,
+    and different logits than before the change."""
+    _log("lean prefill blocks follow weight changes")
+    model = _model(dtype=torch.bfloat16, hidden=512, q_heads=8, kv_heads=2, layers=2, vocab=256, max_seq_len=64, seed=8)
+    prompt = torch.randint(0, 256, (1, 40), generator=torch.Generator().manual_seed(8)).to(DEV)
+
+    def run(lean):
+        with monkeypatch.context() as m:
+            if not lean:
+                m.setattr(Llama3_2, "_lean_stream", lambda self, x: None)
+            cache = _cache_for(model, 8, block_size=8)
+            with torch.inference_mode():
+                out = model(prompt, kv_cache=cache, sequence_ids=("s",))
+            torch.cuda.synchronize()
+            return out
+
+    before = run(True)
+    with torch.no_grad():
+        model.decoders[1].attn.o_proj.weight.mul_(1.5)
+    changed = run(True)
+    assert torch.equal(changed, run(False)) and not torch.equal(changed, before)
+    down = model.decoders[0].ffn.down_proj
+    down.weight = torch.nn.Parameter(down.weight.detach() * 0.5)
+    replaced = run(True)
+    assert torch.equal(replaced, run(False)) and not torch.equal(replaced, changed)

@@ -605,3 +605,32 @@ def test_library_rejects_bad_decoder_and_fused_arguments():
     assert lib.nie_paged_decode_append(*base, None, 512, p, 512, None, None, 0, *rest) < 0  # no new keys
     assert lib.nie_paged_decode_append(*base, p, 512, p, 512, p, None, 4, *rest) < 0  # one table
     assert b"RoPE" in lib.nie_last_error()
+
+
+def test_lean_weight_key_follows_parameters_and_tolerates_weightless_norms():
+    """The key that keeps a block's cached lean weights valid changes when a
+    weight is modified in place, replaced, or given a bias, or when a norm's
+    eps changes; a block with a weightless norm is simply not taken (on the
+    CPU no block is: the lean path needs the HIP kernels)."""
+    from torch import nn
+
+    from nano_infer_engine.layers.decoder import Llama3Decoder
+    from nano_infer_engine.layers.rms_norm import RmsNorm
+
+    d = Llama3Decoder(1e-5, 4, 2, 64, 128)
+    x = torch.zeros(3, 64)
+    keys = [d._lean_key(x)]
+    assert d._lean_key(x) == keys[0]
+    with torch.no_grad():
+        d.attn.o_proj.weight.mul_(2)
+    keys.append(d._lean_key(x))
+    d.ffn.up_proj.weight = nn.Parameter(d.ffn.up_proj.weight.detach().clone())
+    keys.append(d._lean_key(x))
+    d.attn.k_proj.bias = nn.Parameter(torch.zeros(d.attn.k_proj.weight.shape[0]))
+    keys.append(d._lean_key(x))
+    d.post_norm.eps = 1e-6
+    keys.append(d._lean_key(x))
+    keys.append(d._lean_key(x.to(torch.bfloat16)))
+    assert len(set(keys)) == len(keys)
+    d.pre_norm = RmsNorm(64, elementwise_affine=False)
+    assert d.lean_weights(x) is False
