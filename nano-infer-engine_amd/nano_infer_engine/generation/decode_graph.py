@@ -8,12 +8,15 @@ graph capture of stable decode shapes as future work
 norm, LM head and the greedy argmax — is captured once per (batch size,
 length bucket) and replayed:
 
-* the step's inputs live in static device buffers: token IDs, block tables
-  (width = bucket / block_size), context and sequence lengths, slot mapping
-  and positions; their pinned host staging persists with the capture, its
-  tables updated in place (:class:`~nano_infer_engine.paged_batch.TableMirror`:
-  only a sequence's new blocks, or a row that changed hands), and one
-  host-to-device copy per buffer refreshes the device side per step;
+* the step's inputs live in one static device buffer: slot mapping,
+  positions, ``cu_seqlens`` and token IDs (int64), block tables (width =
+  bucket / block_size) and context and sequence lengths (int32); its pinned
+  host staging persists with the capture, its tables updated in place
+  (:class:`~nano_infer_engine.paged_batch.TableMirror`: only a sequence's new
+  blocks, or a row that changed hands), and one host-to-device copy
+  refreshes the device side per step (the token IDs included when the
+  caller has them on the host, as the scheduler does after reading the last
+  step's tokens);
 * the decode launch inside the graph is planned for the bucket
   (:func:`~nano_infer_engine.paged_batch.decode_plan_bound`), exactly as the
   eager step plans it, so a replay computes the same values as the eager
@@ -42,11 +45,12 @@ from nano_infer_engine.paged_cache import PagedKVCache
 class _CapturedStep:
     graph: torch.cuda.CUDAGraph
     batch: RaggedBatch
-    ids: torch.Tensor  # (B,) int64 input token IDs
-    ints: torch.Tensor  # device: tables (B*W), context lens (B), sequence lens (B)
-    longs: torch.Tensor  # device: slots (B), positions (B), cu_seqlens (B + 1)
-    ints_host: torch.Tensor  # pinned staging of ``ints``
-    longs_host: torch.Tensor  # pinned staging of ``longs``
+    meta: torch.Tensor  # device bytes: ``longs``, ``ids``, then ``ints``
+    ids: torch.Tensor  # (B,) int64 input token IDs (a view of ``meta``)
+    meta_host: torch.Tensor  # pinned staging of ``meta``
+    ints_np: np.ndarray  # staging views: tables (B*W), context lens (B), sequence lens (B)
+    longs_np: np.ndarray  # slots (B), positions (B), cu_seqlens (B + 1)
+    ids_np: np.ndarray  # token IDs (B)
     width: int
     copied: torch.cuda.Event  # recorded after the staging copies of the last step
     logits: torch.Tensor  # (B, vocab) output of the last replay
@@ -91,9 +95,13 @@ class DecodeGraphRunner:
     def _capture(self, batch_size: int, bound: int) -> _CapturedStep:
         cache, model = self.cache, self.model
         b, width = batch_size, -(-bound // cache.block_size)
-        ints = torch.zeros(b * width + 2 * b, dtype=torch.int32, device=self.device)
-        longs = torch.zeros(3 * b + 1, dtype=torch.int64, device=self.device)
-        ids = torch.zeros(b, dtype=torch.int64, device=self.device)
+        # one buffer, so a step's inputs are one copy: int64 slots, positions,
+        # cu_seqlens and token IDs first (8-byte aligned), then the int32s
+        n_long, n_int = 4 * b + 1, b * width + 2 * b
+        meta = torch.zeros(8 * n_long + 4 * n_int, dtype=torch.uint8, device=self.device)
+        longs = meta[: 8 * (3 * b + 1)].view(torch.int64)
+        ids = meta[8 * (3 * b + 1) : 8 * n_long].view(torch.int64)
+        ints = meta[8 * n_long :].view(torch.int32)
         # capture-time contents: length-1 sequences at position 0 whose
         # table entries lie outside the pool and whose slots are -1, so the
         # K/V writes of the warm-up and capture runs are skipped (the fused
@@ -132,14 +140,17 @@ class DecodeGraphRunner:
                 _native.argmax_rows(logits, out=next_ids)
         torch.cuda.current_stream(self.device).wait_stream(stream)
         self.captures += 1
+        meta_host = torch.empty(meta.shape, dtype=torch.uint8, pin_memory=True)
+        staged = meta_host.numpy()
         return _CapturedStep(
             graph=graph,
             batch=batch,
+            meta=meta,
             ids=ids,
-            ints=ints,
-            longs=longs,
-            ints_host=torch.empty(ints.shape, dtype=ints.dtype, pin_memory=True),
-            longs_host=torch.empty(longs.shape, dtype=longs.dtype, pin_memory=True),
+            meta_host=meta_host,
+            ints_np=staged[8 * n_long :].view(np.int32),
+            longs_np=staged[: 8 * (3 * b + 1)].view(np.int64),
+            ids_np=staged[8 * (3 * b + 1) : 8 * n_long].view(np.int64),
             width=width,
             copied=torch.cuda.Event(),
             logits=logits,
@@ -149,22 +160,27 @@ class DecodeGraphRunner:
 
     # ------------------------------------------------------------------ step
     @torch.inference_mode()
-    def step(self, token_ids: torch.Tensor, sequence_ids: tuple[str, ...]) -> tuple[torch.Tensor, torch.Tensor]:
+    def step(self, token_ids: torch.Tensor | None, sequence_ids: tuple[str, ...],
+             host_ids: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """Append one token per sequence and run the model: returns (logits (B, vocab), next IDs (B,)).
 
         Both are views of static buffers, valid until the next call with the
         same batch size and bucket.  Validation and cache bookkeeping follow
-        the eager path (``Llama3_2._forward_packed``).
+        the eager path (``Llama3_2._forward_packed``).  ``host_ids``: the
+        token IDs as a host list, in place of ``token_ids`` (None); they then
+        travel with the step's metadata copy instead of in a device copy.
+        ``sequence_ids`` must be the scheduler's checked IDs.
         """
         cache, config = self.cache, self.model.config
         b = len(sequence_ids)
-        if token_ids.numel() != b:
+        given = len(host_ids) if host_ids is not None else (-1 if token_ids is None else token_ids.numel())
+        if given != b:
             raise ValueError("one token per sequence is required")
-        context = [cache.get_sequence_length(s) for s in sequence_ids]
-        for s, ctx in zip(sequence_ids, context):
+        context = cache._lengths(sequence_ids)
+        for ctx in context:
             if ctx + 1 > config.max_seq_len:
                 raise ValueError(f"Sequence length {ctx + 1} exceeds max_seq_len={config.max_seq_len}")
-            cache.ensure_capacity(s, ctx + 1)
+        rows = cache._reserve_next(sequence_ids, context)
         bound = decode_plan_bound(max(context) + 1)
         if not self.supports(b, max(context) + 1):
             raise ValueError("batch size or sequence length outside the captured range")
@@ -187,24 +203,24 @@ class DecodeGraphRunner:
         # step's copies out of them have run), then one copy each
         step.copied.synchronize()
         bs, width = cache.block_size, step.width
-        ints = step.ints_host.numpy()
-        longs = step.longs_host.numpy()
+        ints, longs = step.ints_np, step.longs_np
         tables = ints[: b * width].reshape(b, width)
         # only the table entries that changed since this capture's last
         # replay are rewritten (a new block per sequence every block_size steps)
-        step.mirror.fill(tables, [cache._row(s) for s in sequence_ids])
+        step.mirror.fill(tables, rows)
         ctx = np.asarray(context, dtype=np.int64)
         ints[b * width : b * width + b] = ctx
         ints[b * width + b :] = ctx + 1
         longs[:b] = tables[np.arange(b), ctx // bs].astype(np.int64) * bs + ctx % bs
         longs[b : 2 * b] = ctx
         longs[2 * b :] = np.arange(b + 1)
-        step.ints.copy_(step.ints_host, non_blocking=True)
-        step.longs.copy_(step.longs_host, non_blocking=True)
+        if host_ids is not None:
+            step.ids_np[:] = host_ids
+        step.meta.copy_(step.meta_host, non_blocking=True)
         step.copied.record()
-        step.ids.copy_(token_ids.reshape(-1))
+        if host_ids is None:
+            step.ids.copy_(token_ids.reshape(-1))
         step.graph.replay()
         self.replays += 1
-        for s in sequence_ids:
-            cache.advance(s, 1)
+        cache._advance_reserved(sequence_ids)
         return step.logits, step.next_ids

@@ -62,6 +62,7 @@ class StepPlan:
     pieces: list[tuple[PagedRequest, int, int]] = field(default_factory=list)  # (request, start, stop) of its prompt
     decode: list[PagedRequest] = field(default_factory=list)
     decode_tokens: list[torch.Tensor] = field(default_factory=list)  # (1, 1) next-token views, one per decode row
+    decode_ids: list[int] = field(default_factory=list)  # the same tokens on the host
 
     @property
     def requests(self) -> list[PagedRequest]:
@@ -362,7 +363,7 @@ class ContinuousBatchingScheduler:
         tokens, ids, events = self._greedy_tokens()
         keep = self._retire_finished(ids, terminal)
         plan = StepPlan(decode=[self.active_requests[i] for i in keep],
-                        decode_tokens=[tokens[i : i + 1] for i in keep])
+                        decode_tokens=[tokens[i : i + 1] for i in keep], decode_ids=[ids[i] for i in keep])
         self.active_requests = list(plan.decode)
         plan.pieces = self._cut_prompt_pieces()
         return plan, events
@@ -370,14 +371,15 @@ class ContinuousBatchingScheduler:
     def _graph_eligible(self, plan: StepPlan) -> bool:
         if self._graphs is None or plan.pieces or not plan.decode:
             return False
-        longest = max(self.paged_cache.get_sequence_length(r.sequence_id) for r in plan.decode) + 1
+        longest = max(self.paged_cache._lengths([r.sequence_id for r in plan.decode])) + 1
         return self._graphs.supports(len(plan.decode), longest)
 
     def _run_plan(self, plan: StepPlan) -> torch.Tensor:
         """The plan's forward; one logits row per planned request, in plan order."""
         self._graph_step = None
         if self._graph_eligible(plan):
-            logits, next_ids = self._graphs.step(torch.cat(plan.decode_tokens).view(-1), plan.sequence_ids)
+            # the host IDs travel with the step's metadata copy
+            logits, next_ids = self._graphs.step(None, plan.sequence_ids, host_ids=plan.decode_ids)
             self._graph_step = (tuple(plan.decode), next_ids)
             return logits
         return paged_prefill_chunks(self.model, plan.chunks(), self.paged_cache, plan.sequence_ids)

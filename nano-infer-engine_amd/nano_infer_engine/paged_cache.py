@@ -175,6 +175,34 @@ class PagedKVCache:
         """The sequence's table object; KeyError if unknown."""
         return self._block_tables[sequence_id]
 
+    def _lengths(self, sequence_ids) -> list[int]:
+        """``get_sequence_length`` of each ID, for callers whose IDs are
+        already checked (a decode step's requests)."""
+        lengths = self._sequence_lengths
+        return [lengths.get(s, 0) for s in sequence_ids]
+
+    def _reserve_next(self, sequence_ids, lengths) -> list[BlockRow]:
+        """``ensure_capacity(s, n + 1)`` for each sequence ``s`` of length
+        ``n``, for already-checked IDs; returns their table objects.  Only a
+        sequence whose last block is full (or that has none) goes through
+        ``ensure_capacity`` and the allocator; the others need no change."""
+        tables, bs = self._block_tables, self.block_size
+        rows = []
+        for s, n in zip(sequence_ids, lengths):
+            row = tables.get(s)
+            if row is None or n >= row.n * bs:
+                self.ensure_capacity(s, n + 1)
+                row = tables[s]
+            rows.append(row)
+        return rows
+
+    def _advance_reserved(self, sequence_ids) -> None:
+        """``advance(s, 1)`` for sequences whose next position
+        ``_reserve_next`` has made room for."""
+        lengths = self._sequence_lengths
+        for s in sequence_ids:
+            lengths[s] += 1
+
     def _resolve_position(self, sequence_id: str, token_position: int) -> tuple[int, int]:
         """(physical block, offset) of a logical token position."""
         if not _is_int(token_position):

@@ -76,7 +76,9 @@ def _cache(model, num_blocks=256):
 @pytest.mark.parametrize("dtype,max_graphs", [(torch.float32, 64), (torch.bfloat16, 64), (torch.bfloat16, 1)])
 def test_decode_graph_replays_match_eager_step(dtype, max_graphs):
     """Replays equal eager steps; captures share one memory pool, and with
-    max_graphs=1 every new (batch, bucket) key evicts the previous capture."""
+    max_graphs=1 every new (batch, bucket) key evicts the previous capture.
+    Odd steps pass the token IDs as a host list (they travel with the
+    metadata copy), even steps as the device tensor."""
     _log(f"decode graph vs eager {dtype} max_graphs={max_graphs}")
     model = _graph_model(dtype)
     gen = torch.Generator(device=DEV).manual_seed(1)
@@ -94,7 +96,10 @@ def test_decode_graph_replays_match_eager_step(dtype, max_graphs):
         if step == 14:  # one sequence leaves: a new batch size
             active, tokens = active[:2], tokens[:2]
         with torch.inference_mode():
-            g_logits, g_next = runner.step(tokens, tuple(active))
+            if step % 2:
+                g_logits, g_next = runner.step(None, tuple(active), host_ids=tokens.tolist())
+            else:
+                g_logits, g_next = runner.step(tokens, tuple(active))
             g_logits, g_next = g_logits.clone(), g_next.clone()
             e_logits = paged_prefill_chunks(model, tuple(t.view(1, 1) for t in tokens), eager_cache, tuple(active))
         if step % 5 == 0:

@@ -634,3 +634,37 @@ def test_lean_weight_key_follows_parameters_and_tolerates_weightless_norms():
     assert len(set(keys)) == len(keys)
     d.pre_norm = RmsNorm(64, elementwise_affine=False)
     assert d.lean_weights(x) is False
+
+
+def test_decode_step_bookkeeping_fast_path_matches_public_methods():
+    """The graph runner's per-step bookkeeping (_lengths, _reserve_next,
+    _advance_reserved) leaves the cache as get_sequence_length,
+    ensure_capacity(s, n + 1) and advance(s, 1) do: the same lengths, block
+    tables and allocator order, over steps that cross block boundaries and
+    with sequences that start empty."""
+    public = PagedKVCache(64, 4, 1, 1, 8, torch.float32, torch.device("cpu"))
+    fast = PagedKVCache(64, 4, 1, 1, 8, torch.float32, torch.device("cpu"))
+    for c in (public, fast):
+        c.ensure_capacity("a", 6)
+        c.advance("a", 6)
+        c.ensure_capacity("b", 1)
+        c.advance("b", 1)
+    ids = ["a", "b"]
+    for step in range(40):
+        if step == 7:
+            ids = ids + ["c"]  # a sequence with no table yet
+        lengths = [public.get_sequence_length(s) for s in ids]
+        for s, n in zip(ids, lengths):
+            public.ensure_capacity(s, n + 1)
+        for s in ids:
+            public.advance(s, 1)
+        got = fast._lengths(ids)
+        assert got == lengths
+        rows = fast._reserve_next(ids, got)
+        assert [r.view().tolist() for r in rows] == [list(public.get_block_table(s)) for s in ids]
+        fast._advance_reserved(ids)
+        for s in ids:
+            assert fast.get_sequence_length(s) == public.get_sequence_length(s)
+            assert fast.get_block_table(s) == public.get_block_table(s)
+    assert fast.allocator.free_block_count == public.allocator.free_block_count
+    assert fast.allocator.allocate(3) == public.allocator.allocate(3)
