@@ -27,7 +27,8 @@ class PagedRequest:
     status: RequestStatus = RequestStatus.PENDING
     error: Exception | None = None
     # the prompt and the tokens generated so far: a joined (1, n) prefix plus
-    # (1, 1) token views not yet joined (see `sequence`)
+    # tokens not yet joined (see `sequence`): (1, 1) tensors, or (tokens,
+    # row) pairs naming row `row` of a step's (n, 1) tokens
     _joined: torch.Tensor | None = field(init=False, default=None, repr=False, compare=False)
     _pending: list = field(init=False, default_factory=list, repr=False, compare=False)
 
@@ -42,7 +43,8 @@ class PagedRequest:
         concatenation, instead of one device copy per token and step.
         """
         if self._pending:
-            self._joined = torch.cat((self._joined, *self._pending), dim=1)
+            parts = [p if isinstance(p, torch.Tensor) else p[0][p[1] : p[1] + 1] for p in self._pending]
+            self._joined = torch.cat((self._joined, *parts), dim=1)
             self._pending = []
         return self._joined
 
@@ -54,3 +56,8 @@ class PagedRequest:
     def append_token(self, token: torch.Tensor) -> None:
         """Appends a generated token, a (1, 1) tensor (kept as given until `sequence` is read)."""
         self._pending.append(token)
+
+    def _append_row(self, tokens: torch.Tensor, row: int) -> None:
+        """Appends row ``row`` of a step's (n, 1) tokens, sliced only when
+        `sequence` is read (a decode step's requests each take one row)."""
+        self._pending.append((tokens, row))

@@ -61,8 +61,15 @@ class StepPlan:
 
     pieces: list[tuple[PagedRequest, int, int]] = field(default_factory=list)  # (request, start, stop) of its prompt
     decode: list[PagedRequest] = field(default_factory=list)
-    decode_tokens: list[torch.Tensor] = field(default_factory=list)  # (1, 1) next-token views, one per decode row
+    decode_src: torch.Tensor | None = None  # (n, 1) tokens the decode rows take their next token from
+    decode_rows: list[int] = field(default_factory=list)  # the row of decode_src of each decode request
     decode_ids: list[int] = field(default_factory=list)  # the same tokens on the host
+
+    @property
+    def decode_tokens(self) -> list[torch.Tensor]:
+        """The decode rows' next tokens, (1, 1) views (built when an eager
+        forward needs them; a graph replay takes ``decode_ids``)."""
+        return [self.decode_src[i : i + 1] for i in self.decode_rows]
 
     @property
     def requests(self) -> list[PagedRequest]:
@@ -294,7 +301,7 @@ class ContinuousBatchingScheduler:
         ids = tokens.view(-1).tolist()
         for i, request in enumerate(lane):
             request.generated_tokens += 1
-            request.append_token(tokens[i : i + 1])
+            request._append_row(tokens, i)
         return tokens, ids, tuple(TokenEvent(r.sequence_id, t) for r, t in zip(lane, ids))
 
     def _graph_tokens(self) -> torch.Tensor | None:
@@ -362,8 +369,8 @@ class ContinuousBatchingScheduler:
     def _plan_ragged_step(self, terminal: list[PagedRequest]) -> tuple[StepPlan, tuple[TokenEvent, ...]]:
         tokens, ids, events = self._greedy_tokens()
         keep = self._retire_finished(ids, terminal)
-        plan = StepPlan(decode=[self.active_requests[i] for i in keep],
-                        decode_tokens=[tokens[i : i + 1] for i in keep], decode_ids=[ids[i] for i in keep])
+        plan = StepPlan(decode=[self.active_requests[i] for i in keep], decode_src=tokens, decode_rows=keep,
+                        decode_ids=[ids[i] for i in keep])
         self.active_requests = list(plan.decode)
         plan.pieces = self._cut_prompt_pieces()
         return plan, events

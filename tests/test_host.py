@@ -498,6 +498,10 @@ def test_request_joins_generated_tokens_when_read():
     assert r.sequence.tolist() == [[5, 6, 7, 2, 9]]  # joined once, stable
     r.append_token(torch.tensor([[4]]))
     assert r.sequence.tolist() == [[5, 6, 7, 2, 9, 4]]
+    r._append_row(step, 0)  # a step's row, sliced when the sequence is read
+    r.append_token(torch.tensor([[8]]))
+    r._append_row(step, 1)
+    assert r.sequence.tolist() == [[5, 6, 7, 2, 9, 4, 1, 8, 2]]
     r.sequence = prompt
     assert r.sequence is prompt
 
