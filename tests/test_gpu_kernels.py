@@ -737,3 +737,50 @@ def test_rms_norm_linear_rows_matches_norm_then_product(rows, with_residual, sil
         err = ((got.double() - prod).abs() - prod.abs() * 2.0**-8).max().item()
         _log(f"  product: excess over half an ulp={err:.3e}")
         assert err <= 1e-5
+
+
+def _random_shape(rng):
+    """(kv_heads, q_heads, head_dim, block_size, dtype, host_plan) of a sweep case."""
+    kv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([g for g in (1, 2, 4, 8, 16) if kv * g <= 64]))
+    return (kv, kv * group, int(rng.choice([64, 128])), int(rng.choice([5, 8, 16, 32])),
+            torch.bfloat16 if rng.random() < 0.7 else torch.float32, bool(rng.random() < 0.6))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_varlen_prefill_random_sweep(seed):
+    """Seeded random ragged batches against the oracle: 1-8 requests, contexts
+    0-2000, query chunks 1-160 (about a third of the requests single-token),
+    1-8 KV heads, GQA groups 1-16, head_dim 64 or 128, block sizes 5-32, fp32
+    or bf16, launches planned from host lengths or from bounds."""
+    rng = np.random.default_rng(1000 + seed)
+    kv, hq, d, bs, dtype, host_plan = _random_shape(rng)
+    n = int(rng.integers(1, 9))
+    ctx = [int(x) for x in rng.integers(0, 2001, size=n)]
+    q = [1 if rng.random() < 0.33 else int(x) for x in rng.integers(1, 161, size=n)]
+    _log(f"varlen sweep {seed}: ctx={ctx} q={q} hkv={kv} hq={hq} d={d} bs={bs} {dtype} host_plan={host_plan}")
+    wl = workloads.ragged(ctx, q, seed=seed, pool_factor=1.3, q_heads=hq, kv_heads=kv, head_dim=d, block_size=bs)
+    got, want = _prefill_case(wl, dtype, host_plan)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_decode_random_sweep(seed):
+    """Seeded random decode batches against the oracle: 1-24 sequences of
+    1-6000 tokens, with the shapes of the prefill sweep."""
+    rng = np.random.default_rng(2000 + seed)
+    kv, hq, d, bs, dtype, host_plan = _random_shape(rng)
+    n = int(rng.integers(1, 25))
+    ctx = [int(x) for x in rng.integers(0, 6000, size=n)]
+    _log(f"decode sweep {seed}: {n} seqs, max ctx {max(ctx)} hkv={kv} hq={hq} d={d} bs={bs} {dtype} host_plan={host_plan}")
+    wl = workloads.ragged(ctx, [1] * n, seed=seed, pool_factor=1.3, q_heads=hq, kv_heads=kv, head_dim=d,
+                          block_size=bs)
+    kc, vc = wl.pool(dtype)
+    qt, _, _ = wl.new_tokens(dtype)
+    got = _decode_hip(wl, kc.to(DEV), vc.to(DEV), qt, dtype, host_plan)
+    want = _decode_oracle(wl, kc, vc, qt)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
