@@ -140,10 +140,15 @@ class DecodeBench:
     def pool_bytes(self) -> int:
         return 2 * self.k_cache.numel() * self.k_cache.element_size()
 
-    def prepared(self, s: int, serving_plan: bool = False):
-        """The step's decode launch.  serving_plan: planned as the serving path
-        plans it (``paged_batch.RaggedBatch``): no host lengths, every row at
-        the 512-rounded bound of the longest sequence."""
+    def prepared(self, s: int, serving_plan: bool = False, fused: bool = True):
+        """The step's decode launch.  serving_plan: as a captured decode step of
+        the serving path runs it (``generation.decode_graph``): sized for the
+        512-rounded bound of the longest sequence, its work items read from
+        the plan of the step's host lengths in device memory (written and
+        copied here, before the step's launches); unfused, from the bound."""
+        import numpy as np
+        import torch
+
         from nano_infer_engine import _native
         from nano_infer_engine.paged_batch import decode_plan_bound
 
@@ -155,12 +160,18 @@ class DecodeBench:
         tables = self.tables
         width = -(-bound // self.wl.block_size)
         if tables.shape[1] < width:
-            import torch
-
             pad = torch.zeros((tables.shape[0], width - tables.shape[1]), dtype=tables.dtype, device=tables.device)
             tables = torch.cat([tables, pad], dim=1)
+        plan = None
+        if fused:
+            host = np.zeros(_native.decode_plan_bytes() // 4, dtype=np.int32)
+            _native.write_decode_plan(host.ctypes.data, host.nbytes, self.k_cache.dtype, self.wl.q_heads,
+                                      self.wl.kv_heads, self.wl.head_dim, self.wl.block_size,
+                                      np.asarray(self.seq_lens_host[s], dtype=np.int32), self.max_len[s],
+                                      self.total_len[s])
+            plan = torch.from_numpy(host.view(np.uint8)).to(self.k_cache.device)
         return _native.PreparedDecode(self.k_cache, self.v_cache, tables, self.lens[s], bound,
-                                      bound * tables.shape[0], self.wl.q_heads, self.scale)
+                                      bound * tables.shape[0], self.wl.q_heads, self.scale, device_plan=plan)
 
     def step(self, s: int, events: list | None = None, fused: bool = True, serving_plan: bool = False) -> None:
         """One decode step over every layer; optionally brackets each decode launch with HIP events.
@@ -176,7 +187,7 @@ class DecodeBench:
         from nano_infer_engine import _native
 
         append = None if fused else _native.PreparedAppend(self.k_cache, self.v_cache, self.slots[s])
-        decode = self.prepared(s, serving_plan)
+        decode = self.prepared(s, serving_plan, fused)
         for layer in range(self.wl.num_layers):
             if append is not None:
                 append(self.k_new, self.v_new, layer)
@@ -307,7 +318,8 @@ def run_decode(args):
             "avg_launch_us": round(avg_s * 1e6, 3),
         },
         "serving_plan_decode": {
-            "plan": "as the serving path plans it: no host lengths, every row at the 512-rounded bound",
+            "plan": "as a captured serving decode step runs it: launch sized for the 512-rounded bound, work "
+                    "items from the step's host plan in device memory",
             "avg_launch_us": round(s_avg * 1e6, 3), "achieved_GBs": round(s_gbs, 1),
             "frac": round(s_gbs / HBM_PEAK_GBS, 4),
         },

@@ -355,6 +355,50 @@ int nie_paged_decode_append(int dtype,
                             void* stream);
 
 /*
+ * A decode plan in memory, for launches captured once and replayed with
+ * other lengths (a HIP graph of the decode step).  nie_paged_decode_plan
+ * writes into `plan` (nie_paged_decode_plan_bytes() bytes, 4-byte aligned,
+ * host memory) the work items nie_paged_decode_append would plan from
+ * host_seq_lens (the same values as the device lengths of the launch it is
+ * for; each in [1, max_seq_len], reaching max_seq_len, summing to
+ * total_seq_len) for these shapes; the caller copies the bytes to device
+ * memory.  nie_paged_decode_append_planned is nie_paged_decode_append
+ * planned from bounds (max_seq_len, total_seq_len as upper bounds; its
+ * workspace nie_paged_decode_workspace_bytes of those bounds, its kernel
+ * arguments fixed), whose kernels take their work items from device_plan at
+ * run time when the table there has any (a table of count 0, as written for
+ * shapes the MFMA kernels do not take or for more items or sequences than a
+ * table holds, leaves them to locate their work from the device lengths).
+ * With a table, its result is bit-identical to nie_paged_decode_append
+ * called with those host lengths; without one (count 0, split length 0),
+ * to nie_paged_decode_append planned from the same bounds.  No counterpart in the reference (whose
+ * decode step runs eagerly, docs/development-roadmap.md:89, :190 list graph
+ * capture as future work); it exists for replayed decode steps, which
+ * cannot pass host lengths in kernel arguments.
+ */
+int64_t nie_paged_decode_plan_bytes(void);
+int nie_paged_decode_plan(int dtype, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                          int64_t block_size, const int32_t* host_seq_lens, int64_t batch,
+                          int64_t max_seq_len, int64_t total_seq_len, void* plan, int64_t plan_bytes);
+int nie_paged_decode_append_planned(int dtype,
+                                    const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                    const void* k_new, int64_t k_new_stride,
+                                    const void* v_new, int64_t v_new_stride,
+                                    const void* cos_table, const void* sin_table, int64_t table_rows,
+                                    void* k_cache, void* v_cache,
+                                    int64_t num_layers, int64_t layer_index,
+                                    int64_t num_blocks, int64_t block_size,
+                                    int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                    const int32_t* block_tables, int64_t table_stride,
+                                    const int32_t* seq_lens, int64_t batch,
+                                    int64_t max_seq_len, int64_t total_seq_len,
+                                    float scale,
+                                    void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                    void* workspace, int64_t workspace_bytes,
+                                    const void* device_plan,
+                                    void* stream);
+
+/*
  * nie_paged_decode_append without a workspace argument: the split partials
  * go to a device array the library owns (nie_paged_decode_noalloc_max_bytes()
  * bytes = 32 MiB per GPU, held from the device's first call until the

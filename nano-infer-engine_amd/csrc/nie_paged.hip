@@ -886,17 +886,23 @@ struct DecodeArgs {
   const void* rope_cos = nullptr;
   const void* rope_sin = nullptr;
   int64_t rope_rows = 0;
+  // A work-item table in device memory (nie_paged_decode_append_planned): a
+  // captured launch replays with the plan its step's host lengths call for,
+  // written there before each replay; count 0 there: locate on the device.
+  const struct DecodeItems* __restrict__ dev_items = nullptr;
 };
 
 // Work items of a decode call planned from host copies of the lengths,
-// passed by value as a kernel argument: item i = sequence << 16 | split, and
-// per sequence its length and first item.  count 0: the kernels locate
-// their work from the device lengths instead.
+// passed by value as a kernel argument (or read from device memory, see
+// DecodeArgs::dev_items): item i = sequence << 16 | split, the split length
+// in 16-key tiles, and per sequence its length and first item.  count 0:
+// the kernels locate their work from the device lengths instead.
 constexpr int kMaxDecodeItems = 256;
 constexpr int kMaxDecodeSeqs = 128;
 
 struct DecodeItems {
   int32_t count;
+  int32_t tps;
   uint32_t item[kMaxDecodeItems];
   int32_t seq_len[kMaxDecodeSeqs];
   int32_t seq_first[kMaxDecodeSeqs];
@@ -1728,7 +1734,18 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
 
   int64_t b, split, first_item, nsplit, tps;
   int seq_len;
-  if (items.count > 0) {
+  if (a.dev_items != nullptr && a.dev_items->count > 0) {
+    // the host's plan of this step, in device memory (scalar loads)
+    const DecodeItems* __restrict__ d = a.dev_items;
+    if ((int)blockIdx.x >= d->count) return;  // uniform over the workgroup
+    const uint32_t it = d->item[blockIdx.x];
+    b = it >> 16;
+    split = it & 0xffffu;
+    seq_len = d->seq_len[b];
+    first_item = d->seq_first[b];
+    tps = d->tps;
+    nsplit = cdiv(cdiv((int64_t)seq_len, (int64_t)kTileKeys), tps);
+  } else if (items.count > 0) {
     if ((int)blockIdx.x >= items.count) return;  // uniform over the workgroup
     const uint32_t it = items.item[blockIdx.x];
     b = it >> 16;
@@ -2037,7 +2054,11 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
   const int qh = (int)blockIdx.y * kMergeWaves + (int)(threadIdx.x / kWave);
   if (qh >= a.q_heads) return;
   int64_t nsplit, first = 0;
-  if (items.count > 0) {
+  if (a.dev_items != nullptr && a.dev_items->count > 0) {
+    const DecodeItems* __restrict__ d = a.dev_items;
+    nsplit = cdiv(cdiv((int64_t)d->seq_len[b], (int64_t)kTileKeys), (int64_t)d->tps);
+    first = d->seq_first[b];
+  } else if (items.count > 0) {
     nsplit = cdiv(cdiv((int64_t)items.seq_len[b], (int64_t)kTileKeys), (int64_t)a.tiles_per_split);
     first = items.seq_first[b];
   } else {
@@ -3758,6 +3779,9 @@ DecodePlan plan_decode_t(int64_t kv_heads, bool uniform, int64_t batch, int64_t 
   p.tps = 0;
   const int64_t capped = decode_max_items(batch, total_seq_len, kDecodeMaxTilesPerSplit);
   p.items = capped > p.slots ? capped : p.slots;
+  // at least a full item table: a launch planned from bounds covers (grid
+  // and workspace) any host plan a device-resident table may hold
+  p.items = p.items > kMaxDecodeItems ? p.items : kMaxDecodeItems;
   const int64_t forced = decode_tiles_override();
   if (forced > 0) {
     p.tps = forced < kDecodeMaxTilesPerSplit ? forced : kDecodeMaxTilesPerSplit;
@@ -3820,6 +3844,7 @@ DecodePlan plan_decode(int dtype, int64_t head_dim, int64_t kv_heads, int64_t bl
 // does not fit the table: the kernels then locate their work themselves).
 void fill_decode_items(const DecodePlan& p, const int32_t* host_lens, int64_t batch, DecodeItems* items) {
   items->count = 0;
+  items->tps = (int32_t)p.tps;
   if (host_lens == nullptr || batch > kMaxDecodeSeqs || p.items > kMaxDecodeItems) return;
   int64_t n = 0;
   for (int64_t b = 0; b < batch; ++b) {
@@ -4370,7 +4395,7 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
                       int64_t max_seq_len, int64_t total_seq_len, float scale, void* out, int64_t out_stride_b,
                       int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
                       const int32_t* host_seq_lens, const DecodeAppend& append, void* stream,
-                      bool static_scratch = false) {
+                      bool static_scratch = false, const void* device_plan = nullptr) {
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -4511,6 +4536,7 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   a.batch = batch;
   a.tiles_per_split = (int32_t)tps;
   a.split_slots = (int32_t)plan.slots;
+  a.dev_items = reinterpret_cast<const DecodeItems*>(device_plan);
   a.scale = scale;
   a.out = out;
   a.o_sb = out_stride_b;
@@ -4582,6 +4608,64 @@ NIE_API int nie_paged_decode_append(int dtype, const void* q, int64_t q_stride_b
                            block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
                            max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, workspace,
                            workspace_bytes, host_seq_lens, append, stream);
+}
+
+NIE_API int64_t nie_paged_decode_plan_bytes(void) { return (int64_t)sizeof(DecodeItems); }
+
+NIE_API int nie_paged_decode_plan(int dtype, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                  int64_t block_size, const int32_t* host_seq_lens, int64_t batch,
+                                  int64_t max_seq_len, int64_t total_seq_len, void* plan, int64_t plan_bytes) {
+  int rc = check_dtype(dtype);
+  if (rc) return rc;
+  rc = check_attention_shape(q_heads, kv_heads, head_dim, 1, block_size);
+  if (rc) return rc;
+  if (block_size <= 0) return fail(NIE_EINVAL, "block_size must be positive");
+  if (plan == nullptr || plan_bytes < (int64_t)sizeof(DecodeItems) || ((uintptr_t)plan % alignof(DecodeItems))) {
+    return fail(NIE_EINVAL, "plan buffer must hold nie_paged_decode_plan_bytes() aligned bytes");
+  }
+  DecodeItems* out = reinterpret_cast<DecodeItems*>(plan);
+  out->count = 0;
+  out->tps = 0;
+  if (batch < 0) return fail(NIE_EINVAL, "batch must be non-negative");
+  if (batch == 0 || !tuned_attention(head_dim, q_heads, kv_heads)) return NIE_OK;  // nothing to plan
+  if (host_seq_lens == nullptr || !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) {
+    return fail(NIE_EINVAL, "host lengths must be in [1, max_seq_len], reach max_seq_len and sum to total_seq_len");
+  }
+  fill_decode_items(plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens),
+                    host_seq_lens, batch, out);
+  // a plan the table cannot hold: the launch plans from its bounds (a caller
+  // that wants the same results eagerly plans from bounds too)
+  if (out->count == 0) out->tps = 0;
+  return NIE_OK;
+}
+
+NIE_API int nie_paged_decode_append_planned(int dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                            const void* k_new, int64_t k_new_stride, const void* v_new,
+                                            int64_t v_new_stride, const void* cos_table, const void* sin_table,
+                                            int64_t table_rows, void* k_cache, void* v_cache, int64_t num_layers,
+                                            int64_t layer_index, int64_t num_blocks, int64_t block_size,
+                                            int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                            const int32_t* block_tables, int64_t table_stride,
+                                            const int32_t* seq_lens, int64_t batch, int64_t max_seq_len,
+                                            int64_t total_seq_len, float scale, void* out, int64_t out_stride_b,
+                                            int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                                            const void* device_plan, void* stream) {
+  if (batch > 0 && (!k_new || !v_new)) return fail(NIE_EINVAL, "null pointer argument");
+  if (device_plan == nullptr || ((uintptr_t)device_plan % alignof(DecodeItems))) {
+    return fail(NIE_EINVAL, "device_plan must be an aligned device buffer of nie_paged_decode_plan_bytes() bytes");
+  }
+  DecodeAppend append;
+  append.k_new = k_new;
+  append.k_stride = k_new_stride;
+  append.v_new = v_new;
+  append.v_stride = v_new_stride;
+  append.cos_table = cos_table;
+  append.sin_table = sin_table;
+  append.table_rows = table_rows;
+  return paged_decode_call(dtype, q, q_stride_b, q_stride_h, k_cache, v_cache, num_layers, layer_index, num_blocks,
+                           block_size, q_heads, kv_heads, head_dim, block_tables, table_stride, seq_lens, batch,
+                           max_seq_len, total_seq_len, scale, out, out_stride_b, out_stride_h, workspace,
+                           workspace_bytes, nullptr, append, stream, /*static_scratch=*/false, device_plan);
 }
 
 // ---------------------------------------------------------------------------

@@ -58,6 +58,9 @@ EXPORTED_SYMBOLS = (
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
+    "nie_paged_decode_plan_bytes",
+    "nie_paged_decode_plan",
+    "nie_paged_decode_append_planned",
     "nie_paged_decode_noalloc_max_bytes",
     "nie_paged_decode_append_noalloc",
     "nie_varlen_prefill_workspace_bytes",
@@ -141,6 +144,32 @@ _SIGNATURES = {
             _ptr, _i64, _i64,                # out, strides
             _ptr, _i64,                      # workspace, bytes
             _ptr, _ptr,                      # host seq_lens, stream
+        ],
+    ),
+    "nie_paged_decode_plan_bytes": (_i64, []),
+    "nie_paged_decode_plan": (
+        _i32,
+        [
+            _i32, _i64, _i64, _i64, _i64,    # dtype, q_heads, kv_heads, head_dim, block_size
+            _ptr, _i64, _i64, _i64,          # host seq_lens, batch, max, total
+            _ptr, _i64,                      # plan buffer, bytes
+        ],
+    ),
+    "nie_paged_decode_append_planned": (
+        _i32,
+        [
+            _i32, _ptr, _i64, _i64,          # dtype, q, q strides
+            _ptr, _i64, _ptr, _i64,          # new K rows, stride, new V rows, stride
+            _ptr, _ptr, _i64,                # RoPE cos / sin tables, rows
+            _ptr, _ptr,                      # caches
+            _i64, _i64, _i64, _i64,          # layers, layer, blocks, block_size
+            _i64, _i64, _i64,                # q_heads, kv_heads, head_dim
+            _ptr, _i64,                      # block tables, stride
+            _ptr, _i64, _i64, _i64,          # seq_lens, batch, max bound, total bound
+            _f32,                            # scale
+            _ptr, _i64, _i64,                # out, strides
+            _ptr, _i64,                      # workspace, bytes
+            _ptr, _ptr,                      # device plan, stream
         ],
     ),
     "nie_paged_decode_noalloc_max_bytes": (_i64, []),
@@ -1013,15 +1042,60 @@ class PreparedRopeAppend:
             _check(rc, "nie_rope_kv_append")
 
 
+def decode_plan_bytes() -> int:
+    """Bytes of a decode plan (``write_decode_plan``, ``PreparedDecode(device_plan=...)``)."""
+    return int(load_library().nie_paged_decode_plan_bytes())
+
+
+def write_decode_plan(plan_ptr: int, plan_bytes: int, dtype: torch.dtype, q_heads: int, kv_heads: int,
+                      head_dim: int, block_size: int, seq_lens_host: np.ndarray, max_seq_len: int,
+                      total_seq_len: int) -> None:
+    """Writes at host address ``plan_ptr`` the work items a decode launch
+    plans from the host lengths ``seq_lens_host`` (contiguous int32), for a
+    device copy that a ``device_plan`` launch reads."""
+    if seq_lens_host.dtype != np.int32 or not seq_lens_host.flags.c_contiguous:
+        raise ValueError("seq_lens_host must be a contiguous int32 array")
+    rc = load_library().nie_paged_decode_plan(dtype_code(dtype), q_heads, kv_heads, head_dim, block_size,
+                                              seq_lens_host.ctypes.data, seq_lens_host.shape[0], max_seq_len,
+                                              total_seq_len, plan_ptr, plan_bytes)
+    if rc:
+        _check(rc, "nie_paged_decode_plan")
+
+
+_plan_probe = threading.local()
+
+
+def decode_plan_fits(dtype: torch.dtype, q_heads: int, kv_heads: int, head_dim: int, block_size: int,
+                     seq_lens_host: list[int]) -> bool:
+    """Whether the decode plan of these host lengths fits a work-item table
+    (``write_decode_plan`` writes a count of 0 otherwise, and a device-planned
+    launch then plans from its bounds)."""
+    buf = getattr(_plan_probe, "buf", None)
+    if buf is None:
+        buf = _plan_probe.buf = np.zeros(-(-decode_plan_bytes() // 4), dtype=np.int32)
+    lens = np.ascontiguousarray(seq_lens_host, dtype=np.int32)
+    write_decode_plan(buf.ctypes.data, buf.nbytes, dtype, q_heads, kv_heads, head_dim, block_size, lens,
+                      int(lens.max()), int(lens.sum()))
+    return int(buf[0]) > 0
+
+
 class PreparedDecode:
-    """``paged_decode`` for one batch of sequences (tables, lengths), any layer."""
+    """``paged_decode`` for one batch of sequences (tables, lengths), any layer.
+
+    ``device_plan``: a device buffer of ``decode_plan_bytes()`` that holds, when
+    the launch runs, the plan ``write_decode_plan`` wrote for the lengths of
+    that moment (or zeros: planned on the device); ``max_seq_len`` and
+    ``total_seq_len`` are then bounds.  For launches captured once and
+    replayed (``append_decode`` only); the result equals the launch prepared
+    with those host lengths.
+    """
 
     __slots__ = ("_fn", "_fn_append", "_pre", "_mid", "_post", "_shape", "_dtype", "_device", "_keep", "_kv_shape",
-                 "_align")
+                 "_align", "_plan")
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                  seq_lens: torch.Tensor, max_seq_len: int, total_seq_len: int, q_heads: int, scale: float,
-                 seq_lens_host=None):
+                 seq_lens_host=None, device_plan: torch.Tensor | None = None):
         num_layers, num_blocks, block_size, kv_heads, head_dim = _check_cache_pair(k_cache, v_cache)
         _require_gpu(block_tables, seq_lens)
         _check_attention_shapes(q_heads, kv_heads, head_dim)
@@ -1033,19 +1107,27 @@ class PreparedDecode:
             raise ValueError("block_tables must be a contiguous int32 (batch, max_blocks) tensor")
         host_lens = _host_seq_lens(seq_lens_host, batch)
         lib = load_library()
+        self._plan = None
+        if device_plan is not None:
+            if host_lens is not None:
+                raise ValueError("a device-planned decode takes no host lengths")
+            if (device_plan.device != k_cache.device or device_plan.numel() * device_plan.element_size()
+                    < decode_plan_bytes() or device_plan.data_ptr() % 4):
+                raise ValueError("device_plan must be a 4-byte aligned buffer of decode_plan_bytes() on the cache's device")
+            self._plan = device_plan.data_ptr()
         code = dtype_code(k_cache.dtype)
         ws_bytes = lib.nie_paged_decode_workspace_bytes(code, batch, q_heads, kv_heads, head_dim, block_size,
                                                         max_seq_len, total_seq_len, _array_ptr(host_lens))
         stream = _stream(k_cache.device)
         workspace = _decode_workspace(k_cache.device, stream, ws_bytes)
         self._fn = lib.nie_paged_decode
-        self._fn_append = lib.nie_paged_decode_append
+        self._fn_append = lib.nie_paged_decode_append if self._plan is None else lib.nie_paged_decode_append_planned
         self._dtype = k_cache.dtype
         self._device = k_cache.device
         self._shape = (batch, q_heads, head_dim)
         self._kv_shape = (batch, kv_heads, head_dim)
         self._align = _row_align(q_heads, kv_heads, head_dim)
-        self._keep = (block_tables, seq_lens, workspace, host_lens)
+        self._keep = (block_tables, seq_lens, workspace, host_lens, device_plan)
         self._pre = (code,)
         self._mid = (k_cache.data_ptr(), v_cache.data_ptr(), num_layers)
         self._post = (num_blocks, block_size, q_heads, kv_heads, head_dim, block_tables.data_ptr(),
@@ -1053,6 +1135,8 @@ class PreparedDecode:
                       (workspace.data_ptr(), workspace.numel(), _array_ptr(host_lens), stream))
 
     def __call__(self, query: torch.Tensor, layer_index: int, out: torch.Tensor) -> torch.Tensor:
+        if self._plan is not None:
+            raise RuntimeError("a device-planned decode runs through append_decode")
         for t in (query, out):
             if (t.shape != self._shape or t.dtype != self._dtype or t.device != self._device or t.stride(2) != 1
                     or t.data_ptr() % self._align):
@@ -1089,7 +1173,7 @@ class PreparedDecode:
                              num_layers, layer_index,
                              num_blocks, block_size, q_heads, kv_heads, head_dim, tables, tstride, lens, batch,
                              max_len, total_len, scale, out.data_ptr(), out.stride(0), out.stride(1), ws, ws_bytes,
-                             hlens, stream)
+                             hlens if self._plan is None else self._plan, stream)
         if rc:
             _check(rc, "nie_paged_decode_append")
         return out

@@ -17,10 +17,11 @@ length bucket) and replayed:
   refreshes the device side per step (the token IDs included when the
   caller has them on the host, as the scheduler does after reading the last
   step's tokens);
-* the decode launch inside the graph is planned for the bucket
-  (:func:`~nano_infer_engine.paged_batch.decode_plan_bound`), exactly as the
-  eager step plans it, so a replay computes the same values as the eager
-  step;
+* the decode launch inside the graph is sized for the bucket
+  (:func:`~nano_infer_engine.paged_batch.decode_plan_bound`) and takes its
+  work items from the exact plan of the step's lengths, which travels in
+  the same buffer (``_native.write_decode_plan``), so a replay computes the
+  same values as the eager step, planned from the same host lengths;
 * the graph ends with :func:`~nano_infer_engine._native.argmax_rows`, so the
   next token IDs are on the device when the replay finishes.
 
@@ -45,12 +46,13 @@ from nano_infer_engine.paged_cache import PagedKVCache
 class _CapturedStep:
     graph: torch.cuda.CUDAGraph
     batch: RaggedBatch
-    meta: torch.Tensor  # device bytes: ``longs``, ``ids``, then ``ints``
+    meta: torch.Tensor  # device bytes: ``longs``, ``ids``, ``ints``, then the decode plan
     ids: torch.Tensor  # (B,) int64 input token IDs (a view of ``meta``)
     meta_host: torch.Tensor  # pinned staging of ``meta``
     ints_np: np.ndarray  # staging views: tables (B*W), context lens (B), sequence lens (B)
     longs_np: np.ndarray  # slots (B), positions (B), cu_seqlens (B + 1)
     ids_np: np.ndarray  # token IDs (B)
+    plan_at: int  # byte offset of the decode plan in ``meta``
     width: int
     copied: torch.cuda.Event  # recorded after the staging copies of the last step
     logits: torch.Tensor  # (B, vocab) output of the last replay
@@ -98,10 +100,11 @@ class DecodeGraphRunner:
         # one buffer, so a step's inputs are one copy: int64 slots, positions,
         # cu_seqlens and token IDs first (8-byte aligned), then the int32s
         n_long, n_int = 4 * b + 1, b * width + 2 * b
-        meta = torch.zeros(8 * n_long + 4 * n_int, dtype=torch.uint8, device=self.device)
+        plan_at = -(-(8 * n_long + 4 * n_int) // 16) * 16
+        meta = torch.zeros(plan_at + _native.decode_plan_bytes(), dtype=torch.uint8, device=self.device)
         longs = meta[: 8 * (3 * b + 1)].view(torch.int64)
         ids = meta[8 * (3 * b + 1) : 8 * n_long].view(torch.int64)
-        ints = meta[8 * n_long :].view(torch.int32)
+        ints = meta[8 * n_long : 8 * n_long + 4 * n_int].view(torch.int32)
         # capture-time contents: length-1 sequences at position 0 whose
         # table entries lie outside the pool and whose slots are -1, so the
         # K/V writes of the warm-up and capture runs are skipped (the fused
@@ -124,6 +127,7 @@ class DecodeGraphRunner:
             positions=longs[b : 2 * b],
             decode_from=0,
             decode_bound=bound,
+            decode_plan=meta[plan_at:],  # zeros at capture: planned from the bounds
         )
         next_ids = torch.zeros(b, dtype=torch.int64, device=self.device)
         stream = self._stream
@@ -148,9 +152,10 @@ class DecodeGraphRunner:
             meta=meta,
             ids=ids,
             meta_host=meta_host,
-            ints_np=staged[8 * n_long :].view(np.int32),
+            ints_np=staged[8 * n_long : 8 * n_long + 4 * n_int].view(np.int32),
             longs_np=staged[: 8 * (3 * b + 1)].view(np.int64),
             ids_np=staged[8 * (3 * b + 1) : 8 * n_long].view(np.int64),
+            plan_at=plan_at,
             width=width,
             copied=torch.cuda.Event(),
             logits=logits,
@@ -214,6 +219,11 @@ class DecodeGraphRunner:
         longs[:b] = tables[np.arange(b), ctx // bs].astype(np.int64) * bs + ctx % bs
         longs[b : 2 * b] = ctx
         longs[2 * b :] = np.arange(b + 1)
+        lens = ints[b * width + b :]  # context + 1
+        keys = cache.keys
+        _native.write_decode_plan(step.meta_host.data_ptr() + step.plan_at, step.meta_host.numel() - step.plan_at,
+                                  keys.dtype, config.q_head_num, keys.shape[3], keys.shape[4], bs, lens,
+                                  int(ctx.max()) + 1, int(ctx.sum()) + b)
         if host_ids is not None:
             step.ids_np[:] = host_ids
         step.meta.copy_(step.meta_host, non_blocking=True)

@@ -26,11 +26,12 @@ from nano_infer_engine import _native
 from nano_infer_engine.paged_cache import PagedKVCache
 
 
-#: Decode launches are planned for the longest sequence rounded up to this
-#: many tokens (and every decode row at that length), so one plan serves every
-#: step until a sequence crosses the next multiple: a captured decode step
-#: (``generation.decode_graph``) replays with the same plan, and gives the
-#: same results, as the eager step.
+#: A captured decode step (``generation.decode_graph``) is captured for the
+#: longest sequence rounded up to this many tokens: its tables, grid and
+#: workspace cover every step until a sequence crosses the next multiple.
+#: Its work items come from the exact plan of each step's lengths, written
+#: to device memory with the step's inputs, so a replay computes what the
+#: eager step (planned from host lengths) computes.
 DECODE_PLAN_BUCKET = 512
 
 
@@ -54,7 +55,10 @@ class RaggedBatch:
     positions: torch.Tensor  # (num_tokens,) int64
     # host-side launch geometry
     decode_from: int  # requests [decode_from, R) have one new token each (a contiguous tail)
-    decode_bound: int = 0  # length bound the decode launch is planned for (0: no decode rows)
+    decode_bound: int = 0  # length bound of a captured decode step's launch (0: no decode rows)
+    # a captured step's device plan buffer (``_native.write_decode_plan`` fills
+    # it before each replay); None: an eager batch, planned from host lengths
+    decode_plan: torch.Tensor | None = None
     # prepared per-layer launches, built on first use (see ``launchers``)
     _launch: dict = field(default_factory=dict, repr=False, compare=False)
 
@@ -99,10 +103,26 @@ class RaggedBatch:
             )
         if split < self.num_requests:
             rows = self.num_requests - split
-            decode = _native.PreparedDecode(
-                cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], self.decode_bound,
-                rows * self.decode_bound, q_heads, scale,
-            )
+            if self.decode_plan is not None:
+                decode = _native.PreparedDecode(
+                    cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], self.decode_bound,
+                    rows * self.decode_bound, q_heads, scale, device_plan=self.decode_plan,
+                )
+            else:
+                # the host lengths' plan, as a replay of the step would run it
+                # (from bounds when that plan does not fit an item table)
+                lens = [c + 1 for c in self.context_lens[split:]]
+                keys = cache.keys
+                if _native.decode_plan_fits(keys.dtype, q_heads, keys.shape[3], keys.shape[4], keys.shape[2], lens):
+                    decode = _native.PreparedDecode(
+                        cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:], max(lens),
+                        sum(lens), q_heads, scale, seq_lens_host=lens,
+                    )
+                else:
+                    decode = _native.PreparedDecode(
+                        cache.keys, cache.values, self.block_tables[split:], self.seq_lens_t[split:],
+                        self.decode_bound, rows * self.decode_bound, q_heads, scale,
+                    )
         found = (append, prefill, decode, (cos, sin))
         self._launch[key] = found
         return found

@@ -784,3 +784,59 @@ def test_decode_random_sweep(seed):
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")
     assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_append_device_plan_matches_host_plan(dtype):
+    """nie_paged_decode_append_planned, planned from a bucket's bounds and
+    reading its work items from a device plan written by write_decode_plan,
+    equals nie_paged_decode_append planned from the same host lengths bit for
+    bit, cache included; with a zeroed plan it equals the launch planned
+    from the bounds."""
+    from nano_infer_engine.paged_batch import decode_plan_bound
+
+    _log(f"decode-append device plan {dtype}")
+    wl = workloads.ragged([500, 37, 3000, 128, 1999], [1] * 5, seed=41, pool_factor=1.5)
+    kc, vc = wl.pool(dtype)
+    q, k_new, v_new = wl.new_tokens(dtype)
+    host = list(wl.seq_lens)
+    bound = decode_plan_bound(max(host))
+    tab = wl.table_array()
+    width = max(tab.shape[1], -(-bound // wl.block_size))
+    padded = np.zeros((tab.shape[0], width), dtype=np.int32)
+    padded[:, : tab.shape[1]] = tab
+    tables = torch.from_numpy(padded).to(DEV)
+    lens = torch.tensor(host, dtype=torch.int32, device=DEV)
+    qd, kd, vd = q.to(DEV), k_new.to(DEV), v_new.to(DEV)
+    scale = wl.head_dim**-0.5
+    plan = np.zeros(_native.decode_plan_bytes() // 4, dtype=np.int32)
+    _native.write_decode_plan(plan.ctypes.data, plan.nbytes, dtype, wl.q_heads, wl.kv_heads, wl.head_dim,
+                              wl.block_size, np.asarray(host, dtype=np.int32), max(host), sum(host))
+    assert plan[0] > 0
+
+    def run(**kw):
+        k, v = kc.to(DEV), vc.to(DEV)
+        if "device_plan" in kw:
+            d = _native.PreparedDecode(k, v, tables, lens, bound, len(host) * bound, wl.q_heads, scale, **kw)
+        elif kw.get("seq_lens_host") is not None:
+            d = _native.PreparedDecode(k, v, tables, lens, max(host), sum(host), wl.q_heads, scale, **kw)
+        else:
+            d = _native.PreparedDecode(k, v, tables, lens, bound, len(host) * bound, wl.q_heads, scale)
+        out = torch.empty_like(qd)
+        d.append_decode(qd, kd, vd, 0, out)
+        torch.cuda.synchronize()
+        return out.cpu(), k.cpu(), v.cpu()
+
+    planned = run(device_plan=torch.from_numpy(plan.view(np.uint8)).to(DEV))
+    host_planned = run(seq_lens_host=host)
+    assert all(torch.equal(a, b) for a, b in zip(planned, host_planned))
+    zero_plan = run(device_plan=torch.zeros(_native.decode_plan_bytes(), dtype=torch.uint8, device=DEV))
+    bound_planned = run()
+    assert all(torch.equal(a, b) for a, b in zip(zero_plan, bound_planned))
+    ref_k, ref_v = kc.clone(), vc.clone()
+    for b, (table, ctx) in enumerate(zip(wl.tables, wl.context_lens)):
+        reference_ops.write_tokens(ref_k, ref_v, 0, table, wl.block_size, ctx, k_new[b : b + 1], v_new[b : b + 1])
+    want = _decode_oracle(wl, ref_k, ref_v, q)
+    err = (planned[0].float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]

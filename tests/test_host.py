@@ -672,3 +672,41 @@ def test_decode_step_bookkeeping_fast_path_matches_public_methods():
             assert fast.get_block_table(s) == public.get_block_table(s)
     assert fast.allocator.free_block_count == public.allocator.free_block_count
     assert fast.allocator.allocate(3) == public.allocator.allocate(3)
+
+
+def test_library_decode_plan_table():
+    """nie_paged_decode_plan writes the host plan's work-item table: for 16
+    sequences of 29,600 tokens the 16 splits of 116 tiles above, items in
+    sequence order and each sequence's first item the splits before it; for
+    ragged lengths ceil(tiles / split) items per sequence; for more sequences
+    than a table holds a count and split length of 0 (the launch then plans
+    from its bounds), which decode_plan_fits reports."""
+    nbytes = _native.decode_plan_bytes()
+    assert nbytes == 4 * (2 + 256 + 128 + 128)
+    buf = np.zeros(nbytes // 4, dtype=np.int32)
+
+    def plan(lens):
+        lens = np.asarray(lens, dtype=np.int32)
+        buf[:] = -1
+        _native.write_decode_plan(buf.ctypes.data, nbytes, torch.bfloat16, 32, 8, 64, 16, lens, int(lens.max()),
+                                  int(lens.sum()))
+        count, tps = int(buf[0]), int(buf[1])
+        items = [(int(i) >> 16, int(i) & 0xFFFF) for i in buf[2 : 2 + count].view(np.uint32)]
+        return count, tps, items, buf[258 : 258 + len(lens)].tolist(), buf[386 : 386 + len(lens)].tolist()
+
+    count, tps, items, seq_len, first = plan([29600] * 16)
+    assert (count, tps) == (256, 116)
+    assert items == [(b, s) for b in range(16) for s in range(16)]
+    assert seq_len == [29600] * 16 and first == [16 * b for b in range(16)]
+
+    lens = [17, 64, 129, 500, 3000]
+    count, tps, items, seq_len, first = plan(lens)
+    splits = [-(-(-(-n // 16)) // tps) for n in lens]
+    assert tps >= 4 and count == sum(splits) and seq_len == lens
+    assert first == [sum(splits[:b]) for b in range(len(lens))]
+    assert items == [(b, s) for b in range(len(lens)) for s in range(splits[b])]
+    assert _native.decode_plan_fits(torch.bfloat16, 32, 8, 64, 16, lens)
+
+    count, tps, *_ = plan([100] * 130)
+    assert (count, tps) == (0, 0)
+    assert not _native.decode_plan_fits(torch.bfloat16, 32, 8, 64, 16, [100] * 130)
