@@ -13,13 +13,15 @@ reads its KV from HBM.
 Prints one JSON line.  ``value`` = algorithmic bytes (decode K/V/Q/O/table
 reads + append traffic) per second over the timed steps.  ``roofline`` is
 for the decode-attention call, timed per launch with HIP events on its
-stream.  Further fields: the same step planned as the serving path plans it
+stream.  Further fields: the same step as a captured serving step runs it
 (``serving_plan_decode``), the 4-sequence decode call (``decode_small``),
 the 16 x 29600 stress step on a pool of ~90% of free HBM, attention only and
 through the whole model (``stress_16x29600``), the mixed chunked-prefill
-step (``mixed_prefill_step``), end-to-end serving of the Llama-3.2-1B-shaped
-model (``e2e_llama1b_serving``) and the reference algorithm's own times on
-the GPU and on the host cores (``reference_path``, ``cpu_baseline``).
+step (``mixed_prefill_step``), longer prefills (``prefill_long``: 4 fresh
+2048-token prompts, 4 chunks of 512 on 8192-token contexts), end-to-end
+serving of the Llama-3.2-1B-shaped model (``e2e_llama1b_serving``) and the
+reference algorithm's own times on the GPU and on the host cores
+(``reference_path``, ``cpu_baseline``).
 """
 
 from __future__ import annotations
@@ -47,10 +49,10 @@ def parse_args():
     p.add_argument("--layers", type=int, default=16)
     p.add_argument("--unfused-append", action="store_true",
                    help="decode step as nie_kv_append then nie_paged_decode (two launches per layer)")
-    p.add_argument("--only", choices=["decode", "small", "stress", "mixed", "e2e", "linear", "reference"],
+    p.add_argument("--only", choices=["decode", "small", "stress", "mixed", "long", "e2e", "linear", "reference"],
                    help="run one leg and print its JSON only")
     p.add_argument("--skip", action="append", default=[],
-                   choices=["small", "stress", "stress-model", "mixed", "e2e", "reference", "cpu", "lockstep"],
+                   choices=["small", "stress", "stress-model", "mixed", "long", "e2e", "reference", "cpu", "lockstep"],
                    help="leave a leg out of the default line (repeatable)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU baseline sample")
     p.add_argument("--pool-fraction", type=float, default=0.9,
@@ -543,6 +545,52 @@ def run_mixed(args):
     }
 
 
+def run_prefill_long(args):
+    """The varlen prefill call on longer prefills than the mixed step's, where
+    the per-call fixed costs (prologue, split partials, merge) weigh less:
+    4 fresh 2048-token prompts, and 4 chunks of 512 tokens on 8192-token
+    contexts; bf16, one layer, launches planned from host lengths."""
+    import numpy as np
+    import torch
+
+    from nano_infer_engine import _native, workloads
+
+    device = torch.device("cuda:0")
+    out = {}
+    for name, wl in (("prompts_4x2048", workloads.prefill_prompts()),
+                     ("chunks_4x512_on_8192", workloads.prefill_long_context())):
+        kc, vc = wl.pool(torch.bfloat16, device)
+        q, k_new, v_new = wl.new_tokens(torch.bfloat16, device)
+        _native.kv_append(kc, vc, 0, k_new, v_new, torch.from_numpy(wl.slots()).to(device))
+        cu_host = [0] + np.cumsum(wl.query_lens).tolist()
+        cu = torch.tensor(cu_host, dtype=torch.int64, device=device)
+        ctx = torch.tensor(wl.context_lens, dtype=torch.int32, device=device)
+        tables = torch.from_numpy(wl.table_array()).to(device)
+        prefill = _native.PreparedPrefill(kc, vc, cu, ctx, tables, wl.num_tokens, max(wl.query_lens),
+                                          max(wl.seq_lens), wl.q_heads, wl.head_dim**-0.5,
+                                          cu_seqlens_host=cu_host, context_lens_host=wl.context_lens)
+        o = torch.empty_like(q)
+        for _ in range(5):
+            prefill(q, 0, o)
+        ev = []
+        for _ in range(30):
+            e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            e[0].record()
+            prefill(q, 0, o)
+            e[1].record()
+            ev.append(e)
+        torch.cuda.synchronize()
+        us = _median_us(ev)
+        flops = workloads.prefill_flops(wl.context_lens, wl.query_lens)
+        tflops = flops / (us * 1e-6) / 1e12
+        log(f"prefill {name}: {us:.1f} us = {tflops:.1f} TFLOP/s ({flops / 1e9:.2f} GFLOP)")
+        out[name] = {"avg_launch_us": round(us, 2), "flops_per_launch": flops, "achieved_TFLOPs": round(tflops, 2),
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del kc, vc, prefill
+        torch.cuda.empty_cache()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # configuration 4: end-to-end serving
 # ---------------------------------------------------------------------------
@@ -882,7 +930,8 @@ def main():
     only = {
         "decode": ("decode", run_decode), "small": ("decode_small", run_decode_small),
         "stress": ("stress_16x29600", lambda a: {"attention": run_stress(a), "full_model": run_stress_model(a)}),
-        "mixed": ("mixed_prefill_step", run_mixed), "e2e": ("e2e_llama1b_serving", run_e2e),
+        "mixed": ("mixed_prefill_step", run_mixed), "long": ("prefill_long", run_prefill_long),
+        "e2e": ("e2e_llama1b_serving", run_e2e),
         "linear": ("decode_projections", run_linear),
         "reference": ("reference_path", lambda a: {**run_reference_path(a), "serving_lockstep": run_lockstep(a)}),
     }
@@ -900,6 +949,8 @@ def main():
             result["stress_16x29600"]["full_model"] = run_stress_model(args)
     if "mixed" not in skip:
         result["mixed_prefill_step"] = run_mixed(args)
+    if "long" not in skip:
+        result["prefill_long"] = run_prefill_long(args)
     if "e2e" not in skip:
         result["e2e_llama1b_serving"] = run_e2e(args)
     if "reference" not in skip:

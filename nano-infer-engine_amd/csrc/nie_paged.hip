@@ -2441,11 +2441,51 @@ __device__ __forceinline__ int prefill_key_tiles(int ctx, int q_len, int tpt, in
 
 // Work items (query tile, key split) of a request with q_len query tokens
 // after ctx cached ones.
-__device__ __forceinline__ int prefill_items_of_len(int q_len, int ctx, int tpt, int S) {
-  const int nqt = (q_len + tpt - 1) / tpt;
+// Walks the query tiles of one request in order, keeping the piece count
+// ceil(key tiles / S) of the current tile without a division per tile: the
+// key tiles a tile sees grow by at most ceil(tpt / 16) + 1 from one tile to
+// the next, so the count catches up by a few additions of S.  (A call too
+// large for the host schedule has up to thousands of query tiles, and two
+// integer divisions per tile in every workgroup's locate cost more VALU
+// time than its attention steps.)
+struct SplitWalk {
+  int q_len, ctx, tpt, S;
+  int t_end;   // query tokens up to the end of the current tile
+  int nsplit;  // pieces of the current tile: ceil(key tiles / S)
+  int cap;     // nsplit * S
+  __host__ __device__ __forceinline__ void start(int q_len_, int ctx_, int tpt_, int S_) {
+    q_len = q_len_;
+    ctx = ctx_;
+    tpt = tpt_;
+    S = S_;
+    t_end = min(tpt, q_len);
+    nsplit = ((ctx + t_end + kTileKeys - 1) / kTileKeys + S - 1) / S;
+    cap = nsplit * S;
+  }
+  __host__ __device__ __forceinline__ void next() {
+    t_end = min(t_end + tpt, q_len);
+    const int kt = (ctx + t_end + kTileKeys - 1) / kTileKeys;
+    while (kt > cap) {
+      cap += S;
+      ++nsplit;
+    }
+  }
+};
+
+// Items of query tiles [0, count) of a request.
+__device__ __forceinline__ int prefill_items_upto(int q_len, int ctx, int tpt, int S, int count) {
+  SplitWalk w;
+  w.start(q_len, ctx, tpt, S);
   int n = 0;
-  for (int qt = 0; qt < nqt; ++qt) n += (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
+  for (int qt = 0; qt < count; ++qt) {
+    if (qt > 0) w.next();
+    n += w.nsplit;
+  }
   return n;
+}
+
+__device__ __forceinline__ int prefill_items_of_len(int q_len, int ctx, int tpt, int S) {
+  return prefill_items_upto(q_len, ctx, tpt, S, (q_len + tpt - 1) / tpt);
 }
 
 __device__ __forceinline__ int64_t prefill_items_of(const PrefillArgs& a, int64_t r) {
@@ -2752,13 +2792,15 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     const PrefillItem pit = prefill_locate(a, (int64_t)wg_item);
     if (pit.r < 0) return;  // uniform over the workgroup
     // (query tile, split) of this item; the loop is wave-uniform
-    int qt = 0, split = (int)pit.local, nsplit = 0;
-    for (;;) {
-      nsplit = (prefill_key_tiles(pit.ctx, pit.q_len, tpt, qt) + S - 1) / S;
-      if (split < nsplit) break;
-      split -= nsplit;
+    int qt = 0, split = (int)pit.local;
+    SplitWalk w;
+    w.start(pit.q_len, pit.ctx, tpt, S);
+    while (split >= w.nsplit && w.nsplit > 0) {  // nsplit >= 1 for a request with query tokens
+      split -= w.nsplit;
       ++qt;
+      w.next();
     }
+    const int nsplit = w.nsplit;
     r = pit.r;
     q_begin = pit.q_begin;
     q_len = pit.q_len;
@@ -3301,8 +3343,7 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
     const int ctx = a.context_lens[r];
     nsplit = (prefill_key_tiles(ctx, q_len, tpt, qt) + S - 1) / S;
     if (nsplit <= 1) return;  // the prefill kernel wrote these rows
-    first = prefill_items_before(a, r);  // the tile's first item
-    for (int k = 0; k < qt; ++k) first += (prefill_key_tiles(ctx, q_len, tpt, k) + S - 1) / S;
+    first = prefill_items_before(a, r) + prefill_items_upto(q_len, ctx, tpt, S, qt);  // the tile's first item
     row0 = q_begin + qt * tpt;
     tokens = min(tpt, q_len - qt * tpt);
   }

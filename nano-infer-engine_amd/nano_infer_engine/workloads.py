@@ -145,6 +145,16 @@ def mixed_prefill(seed: int = 2) -> PagedWorkload:
     return ragged([0, 384, 1024, 4000] + decode_ctx, [128] * 4 + [1] * 12, seed=seed, pool_factor=2.0)
 
 
+def prefill_prompts(seed: int = 5) -> PagedWorkload:
+    """4 fresh prompts of 2048 tokens each (no cached context), one chunk each."""
+    return ragged([0] * 4, [2048] * 4, seed=seed, pool_factor=1.25)
+
+
+def prefill_long_context(seed: int = 6) -> PagedWorkload:
+    """4 chunks of 512 tokens on 8192-token cached contexts."""
+    return ragged([8192] * 4, [512] * 4, seed=seed, pool_factor=1.25)
+
+
 def decode_long(num_layers: int = 1, seed: int = 4, num_blocks: int | None = None) -> PagedWorkload:
     """16 decode rows at 29600 tokens of context (fully permuted tables)."""
     return ragged([29600] * 16, [1] * 16, seed=seed, num_blocks=num_blocks, pool_factor=2.0, num_layers=num_layers)

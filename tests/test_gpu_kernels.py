@@ -486,6 +486,19 @@ def test_varlen_prefill_mixed_batch(dtype, host_plan):
     assert err <= TOL[dtype]
 
 
+@pytest.mark.parametrize("which", ["prefill_prompts", "prefill_long_context"])
+def test_varlen_prefill_long_workloads(which):
+    """The long-prefill workloads the bench times: 4 fresh 2048-token prompts
+    (64 query tiles per request, causal) and 4 chunks of 512 tokens on
+    8192-token contexts, bf16, launches planned from host lengths."""
+    _log(f"varlen long {which}")
+    wl = getattr(workloads, which)()
+    got, want = _prefill_case(wl, torch.bfloat16, True)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[torch.bfloat16]
+
+
 @pytest.mark.parametrize("context,query", [(300, 16), (600, 8), (1000, 40), (20000, 16)])
 @pytest.mark.parametrize("host_plan", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
