@@ -3426,7 +3426,8 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
 // bound on the total work gives about kPrefillTargetItems workgroups.
 constexpr int64_t kPrefillTargetItems = 2048;
 constexpr int64_t kPrefillMinTilesPerSplit = 8;
-constexpr int64_t kPrefillMaxTilesPerSplit = 64;
+constexpr int64_t kPrefillMaxTilesPerSplit = kTableWindow;  // a piece's blocks fit the block-table window
+static_assert(kPrefillMaxTilesPerSplit <= kTableWindow, "a piece's lookups stay in its block-table window");
 
 // A query tile of a host-planned prefill call (tiles in request order) and
 // its pieces' workspace slots [first, first + pieces).
