@@ -2789,7 +2789,10 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     t0 = sc.t0[k];
     slot = ((tl >> 8) & 0xff) == 1 ? -1 : (int64_t)(tl >> 16) + (int64_t)((it >> 8) & 0xff);
   } else {
-    const PrefillItem pit = prefill_locate(a, (int64_t)wg_item);
+    // in reverse order: a request's later query tiles see more keys, so the
+    // longest items start first and the short ones fill the end of the
+    // launch (indices past the call's items exit here, first)
+    const PrefillItem pit = prefill_locate(a, (int64_t)(a.grid_items - 1 - wg_item));
     if (pit.r < 0) return;  // uniform over the workgroup
     // (query tile, split) of this item; the loop is wave-uniform
     int qt = 0, split = (int)pit.local;
