@@ -52,6 +52,10 @@ extern "C" {
 #define NIE_DTYPE_F32 0
 #define NIE_DTYPE_BF16 1
 
+/* Rounding point of the bf16 attention probabilities (nie_set_attention_rounding). */
+#define NIE_ROUND_REFERENCE 0 /* the reference's: P = bf16(exp(s - m) / l), two passes over the keys */
+#define NIE_ROUND_FAST 1      /* online softmax: bf16(exp(s - running max)), O / l at the end; one pass */
+
 /* Library version string, e.g. "nie_paged 0.1 gfx950". */
 const char* nie_version(void);
 
@@ -253,12 +257,38 @@ int nie_argmax_rows_split(int dtype, const void* logits, int64_t rows, int64_t c
                           int64_t* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Where the bf16 attention kernels (nie_paged_decode*, nie_varlen_prefill)
+ * round the softmax probabilities, for calls issued after this one in the
+ * whole process (default NIE_ROUND_REFERENCE).
+ *  NIE_ROUND_REFERENCE: the reference's rounding point.  Scores are
+ *    bf16(bf16(q.k) * scale), the softmax runs in fp32 over a row's whole
+ *    key range, the normalised probabilities exp(s - m) / l are rounded to
+ *    bf16, and P.V accumulates them in fp32 (rounded once).  The kernels make
+ *    two passes over the keys: the first forms each row's maximum and sum
+ *    (decode: and keeps every score in the workspace), the second the
+ *    probabilities and P.V.
+ *  NIE_ROUND_FAST: one pass with an online softmax; the unnormalised
+ *    exp(s - running maximum) is rounded to bf16 and the row is divided by
+ *    its sum at the end (flash-attention style).  Same inputs to the softmax,
+ *    a different rounding point for P.
+ * fp32 calls are unaffected (the probabilities are not rounded).  The
+ * workspace sizes depend on the mode: query them after setting it.
+ * NIE_EINVAL for any other value.
+ * Replaces: the probability cast of the reference's softmax
+ *           (src/nano_infer_engine/layers/paged_attention.py:109-114,
+ *           layers/attention.py:410-411), which the default mode keeps.
+ */
+int nie_set_attention_rounding(int mode);
+int nie_attention_rounding(void);
+
+/*
  * Workspace bytes needed by nie_paged_decode for a call with these
  * arguments (same meaning as there; host values), whose sequence lengths
  * have maximum max_seq_len and sum total_seq_len, and the same optional
  * host copy of the lengths as the call.  The split of the work depends on
  * all of them, so query with the values of the call.
- * Layout: fp32 split partials (unnormalised O rows, then (max, sum) pairs).
+ * Layout: fp32 split partials (O rows, then (max, sum) pairs); with the
+ * reference rounding (bf16) also the bf16 scores of every key of the call.
  * The pointer must be 16-byte aligned.  Returns 0 for invalid arguments.
  */
 int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,

@@ -142,6 +142,35 @@ __device__ __forceinline__ v4s pack_bf16x4(float x0, float x1, float x2, float x
 // sums cannot resolve anyway).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// e^x to about one ulp, for the probabilities that are rounded to bf16 as
+// the reference rounds them (torch's exp is accurate to about an ulp; 2^(x
+// log2 e) through fast_exp2 would carry the rounding of x log2 e, an error
+// of |x| 2^-24 in the exponent, and move the bf16 rounding of about one
+// probability in 10^4).  x log2 e is formed as hi + lo: hi the rounded
+// product, lo its rounding error (fma) plus x times the part of log2 e that
+// float drops; then e^x = 2^hi (1 + lo ln 2) to within lo^2.  Results below
+// 2^-126 flush to zero (no bf16 probability of a sum of at least 1 gets
+// there with an effect on the output).
+__device__ __forceinline__ float exp_ref(float x) {
+  constexpr float kL2eHi = 1.44269502162933349609375f;  // log2(e) rounded to float
+  constexpr float kL2eLo = 1.925963033500011079e-8f;    // log2(e) - kL2eHi
+  constexpr float kLn2 = 0.693147180559945309f;
+  // -inf (a masked key) gives 0 through a finite argument; NaN propagates
+  x = __builtin_elementwise_maximum(x, -200.f);
+  const float hi = x * kL2eHi;
+  const float lo = fmaf(x, kL2eLo, fmaf(x, kL2eHi, -hi));
+  const float e = __builtin_amdgcn_exp2f(hi);
+  return fmaf(e, lo * kLn2, e);
+}
+
+// e / l rounded to nearest, given r = 1 / l rounded to nearest: the product
+// e r (two roundings) corrected by one Newton step on its exact residual
+// e - q l (fma), as torch's division e / l rounds once.
+__device__ __forceinline__ float div_ref(float e, float l, float r) {
+  const float q = e * r;
+  return fmaf(fmaf(-q, l, e), r, q);
+}
+
 // Rounds a value to the storage dtype (identity for fp32).
 template <typename T>
 __device__ __forceinline__ float round_storage(float x) {
@@ -876,6 +905,10 @@ struct DecodeArgs {
   float* ws_o;   // (ws_items, q_heads, head_dim)
   float* ws_ml;  // (ws_items, q_heads, 2)
   int64_t ws_items;  // partial slots in the workspace (0 when there is none)
+  // Two-pass rounding: the scores, (ws_items, tiles_per_split, q_heads, 16)
+  // bf16, written by the scores pass and read by the P.V pass
+  uint16_t* ws_s = nullptr;
+  int64_t ws_s_keys = 0;  // key slots there (items x tiles_per_split x 16 must fit)
   // Fused append (nie_paged_decode_append): new K/V rows (batch, kv_heads,
   // head_dim), row strides in elements; k_new == nullptr: no append.
   const void* k_new = nullptr;
@@ -962,26 +995,18 @@ constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 
 // an item fewer groups are in flight and the wait tightens with them.
 template <int kOps, int kMaxLater>
 __device__ __forceinline__ void wait_dma_groups(int later) {
-  static_assert(kMaxLater >= 0 && kMaxLater <= 3 && kMaxLater * kOps < 64, "vmcnt immediate range");
-  if constexpr (kMaxLater >= 3) {
-    if (later >= 3) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kOps));
-      return;
-    }
-  }
-  if constexpr (kMaxLater >= 2) {
-    if (later == 2) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kOps));
-      return;
-    }
-  }
+  static_assert(kMaxLater >= 0 && kMaxLater <= 7 && kMaxLater * kOps < 64, "vmcnt immediate range");
   if constexpr (kMaxLater >= 1) {
-    if (later == 1) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kOps));
+    // s_waitcnt takes an immediate: one test per possible group count,
+    // from the most groups down (a count above kMaxLater waits for kMaxLater)
+    if (later >= kMaxLater) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kMaxLater * kOps));
       return;
     }
+    wait_dma_groups<kOps, kMaxLater - 1>(later);
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -1637,6 +1662,47 @@ __device__ __forceinline__ void rope_vec(v4u& lo, v4u& hi, const v4u& c, const v
 // (max, sum) pair per lane) is issued before any is used, and batches
 // combine through a running maximum, so the usual merge (<= 32 splits at
 // head_dim 64) costs one memory round trip.
+// The sum of the nsplit split partials of one row (the two-pass rounding's
+// partials are shares of the normalised output, so they merge by plain
+// addition), in the same fixed order as merge_row, rounded once.
+template <typename T, int D>
+__device__ __forceinline__ void sum_row(const float* po, int64_t po_stride, int nsplit, T* out) {
+  constexpr int kLanesPerSplit = D / 4;
+  constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
+  constexpr int kPasses = 8;
+  constexpr int kBatch = kPasses * kSplitsPerPass;
+  const int lane = lane_id();
+  const int sub = lane / kLanesPerSplit;
+  const int chunk = lane % kLanesPerSplit;
+  po += 4 * chunk;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+    const int count = min(kBatch, nsplit - s0);
+    float4 v[kPasses];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int sp = p * kSplitsPerPass + sub;
+      v[p] = sp < count ? *reinterpret_cast<const float4*>(po + (s0 + sp) * po_stride)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      acc.x += v[p].x;
+      acc.y += v[p].y;
+      acc.z += v[p].z;
+      acc.w += v[p].w;
+    }
+  }
+#pragma unroll
+  for (int off = kLanesPerSplit; off < kWave; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off);
+    acc.y += __shfl_xor(acc.y, off);
+    acc.z += __shfl_xor(acc.z, off);
+    acc.w += __shfl_xor(acc.w, off);
+  }
+  if (sub == 0) store4<T>(out + 4 * chunk, acc.x, acc.y, acc.z, acc.w);
+}
+
 template <typename T, int D>
 __device__ __forceinline__ void merge_row(const float* po, int64_t po_stride, const float* ml, int64_t ml_stride,
                                           int nsplit, T* out) {
@@ -1709,21 +1775,53 @@ constexpr int decode_max_heads() {
 
 constexpr int kDecodeLdsBudget = 160 * 1024;
 
-template <typename T, int D, int kHeads>
+// Passes of a decode call.  kDecodeFused: one pass, the online softmax
+// (bf16 P = exp(s - running max), O / l at the end).  With the reference's
+// rounding point (the normalised probabilities rounded to bf16 before P.V,
+// layers/paged_attention.py:109-114) two passes over the keys:
+// kDecodeScores reads K, writes every key's score (bf16, the value the
+// reference feeds its softmax) and each split's (max, sum of exp); then
+// kDecodePV reads V and those scores, forms each row's (max, sum) over all
+// its splits, and accumulates bf16(e^(s - m) / l) . V in fp32.
+constexpr int kDecodeFused = 0;
+constexpr int kDecodeScores = 1;
+constexpr int kDecodePV = 2;
+
+// LDS stage of a decode pass: the K tile and/or the V tile of all the
+// workgroup's heads, and in the P.V pass 1 KiB of scores per wave (one DMA
+// op: the head's G query heads x 16 keys, at most 512 bytes).
+template <typename T, int D, int kHeads, int kPass>
+constexpr int decode_stage_bytes() {
+  constexpr int tile = GroupTile<T, D, kHeads>::kBytes;
+  return kPass == kDecodeFused ? 2 * tile : (kPass == kDecodeScores ? tile : tile + kHeads * kWave * 16);
+}
+
+// Ring depth: four stages for the fused pass (two tiles each), as many as
+// fit up to eight for the single-tensor passes, so that every pass keeps
+// about the same bytes in flight with one workgroup per CU.
+template <typename T, int D, int kHeads, int kPass = kDecodeFused>
 constexpr int decode_stages() {
-  constexpr int per_stage = 2 * GroupTile<T, D, kHeads>::kBytes;
-  return kDecodeLdsBudget / per_stage >= 4 ? 4 : (kDecodeLdsBudget / per_stage >= 3 ? 3 : 2);
+  constexpr int per_stage = decode_stage_bytes<T, D, kHeads, kPass>();
+  constexpr int fit = kDecodeLdsBudget / per_stage;
+  if constexpr (kPass == kDecodeFused) return fit >= 4 ? 4 : (fit >= 3 ? 3 : 2);
+  return fit >= 8 ? 8 : (fit >= 2 ? fit : 2);
 }
 
 // One workgroup = one (sequence, key split, head group); wave w handles KV
 // head group*kHeads + w and its GQA query heads.
-template <typename T, int D, bool kUniform, int kHeads>
+template <typename T, int D, bool kUniform, int kHeads, int kPass>
 __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs a, DecodeItems items) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, kHeads>;
-  constexpr int kStages = decode_stages<T, D, kHeads>();
-  constexpr int kStageBytes = 2 * GT::kBytes;  // K tile then V tile
-  constexpr int kOwnOps = 2 * GT::kOpsPerWave;  // DMA ops one wave issues per tile
+  static_assert(kPass == kDecodeFused || Elt<T>::kIsBf16, "the two-pass rounding mode is for bf16");
+  constexpr bool kFetchK = kPass != kDecodePV;
+  constexpr bool kFetchV = kPass != kDecodeScores;
+  constexpr int kVOff = kFetchK ? GT::kBytes : 0;  // the V tile within a stage
+  constexpr int kScoreOff = kVOff + GT::kBytes;   // P.V pass: the scores within a stage
+  constexpr int kStages = decode_stages<T, D, kHeads, kPass>();
+  constexpr int kStageBytes = decode_stage_bytes<T, D, kHeads, kPass>();
+  // DMA ops one wave issues per tile
+  constexpr int kOwnOps = (kFetchK ? GT::kOpsPerWave : 0) + (kFetchV ? GT::kOpsPerWave : 0) + (kPass == kDecodePV);
   constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
   __shared__ __attribute__((aligned(16))) unsigned char ring[kStages][kStageBytes];
 
@@ -1783,7 +1881,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   F qf;
   const bool row_valid = row < a.group;
   const int qh = h * a.group + row;
-  if (row_valid) {
+  if (kPass != kDecodePV && row_valid) {
     load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + b * a.q_sb + qh * a.q_sh);
   } else {
 #pragma unroll
@@ -1792,6 +1890,39 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
 
   SoftmaxState<D> st;
   st.init();
+  // Two-pass rounding: this item's score rows in the workspace, 16-key tile
+  // t of query head qh at ((item * tps + t) * q_heads + qh) * 16 elements
+  const int64_t item = first_item + split;
+  uint16_t* const scores = kPass == kDecodeFused ? nullptr : a.ws_s + item * tps * a.q_heads * kTileKeys;
+  // the item's rows lie in the score buffer (lengths inconsistent with the
+  // host's bounds could place them past it: then no score is written, and
+  // the P.V pass of the item does nothing)
+  const bool scores_ok = kPass != kDecodeFused && a.ws_s != nullptr && (item + 1) * tps * kTileKeys <= a.ws_s_keys;
+  if constexpr (kPass == kDecodePV) {
+    if (!scores_ok) return;  // uniform over the workgroup
+  }
+  // scores pass: this lane's share (keys 4g..4g+3 of every tile) of the
+  // row's sum of e^(s - m) (double, so that the sum carries no rounding
+  // beyond the exponentials'); all four lane groups share the row's m
+  double pl = 0.0;
+  // P.V pass: the row's maximum, sum and 1 / sum over all its splits
+  float row_m = 0.f, row_l = 1.f, row_r = 1.f;
+  if constexpr (kPass == kDecodePV) {
+    // lane group g combines splits g, g + 4, ... (as (max, sum) pairs), then
+    // the four groups combine in a fixed order (rows >= group: m = -inf)
+    float m = kNegInf, l = 0.f;
+    if (row_valid && a.ws_ml != nullptr && first_item + nsplit <= a.ws_items) {
+      for (int64_t s = g; s < nsplit; s += 4) {
+        const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + ((first_item + s) * a.q_heads + qh) * 2);
+        const float mn = score_max(m, ml.x);
+        if (mn != kNegInf) l = l * exp_ref(m - mn) + ml.y * exp_ref(ml.x - mn);
+        m = mn;
+      }
+    }
+    row_m = max_over_groups(m);
+    row_l = sum_over_groups(row_m == kNegInf ? 0.f : l * exp_ref(m - row_m));
+    row_r = 1.f / row_l;
+  }
 
   // Fused append: the workgroup whose split ends the sequence takes the new
   // K/V row of position seq_len - 1.  In wave w, lanes [0, kHeadChunks)
@@ -1847,20 +1978,28 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // position ^ swz(r).  Keys past the end of the split are clamped to its
   // last key (so no lane reads a slot the sequence does not own; those keys
   // are masked to p = 0).
+  // P.V pass: each wave's one score op per tile reads its head's G x 16
+  // scores (2G 16-byte chunks; the other lanes repeat the last chunk)
+  const int score_chunk = min(lane, 2 * a.group - 1) * kEltPerChunk;
   auto issue = [&](int slot, int key0) {
     TileAddr<kUniform, false> ta;  // a split covers <= kTableWindow tiles, so <= kTableWindow blocks
     ta.init(a.geom, table, tlen, tc, key0);
     const int lim = last - key0;
     unsigned char* kdst = &ring[slot][0];
-    unsigned char* vdst = kdst + GT::kBytes;
+    unsigned char* vdst = kdst + kVOff;
 #pragma unroll
     for (int i = 0; i < GT::kOpsPerWave; ++i) {
       const int op = wave + i * kHeads;
       const int r = op * GT::kRowsPerOp + lane / GT::kChunks;
       const int chunk = (lane % GT::kChunks) ^ GT::swz(r);
       const int64_t src = ta.at(a.geom, table, tlen, key0, min(r, lim)) + chunk * kEltPerChunk;
-      lds_dma16<kCacheStream>(kc + src, kdst + op * kWave * 16);
-      lds_dma16<kCacheStream>(vc + src, vdst + op * kWave * 16);
+      if constexpr (kFetchK) lds_dma16<kCacheStream>(kc + src, kdst + op * kWave * 16);
+      if constexpr (kFetchV) lds_dma16<kCacheStream>(vc + src, vdst + op * kWave * 16);
+    }
+    if constexpr (kPass == kDecodePV) {
+      const int t = (key0 - key_begin) / kTileKeys;
+      const uint16_t* src = scores + ((int64_t)t * a.q_heads + h * a.group) * kTileKeys + score_chunk;
+      lds_dma16<kCacheDefault>(src, kdst + kScoreOff + wave * kWave * 16);
     }
   };
 
@@ -1875,34 +2014,76 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   uint32_t vtr[D / 16];         // bf16: transposing reads
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
-    vtr[c] = GT::kBytes + GT::vt_offset(lane, wave, c);
+    vtr[c] = kVOff + GT::vt_offset(lane, wave, c);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, wave, 16 * c + row);
+    for (int e = 0; e < 4; ++e) voff[4 * c + e] = kVOff + GT::elt_offset(4 * g + e, wave, 16 * c + row);
   }
+  // P.V pass: this lane's four scores (keys 4g..4g+3 of query head row) in
+  // its wave's score chunk of a stage
+  const uint32_t soff = kScoreOff + wave * kWave * 16 + row * 2 * kTileKeys + 8 * g;
 
   auto consume = [&](int slot, int key0) {
     const unsigned char* stage = &ring[slot][0];
-    F kf;
-    if constexpr (Elt<T>::kIsBf16) {
-      const uint32_t base = lds_off(stage);
-      uint32_t ka[F::kVec];
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kPass != kDecodePV) {
+      F kf;
+      if constexpr (Elt<T>::kIsBf16) {
+        const uint32_t base = lds_off(stage);
+        uint32_t ka[F::kVec];
 #pragma unroll
-      for (int j = 0; j < F::kVec; ++j) ka[j] = base + koff[j];
-      ring_read_k<F::kVec>(kf.v, ka);
+        for (int j = 0; j < F::kVec; ++j) ka[j] = base + koff[j];
+        ring_read_k<F::kVec>(kf.v, ka);
+      } else {
+#pragma unroll
+        for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
+      }
+      s = qk_mfma<T, D>(kf, qf);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = scaled_score<T>(s[i], a.scale);
+      if (key0 + kTileKeys - 1 > last) {  // only the split's last tile can pass its end
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = (key0 + 4 * g + i <= last) ? s[i] : kNegInf;
+      }
+    }
+    if constexpr (kPass == kDecodeScores) {
+      // the tile's scores (bf16 values, exactly representable) for the P.V
+      // pass, then the row's running maximum and this lane's share of its
+      // sum of e^(s - m), rescaled when the maximum moves
+      if (row_valid && scores_ok) {
+        const int t = (key0 - key_begin) / kTileKeys;
+        *reinterpret_cast<uint2*>(scores + ((int64_t)t * a.q_heads + qh) * kTileKeys + 4 * g) =
+            uint2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+      }
+      const float m_new = score_max(st.m, max_over_groups(score_max(score_max(s[0], s[1]), score_max(s[2], s[3]))));
+      if (m_new != kNegInf) {
+        double add = 0.0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) add += (double)exp_ref(s[i] - m_new);
+        pl = pl * (double)exp_ref(st.m - m_new) + add;
+      }
+      st.m = m_new;
+      return;
+    }
+    v4s pb;
+    if constexpr (kPass == kDecodePV) {
+      // P = bf16(e^(s - m) / l) with the row's (m, l) over all splits:
+      // the reference's normalised probabilities (rows >= group and keys
+      // past the split's end: 0)
+      v2u sv;
+      asm volatile("ds_read_b64 %0, %1" : "=v"(sv) : "v"(lds_off(stage) + soff));
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sv));
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = bf16_bits_to_f32((sv[i / 2] >> (16 * (i % 2))) & 0xffffu);
+        p[i] = (row_valid && key0 + 4 * g + i <= last) ? div_ref(exp_ref(x - row_m), row_l, row_r) : 0.f;
+      }
+      pb = pack_bf16x4(p[0], p[1], p[2], p[3]);
     } else {
-#pragma unroll
-      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
+      softmax_tile<D>(st, s);
+      if constexpr (Elt<T>::kIsBf16) pb = pack_bf16x4(s[0], s[1], s[2], s[3]);
     }
-    v4f s = qk_mfma<T, D>(kf, qf);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = scaled_score<T>(s[i], a.scale);
-    if (key0 + kTileKeys - 1 > last) {  // only the split's last tile can pass its end
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[i] = (key0 + 4 * g + i <= last) ? s[i] : kNegInf;
-    }
-    softmax_tile<D>(st, s);
     if constexpr (Elt<T>::kIsBf16) {
-      const v4s pb = pack_bf16x4(s[0], s[1], s[2], s[3]);
       const uint32_t base = lds_off(stage);
 #pragma unroll
       for (int c0 = 0; c0 < D / 16; c0 += 4) {
@@ -2002,10 +2183,13 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
           // but their V rows still meet p = 0 in the P.V MFMAs, so they must
           // hold the new row, not the slot's old content).  The wait +
           // barrier above ordered the tile's DMA before these writes.
-          const uint32_t base = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)GT::kBytes);
-          for (int rr = pos - key_begin - tt * kTileKeys; rr < kTileKeys; ++rr) {
-            const uint32_t patch = base + (uint32_t)GT::chunk_offset(rr, wave * kHeadChunks + new_c);
-            asm volatile("ds_write_b128 %0, %1" : : "v"(patch), "v"(new_chunk) : "memory");
+          // (the scores pass stages no V: its V lanes only write the cache)
+          if (carries_k || kFetchV) {
+            const uint32_t base = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)kVOff);
+            for (int rr = pos - key_begin - tt * kTileKeys; rr < kTileKeys; ++rr) {
+              const uint32_t patch = base + (uint32_t)GT::chunk_offset(rr, wave * kHeadChunks + new_c);
+              asm volatile("ds_write_b128 %0, %1" : : "v"(patch), "v"(new_chunk) : "memory");
+            }
           }
           asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
         }
@@ -2018,7 +2202,19 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // every fetch has been waited for (the last tile's wait is vmcnt(0))
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   if (carry) *reinterpret_cast<v4u*>(new_dst) = new_chunk;
-  const float lsum = sum_over_groups(st.lsum);
+  if constexpr (kPass == kDecodeScores) {
+    // the split's (max, sum of e^(s - max)) per query head, for the P.V pass
+    // of every split of the sequence (one split included)
+    double tl = pl + __shfl_xor(pl, 16);  // a + b == b + a: every lane gets the same sum
+    tl = tl + __shfl_xor(tl, 32);
+    const float lsum = (float)tl;
+    if (row_valid && g == 0 && a.ws_ml != nullptr && item < a.ws_items) {
+      *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
+    }
+    return;
+  }
+  // the fused pass divides by the row's sum; the P.V pass's P is normalised
+  const float lsum = kPass == kDecodePV ? 1.f : sum_over_groups(st.lsum);
   if (nsplit == 1) {
     if (!row_valid) return;
     const float inv = 1.f / lsum;
@@ -2030,17 +2226,21 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     }
     return;
   }
-  // Split-K: store this split's partial (unnormalised O, running max, sum)
-  // for the merge kernel.  The bound keeps inconsistent length hints from
-  // writing outside the workspace.
-  const int64_t item = first_item + split;
+  // Split-K: store this split's partial (unnormalised O, running max, sum;
+  // in the P.V pass the split's share of the normalised O) for the merge
+  // kernel.  The bound keeps inconsistent length hints from writing outside
+  // the workspace.
   if (!row_valid || a.ws_o == nullptr || item >= a.ws_items) return;
   float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
     *reinterpret_cast<float4*>(dst + 16 * c) = make_float4(st.o[c][0], st.o[c][1], st.o[c][2], st.o[c][3]);
   }
-  if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
+  // (the P.V pass leaves the scores pass's pairs alone: other splits of the
+  // sequence may still be reading them)
+  if (kPass == kDecodeFused && g == 0) {
+    *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
+  }
 }
 
 // Split merge: one wave per (sequence, query head); sequences with a single
@@ -2048,7 +2248,8 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
 // the sum of the split counts of the sequences before it.
 constexpr int kMergeWaves = 4;
 
-template <typename T, int D>
+// kSum: the partials of the two-pass rounding (summed, not weighted).
+template <typename T, int D, bool kSum>
 __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(DecodeArgs a, DecodeItems items) {
   const int64_t b = blockIdx.x;
   const int qh = (int)blockIdx.y * kMergeWaves + (int)(threadIdx.x / kWave);
@@ -2073,6 +2274,11 @@ __global__ __launch_bounds__(kMergeWaves* kWave) void decode_merge_kernel(Decode
   }
   if (nsplit <= 1) return;
   if (first + nsplit > a.ws_items) return;
+  if constexpr (kSum) {
+    sum_row<T, D>(a.ws_o + (first * a.q_heads + qh) * D, (int64_t)a.q_heads * D, (int)nsplit,
+                  reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh);
+    return;
+  }
   merge_row<T, D>(a.ws_o + (first * a.q_heads + qh) * D, (int64_t)a.q_heads * D,
                   a.ws_ml + (first * a.q_heads + qh) * 2, (int64_t)a.q_heads * 2, (int)nsplit,
                   reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh);
@@ -2144,6 +2350,38 @@ struct DecodePlan {
 int64_t decode_max_items(int64_t batch, int64_t total_seq_len, int64_t tps) {
   // sum_b ceil(ceil(len_b/16)/tps) <= (sum_b len_b/16 + batch)/tps + batch
   return (cdiv(total_seq_len, kTileKeys) + batch) / tps + batch + 1;
+}
+
+// Rounding point of the bf16 attention probabilities, process-wide
+// (nie_set_attention_rounding): NIE_ROUND_REFERENCE, the reference's (two
+// passes), or NIE_ROUND_FAST (one pass, online softmax).
+std::atomic<int> g_rounding{NIE_ROUND_REFERENCE};
+
+bool two_pass(int dtype) {
+  return dtype == NIE_DTYPE_BF16 && g_rounding.load(std::memory_order_relaxed) == NIE_ROUND_REFERENCE;
+}
+
+// Key slots (16 per tile of every item) of the two-pass score buffer: items
+// x tps x 16.  With the split length chosen on the device (tps 0) the items
+// of a sequence cover at most its tiles + tps - 1 slots' worth of tiles, so
+// items x tps <= sum of tiles + batch x (kDecodeMaxTilesPerSplit - 1).
+int64_t decode_score_keys(const DecodePlan& p, int64_t batch, int64_t total_seq_len) {
+  if (p.tps > 0) return p.items * p.tps * kTileKeys;
+  return (cdiv(total_seq_len, kTileKeys) + batch * kDecodeMaxTilesPerSplit) * kTileKeys;
+}
+
+// Workspace of a decode call: the partial O rows (items x q_heads x head_dim
+// floats), the (max, sum) pairs (items x q_heads x 2 floats), and with the
+// two-pass rounding the scores (key slots x q_heads bf16), 256-byte aligned.
+int64_t decode_ws_partials(const DecodePlan& p, int64_t q_heads, int64_t head_dim) {
+  return (p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float) + 255) / 256 * 256;
+}
+
+int64_t decode_workspace_need(const DecodePlan& p, int64_t q_heads, int64_t head_dim, int64_t batch,
+                              int64_t total_seq_len, bool two) {
+  const int64_t partials = p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
+  if (!two) return partials;
+  return decode_ws_partials(p, q_heads, head_dim) + decode_score_keys(p, batch, total_seq_len) * q_heads * 2;
 }
 
 // ---------------------------------------------------------------------------
@@ -3748,7 +3986,8 @@ template <typename T, int D, bool U, int H>
 int decode_resident() {
   static const int n = [] {
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_kernel<T, D, U, H>, H * kWave, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_kernel<T, D, U, H, kDecodeFused>,
+                                                     H * kWave, 0) !=
             hipSuccess ||
         blocks < 1) {
       (void)hipGetLastError();
@@ -3788,21 +4027,21 @@ int decode_resident_u(int heads) {
   }
 }
 
-template <typename T, int D, bool U, int H>
+template <typename T, int D, bool U, int H, int P>
 void launch_decode_h(const DecodeArgs& a, const DecodeItems& items, int64_t grid_items, hipStream_t stream) {
   const dim3 grid((unsigned)grid_items, (unsigned)(a.geom.kv_heads / H));
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a, items);
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H, P>), grid, dim3(H * kWave), 0, stream, a, items);
 }
 
-template <typename T, int D, bool U>
+template <typename T, int D, bool U, int P = kDecodeFused>
 void launch_decode_u(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& items, hipStream_t stream) {
   constexpr int kMax = decode_max_heads<T, D>();
   const int64_t n = items.count > 0 ? items.count : p.items;
   switch (p.heads) {
-    case 1: launch_decode_h<T, D, U, 1>(a, items, n, stream); break;
-    case 2: launch_decode_h<T, D, U, heads_clamp<kMax, 2>()>(a, items, n, stream); break;
-    case 4: launch_decode_h<T, D, U, heads_clamp<kMax, 4>()>(a, items, n, stream); break;
-    default: launch_decode_h<T, D, U, heads_clamp<kMax, 8>()>(a, items, n, stream); break;
+    case 1: launch_decode_h<T, D, U, 1, P>(a, items, n, stream); break;
+    case 2: launch_decode_h<T, D, U, heads_clamp<kMax, 2>(), P>(a, items, n, stream); break;
+    case 4: launch_decode_h<T, D, U, heads_clamp<kMax, 4>(), P>(a, items, n, stream); break;
+    default: launch_decode_h<T, D, U, heads_clamp<kMax, 8>(), P>(a, items, n, stream); break;
   }
 }
 
@@ -3920,7 +4159,29 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& 
   else launch_decode_u<T, D, false>(a, p, items, stream);
   if (merge) {
     const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv((int64_t)a.q_heads, (int64_t)kMergeWaves));
-    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a, items);
+    hipLaunchKernelGGL((decode_merge_kernel<T, D, false>), mgrid, dim3(kMergeWaves * kWave), 0, stream, a, items);
+  }
+}
+
+// The two-pass rounding: the scores pass (with the fused append and RoPE),
+// then the P.V pass over the cache it appended to, then the sum of the
+// split partials.
+template <typename T, int D>
+void launch_decode_two_pass(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& items, hipStream_t stream,
+                            bool merge) {
+  DecodeArgs pv = a;
+  pv.k_new = pv.v_new = nullptr;
+  pv.rope_cos = pv.rope_sin = nullptr;
+  if (uniform_tiles(a.geom)) {
+    launch_decode_u<T, D, true, kDecodeScores>(a, p, items, stream);
+    launch_decode_u<T, D, true, kDecodePV>(pv, p, items, stream);
+  } else {
+    launch_decode_u<T, D, false, kDecodeScores>(a, p, items, stream);
+    launch_decode_u<T, D, false, kDecodePV>(pv, p, items, stream);
+  }
+  if (merge) {
+    const dim3 mgrid((unsigned)a.batch, (unsigned)cdiv((int64_t)a.q_heads, (int64_t)kMergeWaves));
+    hipLaunchKernelGGL((decode_merge_kernel<T, D, true>), mgrid, dim3(kMergeWaves * kWave), 0, stream, pv, items);
   }
 }
 
@@ -4417,8 +4678,18 @@ NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64
   if (host_seq_lens != nullptr && !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) return 0;
   if (!tuned_attention(head_dim, q_heads, kv_heads)) return 0;  // the generic kernel needs no workspace
   const DecodePlan p = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
-  return p.items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
+  return decode_workspace_need(p, q_heads, head_dim, batch, total_seq_len, two_pass(dtype));
 }
+
+NIE_API int nie_set_attention_rounding(int mode) {
+  if (mode != NIE_ROUND_REFERENCE && mode != NIE_ROUND_FAST) {
+    return fail(NIE_EINVAL, "attention rounding must be NIE_ROUND_REFERENCE or NIE_ROUND_FAST");
+  }
+  g_rounding.store(mode, std::memory_order_relaxed);
+  return NIE_OK;
+}
+
+NIE_API int nie_attention_rounding(void) { return g_rounding.load(std::memory_order_relaxed); }
 
 namespace {
 
@@ -4554,8 +4825,11 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   const int64_t tps = plan.tps;  // 0: chosen on the device, at least kDecodeMinTilesPerSplit
   const int64_t items = plan.items;
   const bool may_split = cdiv(max_seq_len, kTileKeys) > (tps > 0 ? tps : kDecodeMinTilesPerSplit);
-  const int64_t need = items * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
-  if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
+  // the two-pass rounding always needs the workspace (its score buffer and
+  // the (max, sum) pairs of every split, one split included)
+  const bool two = two_pass(dtype);
+  const int64_t need = decode_workspace_need(plan, q_heads, head_dim, batch, total_seq_len, two);
+  if ((may_split || two) && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     if (static_scratch) {
       return fail(NIE_EINVAL,
                   "split partials need %lld bytes, beyond the %lld-byte static scratch of the allocation-free "
@@ -4590,6 +4864,11 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + items * q_heads * head_dim : nullptr;
   a.ws_items = have_ws ? items : 0;
+  if (two && have_ws) {
+    a.ws_s = reinterpret_cast<uint16_t*>(reinterpret_cast<unsigned char*>(workspace) +
+                                         decode_ws_partials(plan, q_heads, head_dim));
+    a.ws_s_keys = decode_score_keys(plan, batch, total_seq_len);
+  }
   a.k_new = append.k_new;
   a.v_new = append.v_new;
   a.kn_s = append.k_stride;
@@ -4602,7 +4881,10 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   DecodeItems work;
   fill_decode_items(plan, host_seq_lens, batch, &work);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NIE_DTYPE_BF16) {
+  if (two) {
+    if (head_dim == 64) launch_decode_two_pass<bf16_t, 64>(a, plan, work, s, may_split);
+    else launch_decode_two_pass<bf16_t, 128>(a, plan, work, s, may_split);
+  } else if (dtype == NIE_DTYPE_BF16) {
     if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, work, s, may_split);
     else launch_decode<bf16_t, 128>(a, plan, work, s, may_split);
   } else {

@@ -20,6 +20,11 @@ LIBRARY_NAME = "libnie_hip.so"
 NIE_DTYPE_F32 = 0
 NIE_DTYPE_BF16 = 1
 
+#: Rounding points of the bf16 attention probabilities (``set_attention_rounding``).
+NIE_ROUND_REFERENCE = 0
+NIE_ROUND_FAST = 1
+ROUNDING_MODES = {"reference": NIE_ROUND_REFERENCE, "fast": NIE_ROUND_FAST}
+
 _DTYPE_CODES = {torch.float32: NIE_DTYPE_F32, torch.bfloat16: NIE_DTYPE_BF16}
 
 #: Head dims and GQA group sizes the attention kernels are built for.
@@ -55,6 +60,8 @@ EXPORTED_SYMBOLS = (
     "nie_silu_mul",
     "nie_linear_rows",
     "nie_rms_norm_linear_rows",
+    "nie_set_attention_rounding",
+    "nie_attention_rounding",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
@@ -113,6 +120,8 @@ _SIGNATURES = {
         _i32,
         [_i32, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _f32, _i64, _ptr, _i64, _i64, _i32, _ptr, _i64, _ptr],
     ),
+    "nie_set_attention_rounding": (_i32, [_i32]),
+    "nie_attention_rounding": (_i32, []),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
@@ -290,6 +299,29 @@ def load_library() -> ctypes.CDLL:
 
 def version() -> str:
     return load_library().nie_version().decode()
+
+
+def set_attention_rounding(mode: str) -> None:
+    """Where the bf16 attention kernels round the softmax probabilities, for
+    every launch made after this call in the process.
+
+    ``"reference"`` (the default): the reference's rounding point, the
+    normalised probabilities exp(s - m) / l cast to bf16 before P.V
+    (``layers/paged_attention.py:109-114``, ``layers/attention.py:410-411``),
+    with two passes over the keys.  ``"fast"``: one pass with an online
+    softmax, exp(s - running max) cast to bf16 and the row divided by its sum
+    at the end.  Prepared launches size their workspace for the mode of the
+    moment they are built.
+    """
+    if mode not in ROUNDING_MODES:
+        raise ValueError(f"attention rounding must be one of {sorted(ROUNDING_MODES)}, not {mode!r}")
+    _check(load_library().nie_set_attention_rounding(ROUNDING_MODES[mode]), "nie_set_attention_rounding")
+
+
+def attention_rounding() -> str:
+    """The rounding mode of ``set_attention_rounding``."""
+    code = load_library().nie_attention_rounding()
+    return next(name for name, value in ROUNDING_MODES.items() if value == code)
 
 
 def _check(rc: int, what: str) -> None:

@@ -342,7 +342,31 @@ def test_library_exports_every_header_symbol():
     assert lib.nie_version().decode().startswith("nie_paged")
 
 
-def test_library_workspace_queries():
+@pytest.fixture
+def fast_rounding():
+    """The one-pass (online softmax) rounding mode for the test's duration."""
+    _native.set_attention_rounding("fast")
+    try:
+        yield
+    finally:
+        _native.set_attention_rounding("reference")
+
+
+def test_attention_rounding_mode_switch():
+    assert _native.attention_rounding() == "reference"  # the default: the reference's rounding point
+    lib = _native.load_library()
+    try:
+        _native.set_attention_rounding("fast")
+        assert _native.attention_rounding() == "fast" and lib.nie_attention_rounding() == _native.NIE_ROUND_FAST
+    finally:
+        _native.set_attention_rounding("reference")
+    assert lib.nie_attention_rounding() == _native.NIE_ROUND_REFERENCE
+    assert lib.nie_set_attention_rounding(7) == -1 and b"NIE_ROUND" in lib.nie_last_error()
+    with pytest.raises(ValueError, match="attention rounding"):
+        _native.set_attention_rounding("exact")
+
+
+def test_library_workspace_queries(fast_rounding):
     lib = _native.load_library()
     # decode partials: items * q_heads * (head_dim + 2) floats, items bounded by the split count
     small = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710, None)
@@ -351,6 +375,15 @@ def test_library_workspace_queries():
     assert big >= small
     # at most 128 tiles of 16 keys per split (the block-table window): at least 16 * ceil(1850 / 128) items
     assert big >= 16 * 15 * 32 * 66 * 4
+    # the reference rounding adds a bf16 score for every key slot of every query head: planned on the
+    # device, (tiles + 128 per sequence) * 16 slots; fp32 calls do not round probabilities (no scores)
+    _native.set_attention_rounding("reference")
+    ref = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710, None)
+    assert ref == -(-small // 256) * 256 + (-(-710 // 16) + 4 * 128) * 16 * 32 * 2
+    assert (lib.nie_paged_decode_workspace_bytes(0, 4, 32, 8, 64, 16, 500, 710, None)
+            == lib.nie_paged_decode_workspace_bytes(0, 4, 32, 8, 64, 16, 500, 710, None))
+    _native.set_attention_rounding("fast")
+    assert lib.nie_paged_decode_workspace_bytes(0, 4, 32, 8, 64, 16, 500, 710, None) > 0
     assert lib.nie_paged_decode_workspace_bytes(1, 0, 32, 8, 64, 16, 1, 1, None) == 0
     assert lib.nie_paged_decode_workspace_bytes(7, 4, 32, 8, 64, 16, 500, 710, None) == 0  # bad dtype
     # head_dim 96 and GQA group 3 run on the generic kernel, which needs no workspace
@@ -375,9 +408,16 @@ def test_library_decode_plan_from_host_lengths():
         lens = np.asarray(lens, dtype=np.int32)
         return lib.nie_paged_decode_workspace_bytes(1, len(lens), 32, 8, 64, 16, mx, total, lens.ctypes.data)
 
-    assert query([29600] * 16, 29600, 16 * 29600) == 256 * 32 * 66 * 4
-    # the bound-based plan (124-tile splits: 240 items) sizes for an upper bound on its items
-    assert lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None) >= 240 * 32 * 66 * 4
+    # reference rounding: the partials, then a bf16 score per key slot (256 items x 116 tiles x 16) and head
+    assert query([29600] * 16, 29600, 16 * 29600) == 256 * 32 * 66 * 4 + 256 * 116 * 16 * 32 * 2
+    _native.set_attention_rounding("fast")
+    try:
+        assert query([29600] * 16, 29600, 16 * 29600) == 256 * 32 * 66 * 4
+        # the bound-based plan (124-tile splits: 240 items) sizes for an upper bound on its items
+        assert (lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None)
+                >= 240 * 32 * 66 * 4)
+    finally:
+        _native.set_attention_rounding("reference")
     assert query([29600] * 16, 29600, 16 * 29600 - 1) == 0  # sum does not match
     assert query([29600] * 15 + [0], 29600, 15 * 29600) == 0  # a length below 1
 
