@@ -64,6 +64,9 @@ def parse_args():
                    help="also replay on the bf16 variant with fp32 attention products")
     p.add_argument("--native-gemm", choices=["on", "off"], default="on",
                    help="serving legs: decode-step projections on nie_linear_rows (on) or torch's GEMM (off)")
+    p.add_argument("--rounding", choices=["reference", "fast"], default="reference",
+                   help="bf16 attention probabilities: the reference's rounding point (normalised P cast to bf16, "
+                        "two passes) or one pass with an online softmax")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 4 device-to-device copies of MIB MiB (reference for HBM byte counters)")
     return p.parse_args()
@@ -927,6 +930,7 @@ def main():
     from nano_infer_engine import _native
 
     _native.load_library()
+    _native.set_attention_rounding(args.rounding)
     only = {
         "decode": ("decode", run_decode), "small": ("decode_small", run_decode_small),
         "stress": ("stress_16x29600", lambda a: {"attention": run_stress(a), "full_model": run_stress_model(a)}),

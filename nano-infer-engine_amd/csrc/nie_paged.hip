@@ -138,6 +138,18 @@ __device__ __forceinline__ v4s pack_bf16x4(float x0, float x1, float x2, float x
   return __builtin_bit_cast(v4s, u32x2_t{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)});
 }
 
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// Two 4-element bf16 operands (sub-tile a's keys, then sub-tile b's) as one
+// 8-element 16x16x32 operand.  With it, K slot 8(l/16) + e of an MFMA is key
+// 4(l/16) + e of sub-tile a for e < 4 and key 4(l/16) + e - 4 of sub-tile b
+// otherwise, the same on the V^T and the P^T side.
+__device__ __forceinline__ bf16x8_t join_bf16x4(v4s a, v4s b) {
+  const u32x2_t lo = __builtin_bit_cast(u32x2_t, a);
+  const u32x2_t hi = __builtin_bit_cast(u32x2_t, b);
+  return __builtin_bit_cast(bf16x8_t, v4u{lo[0], lo[1], hi[0], hi[1]});
+}
+
 // 2^x on v_exp_f32 (results below 2^-126 flush to zero, which the softmax
 // sums cannot resolve anyway).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -1083,7 +1095,6 @@ struct GroupTile {
 // lgkmcnt(0) asm takes every result as a read-write operand, so no use of a
 // result can be scheduled before the data has arrived.
 // ---------------------------------------------------------------------------
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -1775,53 +1786,22 @@ constexpr int decode_max_heads() {
 
 constexpr int kDecodeLdsBudget = 160 * 1024;
 
-// Passes of a decode call.  kDecodeFused: one pass, the online softmax
-// (bf16 P = exp(s - running max), O / l at the end).  With the reference's
-// rounding point (the normalised probabilities rounded to bf16 before P.V,
-// layers/paged_attention.py:109-114) two passes over the keys:
-// kDecodeScores reads K, writes every key's score (bf16, the value the
-// reference feeds its softmax) and each split's (max, sum of exp); then
-// kDecodePV reads V and those scores, forms each row's (max, sum) over all
-// its splits, and accumulates bf16(e^(s - m) / l) . V in fp32.
-constexpr int kDecodeFused = 0;
-constexpr int kDecodeScores = 1;
-constexpr int kDecodePV = 2;
 
-// LDS stage of a decode pass: the K tile and/or the V tile of all the
-// workgroup's heads, and in the P.V pass 1 KiB of scores per wave (one DMA
-// op: the head's G query heads x 16 keys, at most 512 bytes).
-template <typename T, int D, int kHeads, int kPass>
-constexpr int decode_stage_bytes() {
-  constexpr int tile = GroupTile<T, D, kHeads>::kBytes;
-  return kPass == kDecodeFused ? 2 * tile : (kPass == kDecodeScores ? tile : tile + kHeads * kWave * 16);
-}
-
-// Ring depth: four stages for the fused pass (two tiles each), as many as
-// fit up to eight for the single-tensor passes, so that every pass keeps
-// about the same bytes in flight with one workgroup per CU.
-template <typename T, int D, int kHeads, int kPass = kDecodeFused>
+template <typename T, int D, int kHeads>
 constexpr int decode_stages() {
-  constexpr int per_stage = decode_stage_bytes<T, D, kHeads, kPass>();
-  constexpr int fit = kDecodeLdsBudget / per_stage;
-  if constexpr (kPass == kDecodeFused) return fit >= 4 ? 4 : (fit >= 3 ? 3 : 2);
-  return fit >= 8 ? 8 : (fit >= 2 ? fit : 2);
+  constexpr int per_stage = 2 * GroupTile<T, D, kHeads>::kBytes;
+  return kDecodeLdsBudget / per_stage >= 4 ? 4 : (kDecodeLdsBudget / per_stage >= 3 ? 3 : 2);
 }
 
 // One workgroup = one (sequence, key split, head group); wave w handles KV
 // head group*kHeads + w and its GQA query heads.
-template <typename T, int D, bool kUniform, int kHeads, int kPass>
+template <typename T, int D, bool kUniform, int kHeads>
 __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs a, DecodeItems items) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, kHeads>;
-  static_assert(kPass == kDecodeFused || Elt<T>::kIsBf16, "the two-pass rounding mode is for bf16");
-  constexpr bool kFetchK = kPass != kDecodePV;
-  constexpr bool kFetchV = kPass != kDecodeScores;
-  constexpr int kVOff = kFetchK ? GT::kBytes : 0;  // the V tile within a stage
-  constexpr int kScoreOff = kVOff + GT::kBytes;   // P.V pass: the scores within a stage
-  constexpr int kStages = decode_stages<T, D, kHeads, kPass>();
-  constexpr int kStageBytes = decode_stage_bytes<T, D, kHeads, kPass>();
-  // DMA ops one wave issues per tile
-  constexpr int kOwnOps = (kFetchK ? GT::kOpsPerWave : 0) + (kFetchV ? GT::kOpsPerWave : 0) + (kPass == kDecodePV);
+  constexpr int kStages = decode_stages<T, D, kHeads>();
+  constexpr int kStageBytes = 2 * GT::kBytes;  // K tile then V tile
+  constexpr int kOwnOps = 2 * GT::kOpsPerWave;  // DMA ops one wave issues per tile
   constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
   __shared__ __attribute__((aligned(16))) unsigned char ring[kStages][kStageBytes];
 
@@ -1881,7 +1861,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   F qf;
   const bool row_valid = row < a.group;
   const int qh = h * a.group + row;
-  if (kPass != kDecodePV && row_valid) {
+  if (row_valid) {
     load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + b * a.q_sb + qh * a.q_sh);
   } else {
 #pragma unroll
@@ -1890,39 +1870,6 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
 
   SoftmaxState<D> st;
   st.init();
-  // Two-pass rounding: this item's score rows in the workspace, 16-key tile
-  // t of query head qh at ((item * tps + t) * q_heads + qh) * 16 elements
-  const int64_t item = first_item + split;
-  uint16_t* const scores = kPass == kDecodeFused ? nullptr : a.ws_s + item * tps * a.q_heads * kTileKeys;
-  // the item's rows lie in the score buffer (lengths inconsistent with the
-  // host's bounds could place them past it: then no score is written, and
-  // the P.V pass of the item does nothing)
-  const bool scores_ok = kPass != kDecodeFused && a.ws_s != nullptr && (item + 1) * tps * kTileKeys <= a.ws_s_keys;
-  if constexpr (kPass == kDecodePV) {
-    if (!scores_ok) return;  // uniform over the workgroup
-  }
-  // scores pass: this lane's share (keys 4g..4g+3 of every tile) of the
-  // row's sum of e^(s - m) (double, so that the sum carries no rounding
-  // beyond the exponentials'); all four lane groups share the row's m
-  double pl = 0.0;
-  // P.V pass: the row's maximum, sum and 1 / sum over all its splits
-  float row_m = 0.f, row_l = 1.f, row_r = 1.f;
-  if constexpr (kPass == kDecodePV) {
-    // lane group g combines splits g, g + 4, ... (as (max, sum) pairs), then
-    // the four groups combine in a fixed order (rows >= group: m = -inf)
-    float m = kNegInf, l = 0.f;
-    if (row_valid && a.ws_ml != nullptr && first_item + nsplit <= a.ws_items) {
-      for (int64_t s = g; s < nsplit; s += 4) {
-        const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + ((first_item + s) * a.q_heads + qh) * 2);
-        const float mn = score_max(m, ml.x);
-        if (mn != kNegInf) l = l * exp_ref(m - mn) + ml.y * exp_ref(ml.x - mn);
-        m = mn;
-      }
-    }
-    row_m = max_over_groups(m);
-    row_l = sum_over_groups(row_m == kNegInf ? 0.f : l * exp_ref(m - row_m));
-    row_r = 1.f / row_l;
-  }
 
   // Fused append: the workgroup whose split ends the sequence takes the new
   // K/V row of position seq_len - 1.  In wave w, lanes [0, kHeadChunks)
@@ -1978,28 +1925,20 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // position ^ swz(r).  Keys past the end of the split are clamped to its
   // last key (so no lane reads a slot the sequence does not own; those keys
   // are masked to p = 0).
-  // P.V pass: each wave's one score op per tile reads its head's G x 16
-  // scores (2G 16-byte chunks; the other lanes repeat the last chunk)
-  const int score_chunk = min(lane, 2 * a.group - 1) * kEltPerChunk;
   auto issue = [&](int slot, int key0) {
     TileAddr<kUniform, false> ta;  // a split covers <= kTableWindow tiles, so <= kTableWindow blocks
     ta.init(a.geom, table, tlen, tc, key0);
     const int lim = last - key0;
     unsigned char* kdst = &ring[slot][0];
-    unsigned char* vdst = kdst + kVOff;
+    unsigned char* vdst = kdst + GT::kBytes;
 #pragma unroll
     for (int i = 0; i < GT::kOpsPerWave; ++i) {
       const int op = wave + i * kHeads;
       const int r = op * GT::kRowsPerOp + lane / GT::kChunks;
       const int chunk = (lane % GT::kChunks) ^ GT::swz(r);
       const int64_t src = ta.at(a.geom, table, tlen, key0, min(r, lim)) + chunk * kEltPerChunk;
-      if constexpr (kFetchK) lds_dma16<kCacheStream>(kc + src, kdst + op * kWave * 16);
-      if constexpr (kFetchV) lds_dma16<kCacheStream>(vc + src, vdst + op * kWave * 16);
-    }
-    if constexpr (kPass == kDecodePV) {
-      const int t = (key0 - key_begin) / kTileKeys;
-      const uint16_t* src = scores + ((int64_t)t * a.q_heads + h * a.group) * kTileKeys + score_chunk;
-      lds_dma16<kCacheDefault>(src, kdst + kScoreOff + wave * kWave * 16);
+      lds_dma16<kCacheStream>(kc + src, kdst + op * kWave * 16);
+      lds_dma16<kCacheStream>(vc + src, vdst + op * kWave * 16);
     }
   };
 
@@ -2014,76 +1953,34 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   uint32_t vtr[D / 16];         // bf16: transposing reads
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
-    vtr[c] = kVOff + GT::vt_offset(lane, wave, c);
+    vtr[c] = GT::kBytes + GT::vt_offset(lane, wave, c);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) voff[4 * c + e] = kVOff + GT::elt_offset(4 * g + e, wave, 16 * c + row);
+    for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, wave, 16 * c + row);
   }
-  // P.V pass: this lane's four scores (keys 4g..4g+3 of query head row) in
-  // its wave's score chunk of a stage
-  const uint32_t soff = kScoreOff + wave * kWave * 16 + row * 2 * kTileKeys + 8 * g;
 
   auto consume = [&](int slot, int key0) {
     const unsigned char* stage = &ring[slot][0];
-    v4f s = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (kPass != kDecodePV) {
-      F kf;
-      if constexpr (Elt<T>::kIsBf16) {
-        const uint32_t base = lds_off(stage);
-        uint32_t ka[F::kVec];
-#pragma unroll
-        for (int j = 0; j < F::kVec; ++j) ka[j] = base + koff[j];
-        ring_read_k<F::kVec>(kf.v, ka);
-      } else {
-#pragma unroll
-        for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
-      }
-      s = qk_mfma<T, D>(kf, qf);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[i] = scaled_score<T>(s[i], a.scale);
-      if (key0 + kTileKeys - 1 > last) {  // only the split's last tile can pass its end
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] = (key0 + 4 * g + i <= last) ? s[i] : kNegInf;
-      }
-    }
-    if constexpr (kPass == kDecodeScores) {
-      // the tile's scores (bf16 values, exactly representable) for the P.V
-      // pass, then the row's running maximum and this lane's share of its
-      // sum of e^(s - m), rescaled when the maximum moves
-      if (row_valid && scores_ok) {
-        const int t = (key0 - key_begin) / kTileKeys;
-        *reinterpret_cast<uint2*>(scores + ((int64_t)t * a.q_heads + qh) * kTileKeys + 4 * g) =
-            uint2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
-      }
-      const float m_new = score_max(st.m, max_over_groups(score_max(score_max(s[0], s[1]), score_max(s[2], s[3]))));
-      if (m_new != kNegInf) {
-        double add = 0.0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) add += (double)exp_ref(s[i] - m_new);
-        pl = pl * (double)exp_ref(st.m - m_new) + add;
-      }
-      st.m = m_new;
-      return;
-    }
-    v4s pb;
-    if constexpr (kPass == kDecodePV) {
-      // P = bf16(e^(s - m) / l) with the row's (m, l) over all splits:
-      // the reference's normalised probabilities (rows >= group and keys
-      // past the split's end: 0)
-      v2u sv;
-      asm volatile("ds_read_b64 %0, %1" : "=v"(sv) : "v"(lds_off(stage) + soff));
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sv));
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = bf16_bits_to_f32((sv[i / 2] >> (16 * (i % 2))) & 0xffffu);
-        p[i] = (row_valid && key0 + 4 * g + i <= last) ? div_ref(exp_ref(x - row_m), row_l, row_r) : 0.f;
-      }
-      pb = pack_bf16x4(p[0], p[1], p[2], p[3]);
-    } else {
-      softmax_tile<D>(st, s);
-      if constexpr (Elt<T>::kIsBf16) pb = pack_bf16x4(s[0], s[1], s[2], s[3]);
-    }
+    F kf;
     if constexpr (Elt<T>::kIsBf16) {
+      const uint32_t base = lds_off(stage);
+      uint32_t ka[F::kVec];
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) ka[j] = base + koff[j];
+      ring_read_k<F::kVec>(kf.v, ka);
+    } else {
+#pragma unroll
+      for (int j = 0; j < F::kVec; ++j) kf.v[j] = *reinterpret_cast<const uint4*>(stage + koff[j]);
+    }
+    v4f s = qk_mfma<T, D>(kf, qf);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = scaled_score<T>(s[i], a.scale);
+    if (key0 + kTileKeys - 1 > last) {  // only the split's last tile can pass its end
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = (key0 + 4 * g + i <= last) ? s[i] : kNegInf;
+    }
+    softmax_tile<D>(st, s);
+    if constexpr (Elt<T>::kIsBf16) {
+      const v4s pb = pack_bf16x4(s[0], s[1], s[2], s[3]);
       const uint32_t base = lds_off(stage);
 #pragma unroll
       for (int c0 = 0; c0 < D / 16; c0 += 4) {
@@ -2183,13 +2080,10 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
           // but their V rows still meet p = 0 in the P.V MFMAs, so they must
           // hold the new row, not the slot's old content).  The wait +
           // barrier above ordered the tile's DMA before these writes.
-          // (the scores pass stages no V: its V lanes only write the cache)
-          if (carries_k || kFetchV) {
-            const uint32_t base = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)kVOff);
-            for (int rr = pos - key_begin - tt * kTileKeys; rr < kTileKeys; ++rr) {
-              const uint32_t patch = base + (uint32_t)GT::chunk_offset(rr, wave * kHeadChunks + new_c);
-              asm volatile("ds_write_b128 %0, %1" : : "v"(patch), "v"(new_chunk) : "memory");
-            }
+          const uint32_t base = lds_off(&ring[j][0]) + (carries_k ? 0u : (uint32_t)GT::kBytes);
+          for (int rr = pos - key_begin - tt * kTileKeys; rr < kTileKeys; ++rr) {
+            const uint32_t patch = base + (uint32_t)GT::chunk_offset(rr, wave * kHeadChunks + new_c);
+            asm volatile("ds_write_b128 %0, %1" : : "v"(patch), "v"(new_chunk) : "memory");
           }
           asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
         }
@@ -2202,19 +2096,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // every fetch has been waited for (the last tile's wait is vmcnt(0))
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   if (carry) *reinterpret_cast<v4u*>(new_dst) = new_chunk;
-  if constexpr (kPass == kDecodeScores) {
-    // the split's (max, sum of e^(s - max)) per query head, for the P.V pass
-    // of every split of the sequence (one split included)
-    double tl = pl + __shfl_xor(pl, 16);  // a + b == b + a: every lane gets the same sum
-    tl = tl + __shfl_xor(tl, 32);
-    const float lsum = (float)tl;
-    if (row_valid && g == 0 && a.ws_ml != nullptr && item < a.ws_items) {
-      *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
-    }
-    return;
-  }
-  // the fused pass divides by the row's sum; the P.V pass's P is normalised
-  const float lsum = kPass == kDecodePV ? 1.f : sum_over_groups(st.lsum);
+  const float lsum = sum_over_groups(st.lsum);
   if (nsplit == 1) {
     if (!row_valid) return;
     const float inv = 1.f / lsum;
@@ -2226,20 +2108,514 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     }
     return;
   }
-  // Split-K: store this split's partial (unnormalised O, running max, sum;
-  // in the P.V pass the split's share of the normalised O) for the merge
-  // kernel.  The bound keeps inconsistent length hints from writing outside
-  // the workspace.
+  // Split-K: store this split's partial (unnormalised O, running max, sum)
+  // for the merge kernel.  The bound keeps inconsistent length hints from
+  // writing outside the workspace.
+  const int64_t item = first_item + split;
   if (!row_valid || a.ws_o == nullptr || item >= a.ws_items) return;
   float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
     *reinterpret_cast<float4*>(dst + 16 * c) = make_float4(st.o[c][0], st.o[c][1], st.o[c][2], st.o[c][3]);
   }
-  // (the P.V pass leaves the scores pass's pairs alone: other splits of the
-  // sequence may still be reading them)
-  if (kPass == kDecodeFused && g == 0) {
-    *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
+  if (g == 0) *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(st.m, lsum);
+}
+
+// ---------------------------------------------------------------------------
+// Decode with the reference's rounding point.  paged_decode_kernel rounds
+// exp(s - running max) to bf16 and divides O by the row sum at the end; the
+// reference rounds the normalised probabilities exp(s - m) / l to bf16
+// before P.V (layers/paged_attention.py:109-114), which needs each row's
+// final (m, l) before any probability is formed.  Two passes over the keys,
+// each a launch of decode_pass_kernel over the same work items:
+//   kDecodeScores reads K, writes every key's score bf16(bf16(q.k) * scale)
+//     (the reference's softmax input) to the workspace, and each split's
+//     (max, sum of e^(s - max)) (the sum in fp64 from exponentials accurate
+//     to about an ulp, so the only rounding left is the exponentials');
+//   kDecodePV reads V and the scores, combines its row's (m, l) over all the
+//     sequence's splits, and accumulates bf16(e^(s - m) / l) . V in fp32:
+//     its share of the normalised output, which decode_merge_kernel<kSum>
+//     adds up over the splits (or, with one split, it rounds and stores).
+// Each pass reads one of K and V, half the bytes of the fused kernel per
+// key, so a loop iteration covers two 16-key tiles (32 keys): one barrier
+// and one dependent chain (LDS read, MFMA, softmax arithmetic) per 32 KiB
+// of a workgroup's heads instead of per 16 KiB, with v_mfma_f32_16x16x32_bf16
+// joining the two tiles (K slot 8(l/16) + e is key 4(l/16) + e of the first
+// tile for e < 4 and of the second otherwise, on both operands).  The
+// scores pass also does the fused append (and RoPE): the new K row patches
+// its LDS copy, and the new K and V rows go to the cache, which the P.V
+// pass then reads.
+// Score layout: item i, KV head h, tile t, query row n (of the group),
+// key k at (((i * kv_heads + h) * tps + t) * group + n) * 16 + k, bf16.
+// ---------------------------------------------------------------------------
+constexpr int kDecodeScores = 1;
+constexpr int kDecodePV = 2;
+constexpr int kPassStepTiles = 2;  // 16-key tiles per loop iteration
+
+template <typename T, int D, int kHeads, int kPass>
+constexpr int decode_pass_stage_bytes() {
+  constexpr int tiles = kPassStepTiles * GroupTile<T, D, kHeads>::kBytes;
+  // the P.V pass adds 1 KiB of scores per wave (one DMA op: the head's
+  // group x 32 keys, at most 1 KiB)
+  return kPass == kDecodeScores ? tiles : tiles + kHeads * kWave * 16;
+}
+
+template <typename T, int D, int kHeads, int kPass>
+constexpr int decode_pass_stages() {
+  constexpr int fit = kDecodeLdsBudget / decode_pass_stage_bytes<T, D, kHeads, kPass>();
+  return fit >= 4 ? 4 : (fit >= 2 ? fit : 2);
+}
+
+// The work item of a decode workgroup (blockIdx.x): from the plan in device
+// memory, from the kernel arguments, or located on the device from the
+// lengths; false past the call's items (uniform over the workgroup).
+struct DecodeWork {
+  int64_t b, split, first_item, nsplit, tps;
+  int seq_len;
+};
+
+__device__ __forceinline__ bool decode_work(const DecodeArgs& a, const DecodeItems& items, DecodeWork& w) {
+  if (a.dev_items != nullptr && a.dev_items->count > 0) {
+    const DecodeItems* __restrict__ d = a.dev_items;
+    if ((int)blockIdx.x >= d->count) return false;
+    const uint32_t it = d->item[blockIdx.x];
+    w.b = it >> 16;
+    w.split = it & 0xffffu;
+    w.seq_len = d->seq_len[w.b];
+    w.first_item = d->seq_first[w.b];
+    w.tps = d->tps;
+  } else if (items.count > 0) {
+    if ((int)blockIdx.x >= items.count) return false;
+    const uint32_t it = items.item[blockIdx.x];
+    w.b = it >> 16;
+    w.split = it & 0xffffu;
+    w.seq_len = items.seq_len[w.b];
+    w.first_item = items.seq_first[w.b];
+    w.tps = a.tiles_per_split;
+  } else {
+    int first_len;
+    w.tps = decode_call_tps(a, &first_len);
+    int64_t count;
+    const int64_t tps = w.tps;
+    locate_item((int64_t)blockIdx.x, a.batch, [&](int64_t s) { return decode_splits_of(a, s, tps, first_len); },
+                &w.b, &w.split, &w.first_item, &count);
+    if (w.b < 0) return false;
+    w.seq_len = w.b < kWave ? __shfl(first_len, (int)w.b) : a.seq_lens[w.b];
+  }
+  w.seq_len = __builtin_amdgcn_readfirstlane(w.seq_len);
+  w.nsplit = cdiv(cdiv((int64_t)w.seq_len, (int64_t)kTileKeys), w.tps);
+  return true;
+}
+
+template <typename T, int D, bool kUniform, int kHeads, int kPass>
+__global__ __launch_bounds__(kHeads* kWave) void decode_pass_kernel(DecodeArgs a, DecodeItems items) {
+  static_assert(Elt<T>::kIsBf16, "the reference rounding point matters for bf16 probabilities");
+  static_assert(kPass == kDecodeScores || kPass == kDecodePV, "a pass of the two-pass decode");
+  using F = Frag<T, D>;
+  using GT = GroupTile<T, D, kHeads>;
+  constexpr int kStages = decode_pass_stages<T, D, kHeads, kPass>();
+  constexpr int kStageBytes = decode_pass_stage_bytes<T, D, kHeads, kPass>();
+  constexpr int kTilesBytes = kPassStepTiles * GT::kBytes;
+  constexpr int kOwnOps = kPassStepTiles * GT::kOpsPerWave + (kPass == kDecodePV ? 1 : 0);
+  constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
+  constexpr int kStepKeys = kPassStepTiles * kTileKeys;
+  __shared__ __attribute__((aligned(16))) unsigned char ring[kStages][kStageBytes];
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int g = lane >> 4;
+  const int row = lane & 15;
+
+  DecodeWork w;
+  if (!decode_work(a, items, w)) return;
+  const int64_t b = w.b;
+  const int64_t nsplit = w.nsplit;
+  const int64_t item = w.first_item + w.split;
+  const int seq_len = w.seq_len;
+  const int tps = (int)w.tps;
+  const int h0 = (int)blockIdx.y * kHeads;
+  const int h = h0 + wave;
+  const int group = a.group;
+  const int32_t* table = a.tables + b * a.table_stride;
+  const int tlen = (int)a.table_stride;
+  const int key_begin = (int)w.split * tps * kTileKeys;
+  const int key_end = min(key_begin + tps * kTileKeys, seq_len);
+  const int last = key_end - 1;
+  const int ntiles = (key_end - key_begin + kTileKeys - 1) / kTileKeys;
+  const int last_key0 = key_begin + (ntiles - 1) * kTileKeys;  // first key of the split's last tile
+  const int nsteps = (ntiles + kPassStepTiles - 1) / kPassStepTiles;
+  const bool row_valid = row < group;
+  const int qh = h * group + row;
+
+  // this item's scores and the sequence's (max, sum) pairs lie inside the
+  // workspace (uniform); otherwise (lengths inconsistent with the host's
+  // bounds) no score is written and the P.V pass does nothing
+  const bool ws_ok = a.ws_s != nullptr && (item + 1) * tps * kTileKeys <= a.ws_s_keys && a.ws_ml != nullptr &&
+                     w.first_item + nsplit <= a.ws_items;
+  if constexpr (kPass == kDecodePV) {
+    if (!ws_ok) return;
+  }
+  // the head's score rows of this item: tile t, row n, key k at (t * group + n) * 16 + k
+  uint16_t* const hscores = ws_ok ? a.ws_s + ((item * a.geom.kv_heads + h) * tps) * group * kTileKeys : nullptr;
+
+  // P.V pass: the (max, sum) pairs of every split of the sequence, loaded in
+  // batches (lane group g takes splits g, g + 4, ...) before anything waits
+  // for them; they are combined once the first tiles are on their way
+  constexpr int kMlBatch = 8;
+  float2 ml_first[kMlBatch];
+  if constexpr (kPass == kDecodePV) {
+#pragma unroll
+    for (int j = 0; j < kMlBatch; ++j) {
+      const int64_t sp = 4 * j + g;
+      ml_first[j] = (row_valid && sp < nsplit)
+                        ? *reinterpret_cast<const float2*>(a.ws_ml + ((w.first_item + sp) * a.q_heads + qh) * 2)
+                        : make_float2(kNegInf, 0.f);
+    }
+  }
+
+  // scores pass: q (rows >= group are zero)
+  F qf;
+  if (kPass == kDecodeScores && row_valid) {
+    load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + b * a.q_sb + qh * a.q_sh);
+  } else {
+#pragma unroll
+    for (int i = 0; i < F::kVec; ++i) qf.v[i] = uint4{0u, 0u, 0u, 0u};
+  }
+
+  // Fused append (scores pass, the split that ends the sequence): lanes
+  // [0, kHeadChunks) of wave w carry the 16-byte K chunks of head h0 + w,
+  // the next kHeadChunks lanes its V chunks (as in paged_decode_kernel).
+  constexpr int kHeadChunks = D * Elt<T>::kBytes / 16;
+  const bool appender = kPass == kDecodeScores && a.k_new != nullptr && key_end == seq_len;
+  const bool carrier = appender && lane < 2 * kHeadChunks;
+  const bool carries_k = lane < kHeadChunks;
+  const int new_c = carries_k ? lane : lane - kHeadChunks;
+  v4u new_chunk = v4u{0u, 0u, 0u, 0u};
+  if (carrier) {
+    const T* src = reinterpret_cast<const T*>(carries_k ? a.k_new : a.v_new) + b * (carries_k ? a.kn_s : a.vn_s) +
+                   h * D + new_c * kEltPerChunk;
+    new_chunk = *reinterpret_cast<const v4u*>(src);
+  }
+  const bool rope = appender && a.rope_cos != nullptr;
+  constexpr int kQHalf = F::kVec / 2;
+  v4u q_cos[kQHalf], q_sin[kQHalf], k_cos = v4u{0u, 0u, 0u, 0u}, k_sin = v4u{0u, 0u, 0u, 0u};
+  if (kPass == kDecodeScores && a.rope_cos != nullptr && a.k_new != nullptr) {
+    int64_t pos = seq_len - 1;
+    pos = pos >= a.rope_rows ? a.rope_rows - 1 : pos;
+    const T* crow = reinterpret_cast<const T*>(a.rope_cos) + pos * (D / 2);
+    const T* srow = reinterpret_cast<const T*>(a.rope_sin) + pos * (D / 2);
+#pragma unroll
+    for (int j = 0; j < kQHalf; ++j) {
+      const int d0 = (64 * j + 16 * (lane >> 4)) / Elt<T>::kBytes;
+      q_cos[j] = *reinterpret_cast<const v4u*>(crow + d0);
+      q_sin[j] = *reinterpret_cast<const v4u*>(srow + d0);
+    }
+    if (carrier && carries_k) {
+      const int d0 = (new_c % (kHeadChunks / 2)) * kEltPerChunk;
+      k_cos = *reinterpret_cast<const v4u*>(crow + d0);
+      k_sin = *reinterpret_cast<const v4u*>(srow + d0);
+    }
+  }
+
+  TableCache tc;
+  if constexpr (kUniform) tc.load(table, tlen, key_begin >> a.geom.bs_shift);
+  asm volatile("" : "+v"(new_chunk));
+
+  const T* src_cache = reinterpret_cast<const T*>(kPass == kDecodeScores ? a.k_cache : a.v_cache) + h0 * D;
+  // P.V pass: the wave's score op per step reads the head's group x 16
+  // scores of the step's tiles (2 x group 16-byte chunks per tile; lanes
+  // past them repeat the step's last chunk)
+  auto issue = [&](int slot, int step) {
+    unsigned char* dst = &ring[slot][0];
+#pragma unroll
+    for (int u = 0; u < kPassStepTiles; ++u) {
+      // a tile past the split's end: the split's last tile again (its keys
+      // are masked; no lane reads a slot the sequence does not own)
+      const int key0 = min(key_begin + (step * kPassStepTiles + u) * kTileKeys, last_key0);
+      TileAddr<kUniform, false> ta;
+      ta.init(a.geom, table, tlen, tc, key0);
+      const int lim = last - key0;
+#pragma unroll
+      for (int i = 0; i < GT::kOpsPerWave; ++i) {
+        const int op = wave + i * kHeads;
+        const int r = op * GT::kRowsPerOp + lane / GT::kChunks;
+        const int chunk = (lane % GT::kChunks) ^ GT::swz(r);
+        const int64_t src = ta.at(a.geom, table, tlen, key0, min(r, lim)) + chunk * kEltPerChunk;
+        lds_dma16<kCacheStream>(src_cache + src, dst + u * GT::kBytes + op * kWave * 16);
+      }
+    }
+    if constexpr (kPass == kDecodePV) {
+      const int t0 = step * kPassStepTiles;
+      const int chunks = min(kPassStepTiles, ntiles - t0) * 2 * group;
+      const uint16_t* src = hscores + ((int64_t)t0 * group) * kTileKeys + min(lane, chunks - 1) * kEltPerChunk;
+      lds_dma16<kCacheDefault>(src, dst + kTilesBytes + wave * kWave * 16);
+    }
+  };
+
+  // Per-lane LDS offsets within a tile: the K slice vectors, the V^T reads.
+  uint32_t koff[F::kVec];
+#pragma unroll
+  for (int j = 0; j < F::kVec; ++j) koff[j] = GT::chunk_offset(row, (wave * D * Elt<T>::kBytes + 64 * j + 16 * g) >> 4);
+  uint32_t vtr[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) vtr[c] = GT::vt_offset(lane, wave, c);
+  // P.V pass: this lane's scores (keys 4g..4g+3 of query row `row`) of the
+  // step's first and second tile in its wave's score chunk
+  const uint32_t soff = kTilesBytes + wave * kWave * 16 + row * 2 * kTileKeys + 8 * g;
+
+  constexpr int kAhead = kStages - 1;
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) {
+    if (j < nsteps) issue(j, j);
+  }
+
+  // P.V pass: the row's (m, l) over all splits of the sequence; scores
+  // pass: RoPE of q and of the new K row
+  float row_m = 0.f, row_l = 1.f, row_r = 1.f;
+  if constexpr (kPass == kDecodePV) {
+    float m = kNegInf, l = 0.f;
+    auto combine = [&](float2 v) {
+      const float mn = score_max(m, v.x);
+      if (mn != kNegInf) l = l * exp_ref(m - mn) + v.y * exp_ref(v.x - mn);
+      m = mn;
+    };
+#pragma unroll
+    for (int j = 0; j < kMlBatch; ++j) combine(ml_first[j]);
+    for (int64_t s0 = 4 * kMlBatch; s0 < nsplit; s0 += 4 * kMlBatch) {
+      float2 v[kMlBatch];
+#pragma unroll
+      for (int j = 0; j < kMlBatch; ++j) {
+        const int64_t sp = s0 + 4 * j + g;
+        v[j] = (row_valid && sp < nsplit)
+                   ? *reinterpret_cast<const float2*>(a.ws_ml + ((w.first_item + sp) * a.q_heads + qh) * 2)
+                   : make_float2(kNegInf, 0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < kMlBatch; ++j) combine(v[j]);
+    }
+    row_m = max_over_groups(m);
+    row_l = sum_over_groups(row_m == kNegInf ? 0.f : l * exp_ref(m - row_m));
+    row_r = 1.f / row_l;
+  } else if (rope) {
+    if (row_valid) {
+#pragma unroll
+      for (int j = 0; j < kQHalf; ++j) {
+        v4u lo = __builtin_bit_cast(v4u, qf.v[j]), hi = __builtin_bit_cast(v4u, qf.v[j + kQHalf]);
+        rope_vec<T>(lo, hi, q_cos[j], q_sin[j]);
+        qf.v[j] = __builtin_bit_cast(uint4, lo);
+        qf.v[j + kQHalf] = __builtin_bit_cast(uint4, hi);
+      }
+    }
+    v4u other;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) other[k] = (uint32_t)__shfl_xor((int)new_chunk[k], kHeadChunks / 2);
+    if (carrier && carries_k) {
+      const bool first_half = new_c < kHeadChunks / 2;
+      v4u lo = first_half ? new_chunk : other, hi = first_half ? other : new_chunk;
+      rope_vec<T>(lo, hi, k_cos, k_sin);
+      new_chunk = first_half ? lo : hi;
+    }
+  } else if (kPass == kDecodeScores && row_valid && a.rope_cos != nullptr && a.k_new != nullptr) {
+    // (a split that does not end the sequence rotates q only)
+#pragma unroll
+    for (int j = 0; j < kQHalf; ++j) {
+      v4u lo = __builtin_bit_cast(v4u, qf.v[j]), hi = __builtin_bit_cast(v4u, qf.v[j + kQHalf]);
+      rope_vec<T>(lo, hi, q_cos[j], q_sin[j]);
+      qf.v[j] = __builtin_bit_cast(uint4, lo);
+      qf.v[j + kQHalf] = __builtin_bit_cast(uint4, hi);
+    }
+  }
+
+  // scores pass: the row's running maximum and this lane's share (keys
+  // 4g..4g+3 of every tile) of its sum of e^(s - m) in fp64
+  float run_m = kNegInf;
+  double run_l = 0.0;
+  // P.V pass: O^T accumulators of the lane's row
+  v4f o[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) o[c] = v4f{0.f, 0.f, 0.f, 0.f};
+  bool carry = false;
+  T* new_dst = nullptr;
+
+  for (int s0 = 0; s0 < nsteps; s0 += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) {
+      const int st = s0 + j;
+      if (st >= nsteps) break;  // uniform over the workgroup
+      // this wave's ops of step st have landed once at most those of the
+      // steps issued after it are outstanding; the barrier extends that to
+      // every wave, and every wave has finished step st-1, whose stage the
+      // next fetch reuses
+      wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1 - st));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + kAhead < nsteps) issue((j + kAhead) % kStages, st + kAhead);
+      __builtin_amdgcn_sched_barrier(0);
+      const unsigned char* stage = &ring[j][0];
+      const int key0 = key_begin + st * kStepKeys;
+      if constexpr (kPass == kDecodeScores) {
+        if (appender && st == nsteps - 1) {
+          // the new token's K row (rotated) over the stale copy the DMA
+          // read from its slot, and its cache slot for both K and V
+          const int pos = seq_len - 1;
+          int lb, off;
+          if (a.geom.bs_shift >= 0) {
+            lb = pos >> a.geom.bs_shift;
+            off = pos & (a.geom.block_size - 1);
+          } else {
+            lb = (int)((uint32_t)pos / (uint32_t)a.geom.block_size);
+            off = pos - lb * a.geom.block_size;
+          }
+          int phys;
+          if constexpr (kUniform) {
+            phys = tc.template lookup<false>(table, tlen, lb);
+          } else {
+            phys = table[lb];
+          }
+          if (carrier && lb < tlen && phys >= 0 && phys < a.geom.num_blocks) {
+            T* cache = reinterpret_cast<T*>(const_cast<void*>(carries_k ? a.k_cache : a.v_cache));
+            new_dst = cache + a.geom.layer_offset + ((int64_t)phys * a.geom.block_size + off) * a.geom.row_elems +
+                      h * D + new_c * kEltPerChunk;
+            carry = true;
+            if (carries_k) {
+              const int rel = pos - key0;  // in [0, 32): tile rel / 16, row rel % 16
+              const uint32_t patch = lds_off(stage) + (uint32_t)((rel / kTileKeys) * GT::kBytes) +
+                                     (uint32_t)GT::chunk_offset(rel % kTileKeys, wave * kHeadChunks + new_c);
+              asm volatile("ds_write_b128 %0, %1" : : "v"(patch), "v"(new_chunk) : "memory");
+            }
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // the step's K slices (both tiles), then S^T = K . Q^T per tile
+        const uint32_t base = lds_off(stage);
+        v4u kr[kPassStepTiles][F::kVec];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+          for (int jj = 0; jj < F::kVec; ++jj) {
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kr[u][jj]) : "v"(base + koff[jj]), "i"(u * GT::kBytes));
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          static_assert(F::kVec == 2 || F::kVec == 4, "head_dim 64 or 128");
+          if constexpr (F::kVec == 2) {
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kr[u][0]), "+v"(kr[u][1]));
+          } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kr[u][0]), "+v"(kr[u][1]), "+v"(kr[u][2]), "+v"(kr[u][3]));
+          }
+        }
+        v4f sc[kPassStepTiles];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int jj = 0; jj < F::kVec; ++jj) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u][jj]),
+                                                          __builtin_bit_cast(bf16x8_t, qf.v[jj]), acc, 0, 0, 0);
+          }
+          sc[u] = acc;
+        }
+        float tmax = kNegInf;
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + u * kTileKeys + 4 * g + i;
+            sc[u][i] = key <= last ? scaled_score<T>(sc[u][i], a.scale) : kNegInf;
+            tmax = score_max(tmax, sc[u][i]);
+          }
+          const int t = st * kPassStepTiles + u;
+          if (ws_ok && row_valid && t < ntiles) {
+            *reinterpret_cast<uint2*>(hscores + ((int64_t)t * group + row) * kTileKeys + 4 * g) =
+                uint2{pack_bf16x2(sc[u][0], sc[u][1]), pack_bf16x2(sc[u][2], sc[u][3])};
+          }
+        }
+        const float m_new = score_max(run_m, max_over_groups(tmax));
+        if (m_new != kNegInf) {
+          double add = 0.0;
+#pragma unroll
+          for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) add += (double)exp_ref(sc[u][i] - m_new);
+          }
+          run_l = run_l * (double)exp_ref(run_m - m_new) + add;
+        }
+        run_m = m_new;
+      } else {
+        // P = bf16(e^(s - m) / l) for the step's keys of the lane's row
+        // (rows >= group and keys past the split's end: 0), then
+        // O^T += V^T . P^T over both tiles in one 16x16x32 MFMA per 16 dims
+        const uint32_t base = lds_off(stage);
+        v2u sv[kPassStepTiles];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          // the second tile's rows follow the first tile's group rows
+          asm volatile("ds_read_b64 %0, %1" : "=v"(sv[u]) : "v"(base + soff + (uint32_t)(u * group * 2 * kTileKeys)));
+        }
+        v2u vt[kPassStepTiles][D / 16];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) {
+            asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(vt[u][c]) : "v"(base + vtr[c]), "i"(u * GT::kBytes));
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sv[0]), "+v"(sv[1]));
+        v4s pb[kPassStepTiles];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          float p[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x = bf16_bits_to_f32((sv[u][i / 2] >> (16 * (i % 2))) & 0xffffu);
+            const int key = key0 + u * kTileKeys + 4 * g + i;
+            p[i] = (row_valid && key <= last) ? div_ref(exp_ref(x - row_m), row_l, row_r) : 0.f;
+          }
+          pb[u] = pack_bf16x4(p[0], p[1], p[2], p[3]);
+        }
+        const bf16x8_t pp = join_bf16x4(pb[0], pb[1]);
+#pragma unroll
+        for (int c = 0; c < D / 16; c += 4) {
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(vt[0][c]), "+v"(vt[0][c + 1]), "+v"(vt[0][c + 2]), "+v"(vt[0][c + 3]));
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(vt[1][c]), "+v"(vt[1][c + 1]), "+v"(vt[1][c + 2]), "+v"(vt[1][c + 3]));
+        }
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const bf16x8_t vv = join_bf16x4(__builtin_bit_cast(v4s, vt[0][c]), __builtin_bit_cast(v4s, vt[1][c]));
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp, o[c], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // every fetch has been waited for (the last step's wait is vmcnt(0))
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  if constexpr (kPass == kDecodeScores) {
+    if (carry) *reinterpret_cast<v4u*>(new_dst) = new_chunk;
+    // the split's (max, sum of e^(s - max)) per query head; a + b == b + a,
+    // so every lane of the row forms the same sum
+    double tl = run_l + __shfl_xor(run_l, 16);
+    tl = tl + __shfl_xor(tl, 32);
+    if (ws_ok && row_valid && g == 0) {
+      *reinterpret_cast<float2*>(a.ws_ml + (item * a.q_heads + qh) * 2) = make_float2(run_m, (float)tl);
+    }
+  } else {
+    if (!row_valid) return;
+    if (nsplit == 1) {
+      T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * g;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) store4<T>(dst + 16 * c, o[c][0], o[c][1], o[c][2], o[c][3]);
+      return;
+    }
+    float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      *reinterpret_cast<float4*>(dst + 16 * c) = make_float4(o[c][0], o[c][1], o[c][2], o[c][3]);
+    }
   }
 }
 
@@ -2848,15 +3224,6 @@ constexpr int prefill_stages() {
   return fit >= want ? want : (fit >= 2 ? fit : 2);
 }
 
-// Two 4-element bf16 operands (sub-tile a's keys, then sub-tile b's) as one
-// 8-element 16x16x32 operand.  With it, K slot 8(l/16) + e of an MFMA is key
-// 4(l/16) + e of sub-tile a for e < 4 and key 4(l/16) + e - 4 of sub-tile b
-// otherwise, the same on the V^T and the P^T side.
-__device__ __forceinline__ bf16x8_t join_bf16x4(v4s a, v4s b) {
-  const u32x2_t lo = __builtin_bit_cast(u32x2_t, a);
-  const u32x2_t hi = __builtin_bit_cast(u32x2_t, b);
-  return __builtin_bit_cast(bf16x8_t, v4u{lo[0], lo[1], hi[0], hi[1]});
-}
 
 // Online softmax over one key step: s[nb][t] holds the scores of sub-tile t
 // for row block nb (-inf where masked); they are overwritten with the
@@ -3986,8 +4353,7 @@ template <typename T, int D, bool U, int H>
 int decode_resident() {
   static const int n = [] {
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_kernel<T, D, U, H, kDecodeFused>,
-                                                     H * kWave, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_kernel<T, D, U, H>, H * kWave, 0) !=
             hipSuccess ||
         blocks < 1) {
       (void)hipGetLastError();
@@ -4027,13 +4393,18 @@ int decode_resident_u(int heads) {
   }
 }
 
+// P: 0 for paged_decode_kernel, else a pass of decode_pass_kernel.
 template <typename T, int D, bool U, int H, int P>
 void launch_decode_h(const DecodeArgs& a, const DecodeItems& items, int64_t grid_items, hipStream_t stream) {
   const dim3 grid((unsigned)grid_items, (unsigned)(a.geom.kv_heads / H));
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H, P>), grid, dim3(H * kWave), 0, stream, a, items);
+  if constexpr (P == 0) {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a, items);
+  } else {
+    hipLaunchKernelGGL((decode_pass_kernel<T, D, U, H, P>), grid, dim3(H * kWave), 0, stream, a, items);
+  }
 }
 
-template <typename T, int D, bool U, int P = kDecodeFused>
+template <typename T, int D, bool U, int P = 0>
 void launch_decode_u(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& items, hipStream_t stream) {
   constexpr int kMax = decode_max_heads<T, D>();
   const int64_t n = items.count > 0 ? items.count : p.items;
