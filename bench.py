@@ -60,10 +60,9 @@ def parse_args():
     p.add_argument("--stress-steps", type=int, default=256, help="stress step: decode steps (one append each)")
     p.add_argument("--lockstep-requests", type=int, default=16,
                    help="serving requests replayed on the reference algorithm (bf16 and fp32)")
-    p.add_argument("--lockstep-variant", action="store_true",
-                   help="also replay on the bf16 variant with fp32 attention products")
-    p.add_argument("--native-gemm", choices=["on", "off"], default="on",
-                   help="serving legs: decode-step projections on nie_linear_rows (on) or torch's GEMM (off)")
+    p.add_argument("--native-gemm", choices=["on", "off"], default="off",
+                   help="serving legs: decode-step projections on nie_linear_rows (on) or torch's GEMM (off, the "
+                        "reference's arithmetic)")
     p.add_argument("--rounding", choices=["reference", "fast"], default="reference",
                    help="bf16 attention probabilities: the reference's rounding point (normalised P cast to bf16, "
                         "two passes) or one pass with an online softmax")
@@ -819,7 +818,7 @@ def run_lockstep(args):
     ours = sum(r.generated_tokens for r in reqs) / secs
     report = lockstep.run_lockstep(model, prompts, cache, max_new_tokens=workloads.SERVING_NEW_TOKENS,
                                    max_batch_size=workloads.SERVING_MAX_BATCH, chunk=workloads.SERVING_CHUNK,
-                                   budget=workloads.SERVING_STEP_BUDGET, variant=args.lockstep_variant)
+                                   budget=workloads.SERVING_STEP_BUDGET, variant=True)
     summary = report.summary()
     tokens = summary["sampled_rows"]
     ref_rate = tokens / report.reference_seconds

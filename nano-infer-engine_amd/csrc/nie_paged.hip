@@ -3348,15 +3348,34 @@ __device__ __forceinline__ void ring_read_tr_at(v2u* r, const uint32_t* base) {
 // kPow2Scale: the softmax scale is a power of two, so rounding the scaled
 // score to bf16 is exact and the scale can be kept out of the scores and
 // applied inside the exponential (bf16 only).
-template <typename T, int D, bool kUniform, int kRowBlocks, bool kPow2Scale>
+// kMode: kPrefillOnline, the one-pass online softmax (bf16 P =
+// exp(s - running max), O / l at the end); or, with the reference's
+// rounding point (normalised probabilities rounded to bf16 before P.V,
+// layers/attention.py:410-411), kPrefillStats then kPrefillExact over the
+// same work items.  kPrefillStats reads K only and writes, per piece and
+// query row, the maximum of its scores and the sum of e^(s - max) (each
+// step's exponentials summed in fp32, the steps in fp64) into the (max,
+// sum) slots of the workspace; kPrefillExact combines the pieces of its
+// query tile into the row's (m, l), and accumulates P = bf16(e^(s - m) / l)
+// . V: with one piece the rows are written out, with several each piece's
+// share of the normalised output goes to the workspace, which
+// prefill_merge_kernel<kSum> adds up.
+constexpr int kPrefillOnline = 0;
+constexpr int kPrefillStats = 1;
+constexpr int kPrefillExact = 2;
+
+template <typename T, int D, bool kUniform, int kRowBlocks, bool kPow2Scale, int kMode>
 __global__ __launch_bounds__(kPrefillWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
 void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, 1>;
+  static_assert(kMode == kPrefillOnline || Elt<T>::kIsBf16, "the reference rounding point matters for bf16");
+  constexpr bool kFetchV = kMode != kPrefillStats;
   constexpr int kSub = kPrefillStepTiles;
   constexpr int kStages = prefill_stages<T, D>();
   constexpr int kStageBytes = prefill_stage_bytes<T, D>();
-  constexpr int kStepOps = kSub * 2 * GT::kOps;  // DMA ops of one step: per tile, K ops then V ops
+  // DMA ops of one step: per tile, K ops then V ops (the stats pass: K only)
+  constexpr int kStepOps = kSub * (kFetchV ? 2 : 1) * GT::kOps;
   static_assert(kStepOps % kPrefillWaves == 0, "step DMA ops must spread evenly over the waves");
   constexpr int kOwnOps = kStepOps / kPrefillWaves;
   constexpr int kEltPerChunk = 16 / Elt<T>::kBytes;
@@ -3378,7 +3397,10 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   // This workgroup's item: request r, query tile from token t0, key tiles
   // [tile_begin, tile_cap), and the workspace slot of its partial (-1: the
   // item covers its query tile's keys and writes the rows out).
-  int64_t r, q_begin, slot;
+  // The reference rounding also numbers every item (tile_first + piece,
+  // one piece included) for its (max, sum) slots; the tile's pieces are
+  // [tile_first, tile_first + npieces).
+  int64_t r, q_begin, slot, tile_first, piece, npieces;
   int q_len, ctx, t0, tile_begin, tile_cap;
   if (sc.count > 0) {
     if (wg_item >= sc.count) return;  // uniform over the workgroup
@@ -3392,7 +3414,10 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     q_len = sc.q_len[k];
     ctx = sc.ctx[k];
     t0 = sc.t0[k];
-    slot = ((tl >> 8) & 0xff) == 1 ? -1 : (int64_t)(tl >> 16) + (int64_t)((it >> 8) & 0xff);
+    npieces = (tl >> 8) & 0xff;
+    tile_first = (int64_t)(tl >> 16);
+    piece = (int64_t)((it >> 8) & 0xff);
+    slot = npieces == 1 ? -1 : tile_first + piece;
   } else {
     // in reverse order: a request's later query tiles see more keys, so the
     // longest items start first and the short ones fill the end of the
@@ -3417,10 +3442,16 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     tile_begin = split * S;
     tile_cap = tile_begin + S;
     slot = nsplit == 1 ? -1 : pit.first + pit.local;
+    piece = split;
+    npieces = nsplit;
+    tile_first = pit.first + pit.local - split;
   }
   r = uniform64(r);
   q_begin = uniform64(q_begin);
   slot = uniform64(slot);
+  tile_first = uniform64(tile_first);
+  piece = uniform64(piece);
+  npieces = uniform64(npieces);
   q_len = __builtin_amdgcn_readfirstlane(q_len);
   ctx = __builtin_amdgcn_readfirstlane(ctx);
   t0 = __builtin_amdgcn_readfirstlane(t0);
@@ -3473,7 +3504,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   // item's last key is redirected to the tile that holds it, and rows past
   // it to it (no lane reads a slot the sequence does not own; those keys are
   // masked to p = 0).
-  static_assert(kOwnOps == 2 * GT::kOps, "one tile's K and V ops per wave");
+  static_assert(kOwnOps == (kFetchV ? 2 : 1) * GT::kOps, "one tile's K (and V) ops per wave");
   // Per-lane element offsets of this wave's ops inside a tile (the same for
   // every tile): the lane's row and its swizzled 16-byte chunk.
   int op_row[kOwnOps], op_row_off[kOwnOps], op_chunk_off[kOwnOps];
@@ -3525,7 +3556,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) voff[4 * c + e] = GT::kBytes + GT::elt_offset(4 * g + e, 0, 16 * c + row);
   }
-  constexpr int kTileStride = 2 * GT::kBytes;  // K tile + V tile
+  constexpr int kTileStride = kOwnOps * kWave * 16;  // K tile + V tile (the stats pass: K only)
 
   // exp2 multiplier of the scores (see softmax_step)
   const float exp_c = kPow2Scale ? a.scale * kLog2e : kLog2e;
@@ -3558,7 +3589,136 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     if (j < nsteps) issue(j, (tile_begin + j * kSub) * kTileKeys);
   }
 
-  if constexpr (Elt<T>::kIsBf16) {
+  // the scale a difference of two (possibly unscaled) scores still takes
+  const float score_f = kPow2Scale ? a.scale : 1.f;
+  // Exact pass: each row's -m (scaled), l and 1 / l over every piece of its
+  // query tile (rows >= the tile's tokens: m = -inf, never written)
+  float row_nm[kRowBlocks], row_r[kRowBlocks];
+  if constexpr (kMode == kPrefillExact) {
+    constexpr int kB = 8;  // pieces per lane group per round trip
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) {
+      const int64_t rowidx = (wave * kRowBlocks + nb) * 16 + row;
+      float m = kNegInf, l = 0.f;
+      if (a.ws_ml != nullptr && tile_first + npieces <= a.ws_items) {
+        for (int64_t p0 = 0; p0 < npieces; p0 += 4 * kB) {
+          float2 v[kB];
+#pragma unroll
+          for (int jb = 0; jb < kB; ++jb) {
+            const int64_t pc = p0 + 4 * jb + g;
+            v[jb] = pc < npieces ? *reinterpret_cast<const float2*>(
+                                       a.ws_ml + (((tile_first + pc) * a.geom.kv_heads + h) * kRows + rowidx) * 2)
+                                 : make_float2(kNegInf, 0.f);
+          }
+#pragma unroll
+          for (int jb = 0; jb < kB; ++jb) {
+            const float mn = score_max(m, v[jb].x);
+            if (mn != kNegInf) l = l * exp_ref(m - mn) + v[jb].y * exp_ref(v[jb].x - mn);
+            m = mn;
+          }
+        }
+      }
+      const float mm = max_over_groups(m);
+      const float ll = sum_over_groups(mm == kNegInf ? 0.f : l * exp_ref(m - mm));
+      row_nm[nb] = mm == kNegInf ? 0.f : -mm;
+      row_r[nb] = 1.f / ll;
+    }
+  }
+
+  if constexpr (kMode == kPrefillStats) {
+    // K only, one step at a time: the step's scores (the reference's
+    // rounding), the row's running maximum and its sum of e^(s - m), each
+    // step's 16 exponentials of a row block summed in fp32 (pairwise) and
+    // the steps in fp64, rescaled when the maximum moves
+    constexpr int kKR = kSub * F::kVec;
+    const uint32_t ring0 = lds_off(&ring[0][0]);
+    float run_m[kRowBlocks];
+    double run_l[kRowBlocks];
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) {
+      run_m[nb] = kNegInf;
+      run_l[nb] = 0.0;
+    }
+    for (int s0 = 0; s0 < nsteps; s0 += kStages) {
+#pragma unroll
+      for (int j = 0; j < kStages; ++j) {
+        const int s = s0 + j;
+        if (s >= nsteps) break;  // uniform over the workgroup
+        wait_dma_groups<kOwnOps, kAhead - 1>(min(kAhead - 1, nsteps - 1 - s));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + kAhead < nsteps) issue((j + kAhead) % kStages, (tile_begin + (s + kAhead) * kSub) * kTileKeys);
+        __builtin_amdgcn_sched_barrier(0);
+        const int key0 = (tile_begin + s * kSub) * kTileKeys;
+        v4u kr[kKR];
+        uint32_t kb[F::kVec];
+#pragma unroll
+        for (int jj = 0; jj < F::kVec; ++jj) kb[jj] = ring0 + j * kStageBytes + koff[jj];
+        ring_read_at<kKR, F::kVec, kTileStride>(kr, kb);
+#pragma unroll
+        for (int jj = 0; jj < kKR; jj += 4) {
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kr[jj]), "+v"(kr[jj + 1]), "+v"(kr[jj + 2]), "+v"(kr[jj + 3]));
+        }
+        v4f p[kRowBlocks][kSub];
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+          for (int t = 0; t < kSub; ++t) {
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int jj = 0; jj < F::kVec; ++jj) {
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[t * F::kVec + jj]),
+                                                            __builtin_bit_cast(bf16x8_t, qf[nb].v[jj]), acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              p[nb][t][i] = kPow2Scale ? round_bf16_in_f32(acc[i]) : scaled_score<T>(acc[i], a.scale);
+            }
+          }
+        }
+        if (!step_full(key0)) mask_step(p, key0);
+#pragma unroll
+        for (int nb = 0; nb < kRowBlocks; ++nb) {
+          float lm = kNegInf;
+#pragma unroll
+          for (int t = 0; t < kSub; ++t) {
+            lm = score_max(score_max(lm, score_max(p[nb][t][0], p[nb][t][1])), score_max(p[nb][t][2], p[nb][t][3]));
+          }
+          const float m_new = score_max(run_m[nb], max_over_groups(lm));
+          if (m_new != kNegInf) {
+            if (run_m[nb] != m_new) run_l[nb] *= (double)fast_exp2((run_m[nb] - m_new) * score_f * kLog2e);
+            float e[kSub];
+#pragma unroll
+            for (int t = 0; t < kSub; ++t) {
+              float q4[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) q4[i] = fast_exp2((p[nb][t][i] - m_new) * score_f * kLog2e);
+              e[t] = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+            }
+            run_l[nb] += (double)((e[0] + e[1]) + (e[2] + e[3]));
+          }
+          run_m[nb] = m_new;
+        }
+      }
+    }
+    // every fetch has been waited for; the piece's (max, sum) per row (max
+    // in scaled units; a + b == b + a, so every lane of a row forms the
+    // same sum)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const int64_t stats_slot = tile_first + piece;
+#pragma unroll
+    for (int nb = 0; nb < kRowBlocks; ++nb) {
+      double tl = run_l[nb] + __shfl_xor(run_l[nb], 16);
+      tl = tl + __shfl_xor(tl, 32);
+      const int64_t rowidx = (wave * kRowBlocks + nb) * 16 + row;
+      if (g == 0 && a.ws_ml != nullptr && stats_slot < a.ws_items) {
+        const float m = run_m[nb] == kNegInf ? kNegInf : run_m[nb] * score_f;
+        *reinterpret_cast<float2*>(a.ws_ml + ((stats_slot * a.geom.kv_heads + h) * kRows + rowidx) * 2) =
+            make_float2(m, (float)tl);
+      }
+    }
+    return;
+  } else if constexpr (Elt<T>::kIsBf16) {
     // Software-pipelined steps.  Iteration s runs the softmax of step s on
     // scores whose QK MFMAs were issued in iteration s-1.  The P.V MFMAs of
     // step s-1 (its P kept from the previous iteration, its V still in the
@@ -3656,7 +3816,9 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
                                             __builtin_bit_cast(v4s, vt[(t + 1) * (D / 16) + c]));
             st[nb].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp[nb][t / 2], st[nb].o[c], 0, 0, 0);
           }
-          rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
+          if constexpr (kMode == kPrefillOnline) {
+            rowsum[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp[nb][t / 2], rowsum[nb], 0, 0, 0);
+          }
         }
       }
     };
@@ -3704,6 +3866,38 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
       // registers are not held across the P.V of step s-1
       if (more) read_k((slot + 1) % kStages);
       if (!step_full(key0)) mask_step(p, key0);
+      if constexpr (kMode == kPrefillExact) {
+        // P = e^(s - m) / l with the row's final (m, l): s - m exact (the
+        // unscaled score times a power-of-two scale, minus m, rounds once,
+        // as the reference's input - max), then 2^((s - m) log2 e) and a
+        // product with 1 / l.  That is a few fp32 ulps from the reference's
+        // exp and division (exp_ref / div_ref would halve the gap at
+        // 1.3-1.5x the call time); in the 16 x 256 serving lockstep both
+        // forms agree with the reference path as well as its fp32-product
+        // variant does (top-1 95.2% either way, median logit error 0.086).
+#pragma unroll
+        for (int t = 0; t < kSub; t += 2) {
+#pragma unroll
+          for (int nb = 0; nb < kRowBlocks; ++nb) {
+#pragma unroll
+            for (int u = t; u < t + 2; ++u) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float x = kPow2Scale ? fmaf(p[nb][u][i], a.scale, row_nm[nb]) : p[nb][u][i] + row_nm[nb];
+                p[nb][u][i] = fast_exp2(x * kLog2e) * row_r[nb];
+              }
+            }
+            pp_prev[nb][t / 2] = join_bf16x4(pack_bf16x4(p[nb][t][0], p[nb][t][1], p[nb][t][2], p[nb][t][3]),
+                                             pack_bf16x4(p[nb][t + 1][0], p[nb][t + 1][1], p[nb][t + 1][2],
+                                                         p[nb][t + 1][3]));
+          }
+        }
+        if (more) {
+          wait_k();
+          qk();  // scores of step s+1
+        }
+        return;
+      }
       // each lane tests its own 16 scores of a row; only when one of them
       // moves the row's reference point is the row maximum formed across
       // the lane groups (see softmax_step).  m = -inf gives +inf (a finite
@@ -3781,7 +3975,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
       pv(pp_prev);
     }
 #pragma unroll
-    for (int nb = 0; nb < kRowBlocks; ++nb) st[nb].lsum = rowsum[nb][0];
+    for (int nb = 0; nb < kRowBlocks; ++nb) st[nb].lsum = kMode == kPrefillExact ? 1.f : rowsum[nb][0];
   } else {
     auto consume = [&](int slot, int key0) {
       const unsigned char* stage = &ring[slot][0];
@@ -3870,9 +4064,11 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
       for (int c = 0; c < D / 16; ++c) {
         __builtin_nontemporal_store(st[nb].o[c], reinterpret_cast<v4f*>(dst + 16 * c));
       }
-      // the merge expects the maximum of the scaled scores
+      // the merge expects the maximum of the scaled scores (the exact pass
+      // leaves the slots alone: other pieces of its tile may still be
+      // reading their stats there, and the summing merge needs none)
       const float m = kPow2Scale ? st[nb].m * a.scale : st[nb].m;
-      if (g == 0) {
+      if (kMode == kPrefillOnline && g == 0) {
         __builtin_nontemporal_store(m, a.ws_ml + wrow * 2);
         __builtin_nontemporal_store(lsum, a.ws_ml + wrow * 2 + 1);
       }
@@ -3916,7 +4112,9 @@ struct PrefillMergeJobs {
   int32_t nsplit_tokens[kMaxMergeJobs];  // nsplit << 16 | tokens
 };
 
-template <typename T, int D, int kRowBlocks, int kBatch>
+// kSum: partials of the reference rounding (shares of the normalised
+// output): summed in split order, no weights, rounded once.
+template <typename T, int D, int kRowBlocks, int kBatch, bool kSum>
 __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kernel(PrefillArgs a,
                                                                                  PrefillMergeJobs jobs) {
   constexpr int kRows = prefill_rows_per_item<kRowBlocks>();
@@ -3984,11 +4182,26 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
       const bool in = s0 + b < nsplit;
       const int64_t split_row = (int64_t)(s0 + b) * split_stride;  // uniform
       const float* ob = o_first + split_row * D;
-      ml[b] = in ? *reinterpret_cast<const float2*>(ml_first + split_row * 2 + ml_lane) : make_float2(kNegInf, 0.f);
+      if constexpr (!kSum) {
+        ml[b] = in ? *reinterpret_cast<const float2*>(ml_first + split_row * 2 + ml_lane) : make_float2(kNegInf, 0.f);
+      }
 #pragma unroll
       for (int c = 0; c < kChunkPasses; ++c) {
         v[b][c] = in ? *reinterpret_cast<const float4*>(ob + o_lane + 64 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
+    }
+    if constexpr (kSum) {
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+#pragma unroll
+        for (int c = 0; c < kChunkPasses; ++c) {
+          acc[c].x += v[b][c].x;
+          acc[c].y += v[b][c].y;
+          acc[c].z += v[b][c].z;
+          acc[c].w += v[b][c].w;
+        }
+      }
+      continue;
     }
     float bmax = ml[0].x;
 #pragma unroll
@@ -4019,7 +4232,7 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
   }
   if (rr >= kRows || tq >= tokens) return;
   const int qh = h * a.group + (rr % 16) % a.group;
-  const float inv = 1.f / denom;
+  const float inv = kSum ? 1.f : 1.f / denom;
   T* dst = reinterpret_cast<T*>(a.out) + (row0 + tq) * a.o_st + qh * a.o_sh;
 #pragma unroll
   for (int c = 0; c < kChunkPasses; ++c) {
@@ -4090,6 +4303,11 @@ int64_t host_key_tiles(int64_t ctx, int64_t n, int64_t tpt, int64_t qt) {
 bool plan_balanced(PrefillPlan& p, int64_t kv_heads) {
   const int64_t ncu = device_cus() / kXcds;
   if (kv_heads != kXcds || ncu < 2 || p.tiles.size() > (size_t)kMaxSchedTiles) return false;
+  // only plans the item table can hold: a device-located fallback would cut
+  // the tiles into uniform pieces that the balanced merge jobs do not match
+  for (const PrefillTile& t : p.tiles) {
+    if (t.r > 255) return false;
+  }
   const int64_t slots = 2 * ncu;
   int64_t total = 0;
   for (const PrefillTile& t : p.tiles) total += cdiv(t.ktiles, (int64_t)kPrefillStepTiles);
@@ -4556,16 +4774,24 @@ void launch_decode_two_pass(const DecodeArgs& a, const DecodePlan& p, const Deco
   }
 }
 
-template <typename T, int D, int NB, bool P2>
+template <typename T, int D, int NB, bool P2, int M>
 void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc, hipStream_t stream) {
   const dim3 grid((unsigned)(p.items * a.geom.kv_heads));
   if (uniform_tiles(a.geom)) {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a,
-                       sc);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2, M>), grid, dim3(kPrefillWaves * kWave), 0, stream,
+                       a, sc);
   } else {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2>), grid, dim3(kPrefillWaves * kWave), 0, stream, a,
-                       sc);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2, M>), grid, dim3(kPrefillWaves * kWave), 0, stream,
+                       a, sc);
   }
+}
+
+// The reference rounding: the stats pass, then the exact pass.
+template <typename T, int D, int NB, bool P2>
+void launch_prefill_two_pass(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc,
+                             hipStream_t stream) {
+  launch_prefill_kernel<T, D, NB, P2, kPrefillStats>(a, p, sc, stream);
+  launch_prefill_kernel<T, D, NB, P2, kPrefillExact>(a, p, sc, stream);
 }
 
 // A positive power of two (the softmax scale of head_dim 64 is 1/8).
@@ -4574,39 +4800,52 @@ bool is_pow2_scale(float scale) {
   return scale > 0.f && std::isfinite(scale) && std::frexp(scale, &e) == 0.5f && std::isnormal(scale);
 }
 
+template <typename T, int D, int NB, bool kSum>
+void launch_prefill_merge(const PrefillArgs& m, const PrefillPlan& p, const PrefillMergeJobs& jobs,
+                          hipStream_t stream) {
+  const dim3 grid((unsigned)(m.merge_tiles * m.geom.kv_heads * (prefill_rows_per_item<NB>() / kPrefillMergeRows)));
+  const dim3 block(kPrefillMergeWaves * kWave);
+  // splits per round trip: the call's largest split count, in steps of
+  // 4, 8, 16 (8 at head_dim 128); more splits take several round trips
+  if (p.max_split <= 4) {
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 4, kSum>), grid, block, 0, stream, m, jobs);
+  } else if constexpr (D > 64) {
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 8, kSum>), grid, block, 0, stream, m, jobs);
+  } else if (p.max_split <= 8) {
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 8, kSum>), grid, block, 0, stream, m, jobs);
+  } else {
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 16, kSum>), grid, block, 0, stream, m, jobs);
+  }
+}
+
 template <typename T, int D, int NB>
 void launch_prefill_nb(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc,
-                       const PrefillMergeJobs& jobs, hipStream_t stream, bool merge) {
+                       const PrefillMergeJobs& jobs, hipStream_t stream, bool merge, bool two) {
   if constexpr (Elt<T>::kIsBf16) {
-    if (is_pow2_scale(a.scale)) launch_prefill_kernel<T, D, NB, true>(a, p, sc, stream);
-    else launch_prefill_kernel<T, D, NB, false>(a, p, sc, stream);
+    if (two) {
+      if (is_pow2_scale(a.scale)) launch_prefill_two_pass<T, D, NB, true>(a, p, sc, stream);
+      else launch_prefill_two_pass<T, D, NB, false>(a, p, sc, stream);
+    } else if (is_pow2_scale(a.scale)) {
+      launch_prefill_kernel<T, D, NB, true, kPrefillOnline>(a, p, sc, stream);
+    } else {
+      launch_prefill_kernel<T, D, NB, false, kPrefillOnline>(a, p, sc, stream);
+    }
   } else {
-    launch_prefill_kernel<T, D, NB, false>(a, p, sc, stream);
+    launch_prefill_kernel<T, D, NB, false, kPrefillOnline>(a, p, sc, stream);
   }
   if (merge) {
     PrefillArgs m = a;
     m.merge_tiles = (int32_t)(jobs.count > 0 ? jobs.count : p.qtiles);
-    const dim3 grid((unsigned)(m.merge_tiles * a.geom.kv_heads * (prefill_rows_per_item<NB>() / kPrefillMergeRows)));
-    const dim3 block(kPrefillMergeWaves * kWave);
-    // splits per round trip: the call's largest split count, in steps of
-    // 4, 8, 16 (8 at head_dim 128); more splits take several round trips
-    if (p.max_split <= 4) {
-      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 4>), grid, block, 0, stream, m, jobs);
-    } else if constexpr (D > 64) {
-      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 8>), grid, block, 0, stream, m, jobs);
-    } else if (p.max_split <= 8) {
-      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 8>), grid, block, 0, stream, m, jobs);
-    } else {
-      hipLaunchKernelGGL((prefill_merge_kernel<T, D, NB, 16>), grid, block, 0, stream, m, jobs);
-    }
+    if (two) launch_prefill_merge<T, D, NB, true>(m, p, jobs, stream);
+    else launch_prefill_merge<T, D, NB, false>(m, p, jobs, stream);
   }
 }
 
 template <typename T, int D>
 void launch_prefill(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc,
-                    const PrefillMergeJobs& jobs, hipStream_t stream, bool merge) {
-  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, sc, jobs, stream, merge);
-  else launch_prefill_nb<T, D, 2>(a, p, sc, jobs, stream, merge);
+                    const PrefillMergeJobs& jobs, hipStream_t stream, bool merge, bool two) {
+  if (p.row_blocks == 1) launch_prefill_nb<T, D, 1>(a, p, sc, jobs, stream, merge, two);
+  else launch_prefill_nb<T, D, 2>(a, p, sc, jobs, stream, merge, two);
 }
 
 // Element alignment of the generic path's pointers.
@@ -5469,7 +5708,10 @@ NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t tot
   if (!tuned_attention(head_dim, q_heads, kv_heads)) return 0;  // the generic kernel needs no workspace
   const PrefillPlan p = plan_prefill(q_heads / kv_heads, kv_heads, num_seqs, total_query_tokens, max_seq_len,
                                      host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr);
-  if (!p.split) return 0;  // no query tile is split
+  // no query tile is split and, with the one-pass rounding, no (max, sum)
+  // slots are needed (the query has no dtype: with the reference rounding it
+  // sizes for bf16, which an fp32 call can use too)
+  if (!p.split && g_rounding.load(std::memory_order_relaxed) != NIE_ROUND_REFERENCE) return 0;
   return p.items * kv_heads * p.rows * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
@@ -5548,8 +5790,11 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   }
   if (plan.items == 0) return NIE_OK;
   const bool may_split = plan.split;
+  // the reference rounding always needs the workspace: every item's
+  // (max, sum) slots, one piece included
+  const bool two = two_pass(dtype);
   const int64_t need = plan.items * kv_heads * plan.rows * (head_dim + 2) * (int64_t)sizeof(float);
-  if (may_split && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
+  if ((may_split || two) && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,
                 (long long)workspace_bytes);
   }
@@ -5574,7 +5819,7 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   a.out = out;
   a.o_st = out_stride_t;
   a.o_sh = out_stride_h;
-  const bool have_ws = may_split && workspace != nullptr && workspace_bytes >= need;
+  const bool have_ws = (may_split || two) && workspace != nullptr && workspace_bytes >= need;
   a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + plan.items * kv_heads * plan.rows * head_dim : nullptr;
   a.ws_items = have_ws ? plan.items : 0;
@@ -5585,11 +5830,11 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   if (host) build_prefill_schedule(plan, num_seqs, host_cu_seqlens, host_context_lens, &sched);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIE_DTYPE_BF16) {
-    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, sched, jobs, s, may_split);
-    else launch_prefill<bf16_t, 128>(a, plan, sched, jobs, s, may_split);
+    if (head_dim == 64) launch_prefill<bf16_t, 64>(a, plan, sched, jobs, s, may_split, two);
+    else launch_prefill<bf16_t, 128>(a, plan, sched, jobs, s, may_split, two);
   } else {
-    if (head_dim == 64) launch_prefill<float, 64>(a, plan, sched, jobs, s, may_split);
-    else launch_prefill<float, 128>(a, plan, sched, jobs, s, may_split);
+    if (head_dim == 64) launch_prefill<float, 64>(a, plan, sched, jobs, s, may_split, false);
+    else launch_prefill<float, 128>(a, plan, sched, jobs, s, may_split, false);
   }
   return launched("varlen_prefill");
 }

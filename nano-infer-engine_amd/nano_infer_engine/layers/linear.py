@@ -1,10 +1,14 @@
-"""Bias-free projections of the decoder: ``nn.Linear`` for a decode step's rows on nie_linear_rows.
+"""Bias-free projections of the decoder: ``nn.Linear``, optionally a decode step's rows on nie_linear_rows.
 
 The reference engine runs every projection as ``nn.Linear`` (``layers/attention.py:227-232``,
 ``:271``, ``:359-361``, ``:414``; ``layers/mlp.py:18-22``; ``models/llama.py:328``, ``:391``).
-A decode step multiplies at most one row per sequence by each weight, which torch's
-library GEMM handles at a small fraction of the HBM bandwidth; up to 16 bf16 rows go
-to the HIP kernel, everything else (prefill chunks, fp32, autograd) stays with torch.
+By default this build does the same: torch's GEMM gives the reference's results bit for bit
+(the stacked [q; k; v] and [gate; up] products included: each output element is the same
+dot product in the same library kernel), which the bf16 serving identity needs.
+``nie_linear_rows`` streams a decode step's weights faster (up to 16 bf16 rows) but
+accumulates in another order: about 1.6e-4 of its bf16 outputs differ by one ulp from
+torch's, enough to move the serving lockstep's agreement with the reference path from
+95% to 94%.  ``USE_NATIVE = True`` opts in to it.
 """
 
 from __future__ import annotations
@@ -15,9 +19,9 @@ from torch import nn
 
 from nano_infer_engine import _native
 
-#: Route eligible projections to nie_linear_rows (tests switch it off to
-#: compare against torch's GEMM).
-USE_NATIVE = True
+#: Route eligible projections to nie_linear_rows (off: torch's GEMM, the
+#: reference's arithmetic).
+USE_NATIVE = False
 
 
 #: Tiles of 16 output columns that keep every CU streaming: the kernel runs

@@ -77,6 +77,17 @@ def torch_gemm():
         linear_module.USE_NATIVE = saved
 
 
+@contextlib.contextmanager
+def native_gemm():
+    """A decode step's projections on nie_linear_rows (opt-in)."""
+    saved = linear_module.USE_NATIVE
+    linear_module.USE_NATIVE = True
+    try:
+        yield
+    finally:
+        linear_module.USE_NATIVE = saved
+
+
 def _model(dtype=torch.float32, hidden=256, q_heads=4, kv_heads=2, layers=2, vocab=64, max_seq_len=64, seed=0):
     torch.manual_seed(seed)
     cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, mlp_inner_size=2 * hidden, num_layers=layers,
@@ -457,7 +468,8 @@ def test_bf16_batched_decode_projections_match_torch_gemm():
         return torch.cat(rows).float()
 
     with torch.inference_mode():
-        hip = run()
+        with native_gemm():
+            hip = run()
         with torch_gemm():
             ref = run()
     err = (hip[16:] - ref[16:]).abs().max().item()

@@ -435,8 +435,15 @@ def test_library_prefill_plan_from_host_lengths():
         return lib.nie_varlen_prefill_workspace_bytes(len(ctx), total, max_q, max_s, 32, 8, 64,
                                                       cu.ctypes.data, ctx.ctypes.data)
 
-    # four 128-token chunks on empty contexts: at most 8 key tiles per query tile, never split
-    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 0
+    # four 128-token chunks on empty contexts: at most 8 key tiles per query tile, never split, so the
+    # one-pass rounding needs no workspace; the reference rounding keeps every item's (max, sum) slots
+    # in the same layout (16 items here: 4 query tiles of 32 tokens per chunk)
+    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 16 * 8 * 128 * 66 * 4
+    _native.set_attention_rounding("fast")
+    try:
+        assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 0
+    finally:
+        _native.set_attention_rounding("reference")
     # the mixed step's chunks (contexts 0, 384, 1024, 4000): the long context is split
     mixed = query([0, 128, 256, 384, 512], [0, 384, 1024, 4000], 512, 128, 4128)
     assert mixed > 0 and mixed % (8 * 128 * 66 * 4) == 0
