@@ -2130,8 +2130,10 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
 // each a launch of decode_pass_kernel over the same work items:
 //   kDecodeScores reads K, writes every key's score bf16(bf16(q.k) * scale)
 //     (the reference's softmax input) to the workspace, and each split's
-//     (max, sum of e^(s - max)) (the sum in fp64 from exponentials accurate
-//     to about an ulp, so the only rounding left is the exponentials');
+//     (max, sum of e^(s - max)) (v_exp_f32 exponentials, a step's summed in
+//     fp32 and the steps in fp64: the sum's relative error stays near
+//     2^-24, which moves the bf16 rounding of P = e / l for about one
+//     probability in 10^4-10^5);
 //   kDecodePV reads V and the scores, combines its row's (m, l) over all the
 //     sequence's splits, and accumulates bf16(e^(s - m) / l) . V in fp32:
 //     its share of the normalised output, which decode_merge_kernel<kSum>
@@ -2376,7 +2378,7 @@ __global__ __launch_bounds__(kHeads* kWave) void decode_pass_kernel(DecodeArgs a
     float m = kNegInf, l = 0.f;
     auto combine = [&](float2 v) {
       const float mn = score_max(m, v.x);
-      if (mn != kNegInf) l = l * exp_ref(m - mn) + v.y * exp_ref(v.x - mn);
+      if (mn != kNegInf) l = fmaf(l, exp_ref(m - mn), v.y * exp_ref(v.x - mn));  // one explicit fma: with two products the compiler may fuse either
       m = mn;
     };
 #pragma unroll
@@ -2427,7 +2429,7 @@ __global__ __launch_bounds__(kHeads* kWave) void decode_pass_kernel(DecodeArgs a
   }
 
   // scores pass: the row's running maximum and this lane's share (keys
-  // 4g..4g+3 of every tile) of its sum of e^(s - m) in fp64
+  // 4g..4g+3 of every tile) of its sum of e^(s - m)
   float run_m = kNegInf;
   double run_l = 0.0;
   // P.V pass: O^T accumulators of the lane's row
@@ -2534,13 +2536,19 @@ __global__ __launch_bounds__(kHeads* kWave) void decode_pass_kernel(DecodeArgs a
         }
         const float m_new = score_max(run_m, max_over_groups(tmax));
         if (m_new != kNegInf) {
-          double add = 0.0;
+          // the step's eight exponentials (v_exp_f32) summed in fp32,
+          // pairwise, the steps in fp64, rescaled when the maximum moves
+          if (run_m != m_new) run_l *= (double)fast_exp2((run_m - m_new) * kLog2e);
+          const float nref = -m_new * kLog2e;
+          float e[kPassStepTiles];
 #pragma unroll
           for (int u = 0; u < kPassStepTiles; ++u) {
+            float q4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) add += (double)exp_ref(sc[u][i] - m_new);
+            for (int i = 0; i < 4; ++i) q4[i] = fast_exp2(fmaf(sc[u][i], kLog2e, nref));
+            e[u] = (q4[0] + q4[1]) + (q4[2] + q4[3]);
           }
-          run_l = run_l * (double)exp_ref(run_m - m_new) + add;
+          run_l += (double)(e[0] + e[1]);
         }
         run_m = m_new;
       } else {
@@ -3613,7 +3621,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 #pragma unroll
           for (int jb = 0; jb < kB; ++jb) {
             const float mn = score_max(m, v[jb].x);
-            if (mn != kNegInf) l = l * exp_ref(m - mn) + v[jb].y * exp_ref(v[jb].x - mn);
+            if (mn != kNegInf) l = fmaf(l, exp_ref(m - mn), v[jb].y * exp_ref(v[jb].x - mn));  // one explicit fma: with two products the compiler may fuse either
             m = mn;
           }
         }
