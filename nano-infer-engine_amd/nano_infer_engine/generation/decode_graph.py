@@ -55,7 +55,7 @@ class _CapturedStep:
     plan_at: int  # byte offset of the decode plan in ``meta``
     width: int
     copied: torch.cuda.Event  # recorded after the staging copies of the last step
-    logits: torch.Tensor  # (B, vocab) output of the last replay
+    logits: torch.Tensor  # (B, vocab) output of the last replay (its own buffer, outside the graph pool)
     next_ids: torch.Tensor  # (B,) int64 argmax of ``logits``
     mirror: TableMirror  # the staged tables, updated in place from step to step
 
@@ -136,12 +136,19 @@ class DecodeGraphRunner:
             # eager warm-up on the capture stream: builds the launches (which
             # remember this stream), their workspaces and the GEMM plans
             logits = model.run_tokens(ids, cache, batch)
-            _native.argmax_rows(logits, out=next_ids)
+            # the step's logits are copied into a buffer of its own, outside
+            # the shared graph pool, so replaying another capture (whose
+            # activations may reuse this capture's pool blocks) leaves them
+            # intact until this capture replays again
+            out_logits = torch.empty_like(logits)
+            out_logits.copy_(logits)
+            _native.argmax_rows(out_logits, out=next_ids)
             stream.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream, pool=self._pool):
                 logits = model.run_tokens(ids, cache, batch)
-                _native.argmax_rows(logits, out=next_ids)
+                out_logits.copy_(logits)
+                _native.argmax_rows(out_logits, out=next_ids)
         torch.cuda.current_stream(self.device).wait_stream(stream)
         self.captures += 1
         meta_host = torch.empty(meta.shape, dtype=torch.uint8, pin_memory=True)
@@ -158,7 +165,7 @@ class DecodeGraphRunner:
             plan_at=plan_at,
             width=width,
             copied=torch.cuda.Event(),
-            logits=logits,
+            logits=out_logits,
             next_ids=next_ids,
             mirror=TableMirror(),
         )
@@ -169,8 +176,9 @@ class DecodeGraphRunner:
              host_ids: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """Append one token per sequence and run the model: returns (logits (B, vocab), next IDs (B,)).
 
-        Both are views of static buffers, valid until the next call with the
-        same batch size and bucket.  Validation and cache bookkeeping follow
+        Both are the capture's own output buffers (outside the graph memory
+        pool the captures share), valid until the next call with the same
+        batch size and bucket; replays of other captures leave them alone.  Validation and cache bookkeeping follow
         the eager path (``Llama3_2._forward_packed``).  ``host_ids``: the
         token IDs as a host list, in place of ``token_ids`` (None); they then
         travel with the step's metadata copy instead of in a device copy.

@@ -28,7 +28,8 @@ Two departures, neither of which changes a value: the per-token gather +
 ``torch.stack`` of ``PagedKVCache.gather`` (``paged_cache.py:349-362``) is one
 ``index_select`` over the same slots (the same elements, copied), and the
 right operands of the two batched products are made contiguous before the
-product (a bf16 bmm over a transposed view has faulted the GPU on ROCm).
+product, which goes through ``reference_ops.batched_product`` (a bf16 bmm
+over a transposed view is a known GPU-fault hazard on ROCm).
 
 The weights are a product ``Llama3_2``'s (same parameter names as the
 reference), optionally cast to another dtype: with ``dtype=torch.float32`` the
@@ -45,7 +46,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from oracle.reference_ops import rope_module_inv_freq
+from oracle.reference_ops import batched_product, rope_module_inv_freq
 
 
 def rms_norm_reference(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
@@ -164,17 +165,17 @@ class ReferenceLlama:
             query = q[start:end].transpose(0, 1)
             keys_t = ks.transpose(0, 1).transpose(-1, -2).contiguous()
             if self.fp32_products:
-                scores = (query.float() @ keys_t.float()).to(query.dtype) * scale
+                scores = batched_product(query.float(), keys_t.float()).to(query.dtype) * scale
             else:
-                scores = query @ keys_t * scale
+                scores = batched_product(query, keys_t) * scale
             q_pos = torch.arange(ctx, total, device=x.device)[:, None]
             k_pos = torch.arange(total, device=x.device)[None, :]
             scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
             probs = torch.softmax(scores, dim=-1, dtype=torch.float32)
             values_t = vs.transpose(0, 1).contiguous()
             if self.fp32_products:
-                context_rows = (probs.to(vs.dtype).float() @ values_t.float()).to(vs.dtype)
+                context_rows = batched_product(probs.to(vs.dtype).float(), values_t.float()).to(vs.dtype)
             else:
-                context_rows = probs.to(vs.dtype) @ values_t
+                context_rows = batched_product(probs.to(vs.dtype), values_t)
             out.append(context_rows.transpose(0, 1).reshape(end - start, hq * d))
         return F.linear(torch.cat(out, dim=0), layer.wo)

@@ -15,6 +15,17 @@ import math
 import torch
 
 
+def batched_product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a @ b`` for the oracle's batched products, refusing the one form known
+    to be unsafe on ROCm GPUs: a bf16 batched product (``torch.bmm`` and what
+    ``matmul`` / ``einsum`` lower to) whose right operand is a transposed,
+    non-contiguous view can fault the device.  Every caller makes its right
+    operand contiguous first; this check keeps it that way (ValueError)."""
+    if b.is_cuda and b.dtype == torch.bfloat16 and b.dim() >= 3 and not b.is_contiguous():
+        raise ValueError("a bf16 batched product on the GPU needs a contiguous right operand")
+    return a @ b
+
+
 def paged_attention_reference(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -60,7 +71,8 @@ def paged_attention_reference_matmul(query, key_cache, value_cache, block_table,
     """:func:`paged_attention_reference` with each ``einsum`` written as a
     batched ``matmul`` over contiguous operands (head-major), for timing the
     reference's per-block loop on a ROCm GPU, where a bf16 batched product
-    over a transposed operand (what einsum forms inside) has faulted.  The
+    over a transposed operand (what einsum forms inside) is a known fault
+    hazard (:func:`batched_product`).  The
     loop, the repeat_interleave, the scale, the fp32 softmax and the casts
     are the reference's (``layers/paged_attention.py:82-114``)."""
     _, _, block_size, kv_heads, head_dim = key_cache.shape
@@ -72,11 +84,11 @@ def paged_attention_reference_matmul(query, key_cache, value_cache, block_table,
         k_rows = key_cache[layer_index, physical, :valid].repeat_interleave(group, dim=1)
         v_rows = value_cache[layer_index, physical, :valid].repeat_interleave(group, dim=1)
         k_t = k_rows.permute(1, 2, 0).contiguous()  # (Hq, D, valid)
-        scores.append((query[:, None, :] @ k_t)[:, 0, :] * (head_dim**-0.5))
+        scores.append(batched_product(query[:, None, :], k_t)[:, 0, :] * (head_dim**-0.5))
         values.append(v_rows)
     weights = torch.softmax(torch.cat(scores, dim=-1), dim=-1, dtype=torch.float32).to(query.dtype)
     v_all = torch.cat(values, dim=0).transpose(0, 1).contiguous()  # (Hq, S, D)
-    return (weights[:, None, :] @ v_all)[:, 0, :]
+    return batched_product(weights[:, None, :], v_all)[:, 0, :]
 
 
 def batched_paged_attention_reference_matmul(query, key_cache, value_cache, block_tables, sequence_lengths,
@@ -141,17 +153,17 @@ def ragged_attention_reference(
         write_tokens(keys, values, layer_index, table, block_size, ctx, k[start:end], v[start:end])
         total = ctx + n
         ks, vs = gather_tokens(keys, values, layer_index, table, block_size, total)
-        # right operands of the batched products made contiguous: on ROCm a
-        # bf16 bmm over a transposed view has faulted the GPU
+        # right operands of the batched products made contiguous (see
+        # batched_product)
         ks = ks.repeat_interleave(group, dim=1).transpose(0, 1)
         vs = vs.repeat_interleave(group, dim=1).transpose(0, 1).contiguous()
         query = q[start:end].transpose(0, 1)
-        scores = query @ ks.transpose(-1, -2).contiguous() * scale
+        scores = batched_product(query, ks.transpose(-1, -2).contiguous()) * scale
         q_pos = torch.arange(ctx, total, device=q.device)[:, None]
         k_pos = torch.arange(total, device=q.device)[None, :]
         scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
         probs = torch.softmax(scores, dim=-1, dtype=torch.float32)
-        outputs.append((probs.to(vs.dtype) @ vs).transpose(0, 1))
+        outputs.append(batched_product(probs.to(vs.dtype), vs).transpose(0, 1))
         start = end
     return torch.cat(outputs, dim=0)
 
@@ -176,10 +188,10 @@ def ragged_attention_reference_vectorized(q, k, v, keys, values, layer_index, ta
         flat_v[slots[ctx:]] = v[start:end]
         ks = flat_k.index_select(0, slots).repeat_interleave(group, dim=1).transpose(0, 1)
         vs = flat_v.index_select(0, slots).repeat_interleave(group, dim=1).transpose(0, 1).contiguous()
-        scores = q[start:end].transpose(0, 1) @ ks.transpose(-1, -2).contiguous() * scale
+        scores = batched_product(q[start:end].transpose(0, 1), ks.transpose(-1, -2).contiguous()) * scale
         scores = scores.masked_fill(pos[None, :] > pos[ctx:, None], float("-inf"))
         probs = torch.softmax(scores, dim=-1, dtype=torch.float32)
-        outputs.append((probs.to(vs.dtype) @ vs).transpose(0, 1))
+        outputs.append(batched_product(probs.to(vs.dtype), vs).transpose(0, 1))
         start = end
     return torch.cat(outputs, dim=0)
 

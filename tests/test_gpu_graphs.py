@@ -121,6 +121,38 @@ def test_decode_graph_replays_match_eager_step(dtype, max_graphs):
     _log(f"  captures={runner.captures} replays={runner.replays} evictions={runner.evictions}")
 
 
+def test_decode_graph_logits_survive_other_captures():
+    """A step's logits (and next IDs) stay as they were while other captures
+    replay: two batch sizes (two captures sharing one memory pool) are
+    replayed alternately, and each step's returned logits, read back after
+    the other capture's next replay, still hold what they held when
+    returned."""
+    _log("decode graph logits across captures")
+    model = _graph_model(torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(2)
+    prompts = [torch.randint(0, 512, (1, n), generator=gen, device=DEV) for n in (40, 90, 17, 64, 33)]
+    ids = ("a", "b", "c", "d", "e")
+    cache = _cache(model)
+    with torch.inference_mode():
+        first = paged_prefill(model, tuple(prompts), cache, ids)
+    runner = DecodeGraphRunner(model, cache, max_batch_size=8)
+    tokens = {sid: first[i].argmax(-1).view(1) for i, sid in enumerate(ids)}
+    groups = (("a", "b"), ("c", "d", "e"))
+    held = []  # (logits view, next view, copies at return time)
+    for step in range(6):
+        group = groups[step % 2]
+        with torch.inference_mode():
+            logits, nxt = runner.step(torch.cat([tokens[s] for s in group]), group)
+        torch.cuda.synchronize()
+        held.append((logits, nxt, logits.clone(), nxt.clone()))
+        for i, s in enumerate(group):
+            tokens[s] = nxt[i].view(1).clone()
+        if step >= 1:  # the previous step (the other capture) was returned before this replay
+            old_logits, old_next, want_logits, want_next = held[step - 1]
+            assert torch.equal(old_logits, want_logits) and torch.equal(old_next, want_next), step
+    assert runner.captures == 2 and runner.replays == 6
+
+
 def test_scheduler_tokens_identical_with_decode_graphs():
     _log("scheduler with decode graphs")
     model = _graph_model(torch.bfloat16)

@@ -44,6 +44,20 @@ def _decode_oracle(wl, kc_cpu, vc_cpu, q_cpu):
     )
 
 
+def test_oracle_refuses_bf16_batched_product_over_a_transposed_view():
+    """The oracle's batched products on the GPU take contiguous right operands
+    only in bf16 (the form that can fault is refused before any launch);
+    contiguous operands and other dtypes go through unchanged."""
+    a = torch.randn((4, 3, 8), device=DEV).to(torch.bfloat16)
+    b = torch.randn((4, 5, 8), device=DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError, match="contiguous right operand"):
+        reference_ops.batched_product(a, b.transpose(-1, -2))
+    got = reference_ops.batched_product(a, b.transpose(-1, -2).contiguous())
+    assert torch.equal(got, torch.matmul(a, b.transpose(-1, -2).contiguous()))
+    f = reference_ops.batched_product(a.float(), b.float().transpose(-1, -2))
+    assert f.shape == (4, 3, 5)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_kv_append_bit_exact(dtype):
     _log(f"kv_append dtype={dtype}")
@@ -497,6 +511,23 @@ def test_varlen_prefill_long_workloads(which):
     err = (got.float() - want.float()).abs().max().item()
     _log(f"  max_abs_err={err:.3e}")
     assert err <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_varlen_prefill_requests_past_index_255(dtype):
+    """260 empty requests before four real ones: the real requests' query
+    tiles carry request indices above 255, which the kernel-argument item
+    table cannot encode, so the host plan must fall back to uniform pieces
+    (whose merge jobs match what the kernel locates) rather than a balanced
+    plan; the output matches the oracle."""
+    _log(f"varlen prefill, requests past index 255, {dtype}")
+    ctx = [16] * 260 + [3000, 0, 1200, 5000]
+    qlen = [0] * 260 + [128, 128, 64, 1]
+    wl = workloads.ragged(ctx, qlen, seed=31, pool_factor=1.2)
+    got, want = _prefill_case(wl, dtype)
+    err = (got.float() - want.float()).abs().max().item()
+    _log(f"  max_abs_err={err:.3e}")
+    assert err <= TOL[dtype]
 
 
 @pytest.mark.parametrize("context,query", [(300, 16), (600, 8), (1000, 40), (20000, 16)])

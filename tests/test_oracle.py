@@ -445,3 +445,11 @@ def test_product_rope_and_tables_match_oracle_bit_for_bit(dtype, scaled):
     angles = positions.float()[:, None] * inv_freq
     assert torch.equal(cos[positions], torch.cos(angles).to(dtype))
     assert torch.equal(sin[positions], torch.sin(angles).to(dtype))
+
+
+def test_batched_product_is_the_matmul_on_the_cpu():
+    """On the CPU the oracle's guarded product is ``a @ b`` for any layout."""
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn((3, 2, 8), generator=gen).to(torch.bfloat16)
+    b = torch.randn((3, 5, 8), generator=gen).to(torch.bfloat16).transpose(-1, -2)
+    assert torch.equal(reference_ops.batched_product(a, b), a @ b)
