@@ -38,7 +38,16 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-TRAFFIC_PROFILE = os.path.join("profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json")
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the value leg's call, per rounding mode
+TRAFFIC_PROFILES = {
+    "reference": os.path.join("profiles", "decode_pass_kernel__decode_step_b16_lognormal__hbm_traffic.json"),
+    "fast": os.path.join("profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json"),
+}
+# the kernels of one nie_paged_decode_append call, per rounding mode
+DECODE_CALL_KERNELS = {
+    "reference": "decode_pass_kernel (scores pass) + decode_pass_kernel (P.V pass) + decode_merge_kernel (sum)",
+    "fast": "paged_decode_kernel + decode_merge_kernel",
+}
 
 
 def parse_args():
@@ -49,7 +58,8 @@ def parse_args():
     p.add_argument("--layers", type=int, default=16)
     p.add_argument("--unfused-append", action="store_true",
                    help="decode step as nie_kv_append then nie_paged_decode (two launches per layer)")
-    p.add_argument("--only", choices=["decode", "small", "stress", "mixed", "long", "e2e", "linear", "reference"],
+    p.add_argument("--only", choices=["decode", "small", "stress", "mixed", "long", "e2e", "linear", "reference",
+                                      "onepass"],
                    help="run one leg and print its JSON only")
     p.add_argument("--skip", action="append", default=[],
                    choices=["small", "stress", "stress-model", "mixed", "long", "e2e", "reference", "cpu", "lockstep"],
@@ -223,10 +233,10 @@ def _event_rate(bench, ev, first_step: int, steps: int, fused: bool):
     return per_call, avg, per_call / avg / 1e9
 
 
-def _measured_traffic():
+def _measured_traffic(rounding: str):
     """HBM bytes per decode call of the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE)."""
     try:
-        with open(os.path.join(REPO, TRAFFIC_PROFILE)) as f:
+        with open(os.path.join(REPO, TRAFFIC_PROFILES[rounding])) as f:
             data = json.load(f)
         return data.get("hbm_bytes_per_launch"), data.get("algorithmic_bytes_per_launch")
     except (OSError, ValueError):
@@ -283,7 +293,7 @@ def run_decode(args):
     log(f"timed {args.steps} steps in {elapsed * 1e3:.2f} ms ({value:.0f} GB/s); {call} call avg "
         f"{avg_s * 1e6:.2f} us for {bytes_per_call / 1e6:.2f} MB -> {achieved:.0f} GB/s; serving plan "
         f"{s_avg * 1e6:.2f} us -> {s_gbs:.0f} GB/s")
-    traffic, traffic_alg = _measured_traffic()
+    traffic, traffic_alg = _measured_traffic(args.rounding)
     result = {
         "metric": "paged-attn HBM GB/s (% of peak); e2e output tok/s, Llama-1B-shape batch 16",
         "value": round(value, 2),
@@ -310,13 +320,14 @@ def run_decode(args):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{call} call: paged_decode_kernel + decode_merge_kernel (HIP events around the call)",
+            "kernel": f"{call} call: {DECODE_CALL_KERNELS[args.rounding]} (HIP events around the call)",
+            "rounding": args.rounding,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "traffic_source": f"{TRAFFIC_PROFILE}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this call on this "
+            "traffic_source": f"{TRAFFIC_PROFILES[args.rounding]}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this call on this "
                               f"workload (algorithmic bytes there: {traffic_alg}), scaled by a 1 GiB copy",
             "algorithmic_bytes_per_launch": int(bytes_per_call),
             "avg_launch_us": round(avg_s * 1e6, 3),
@@ -667,14 +678,22 @@ def run_e2e(args):
 # the reference algorithm's own times (the oracle, on the GPU and the host)
 # ---------------------------------------------------------------------------
 def _cpu_model() -> str:
+    """The host CPU's model name with its family / model / stepping numbers
+    (a virtualised host may report only a generic name)."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" in line:
+                    key, value = (s.strip() for s in line.split(":", 1))
+                    fields.setdefault(key, value)
+                if not line.strip() and fields:
+                    break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ids = [f"{k.split()[-1]} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def _time_host(fn, min_seconds: float, max_reps: int = 1000, warmup: bool = True):
@@ -904,6 +923,38 @@ def run_linear(args):
     return out
 
 
+def run_one_pass_rounding(args):
+    """The cost of the reference's rounding point: configurations 2, 3 and 5
+    (and the long prefills) again with the one-pass rounding (online softmax,
+    NIE_ROUND_FAST), the kernels the reference rounding replaced."""
+    from nano_infer_engine import _native
+
+    _native.set_attention_rounding("fast")
+    try:
+        fast = argparse.Namespace(**{**vars(args), "rounding": "fast"})
+        d = run_decode(fast)
+        s = run_stress(fast)
+        m = run_mixed(fast)
+        lp = run_prefill_long(fast)
+    finally:
+        _native.set_attention_rounding(args.rounding)
+    return {
+        "rounding": "fast (one pass, online softmax)",
+        "config2_decode_call": {"avg_launch_us": d["roofline"]["avg_launch_us"], "frac": d["roofline"]["frac"],
+                                "step_GBs": d["value"]},
+        "config2_serving_plan_call": {"avg_launch_us": d["serving_plan_decode"]["avg_launch_us"],
+                                      "frac": d["serving_plan_decode"]["frac"]},
+        "config5_16x29600_call": {"avg_launch_us": s["avg_launch_us"], "frac": s["frac"]},
+        "config3_prefill_call": {"avg_launch_us": m["prefill"]["avg_launch_us"], "frac": m["prefill"]["frac"]},
+        "config3_decode_rows_call": {"avg_launch_us": m["decode_rows"]["avg_launch_us"],
+                                     "frac": m["decode_rows"]["frac"]},
+        "prefill_prompts_4x2048": {"avg_launch_us": lp["prompts_4x2048"]["avg_launch_us"],
+                                   "frac": lp["prompts_4x2048"]["frac"]},
+        "prefill_chunks_4x512_on_8192": {"avg_launch_us": lp["chunks_4x512_on_8192"]["avg_launch_us"],
+                                         "frac": lp["chunks_4x512_on_8192"]["frac"]},
+    }
+
+
 def run_copy_calibration(mib: int):
     """A plain copy of known size: each launch reads and writes mib MiB."""
     import torch
@@ -937,6 +988,7 @@ def main():
         "e2e": ("e2e_llama1b_serving", run_e2e),
         "linear": ("decode_projections", run_linear),
         "reference": ("reference_path", lambda a: {**run_reference_path(a), "serving_lockstep": run_lockstep(a)}),
+        "onepass": ("one_pass_rounding", run_one_pass_rounding),
     }
     if args.only:
         key, fn = only[args.only]
@@ -960,6 +1012,8 @@ def main():
         result["reference_path"] = run_reference_path(args)
         if "lockstep" not in skip:
             result["reference_path"]["serving_lockstep"] = run_lockstep(args)
+    if "onepass" not in skip and args.rounding == "reference":
+        result["one_pass_rounding"] = run_one_pass_rounding(args)
     result["cpu_baseline"] = None if "cpu" in skip else run_cpu_baseline(args)
     print(json.dumps(result), flush=True)
 
