@@ -25,6 +25,18 @@ def _log(msg: str) -> None:
     print(msg, flush=True)
 
 
+@pytest.fixture(params=["reference", "fast"])
+def rounding(request):
+    """Both bf16 rounding points: the reference's (two passes, the default)
+    and the one-pass online softmax (NIE_ROUND_FAST); fp32 calls are the
+    same either way."""
+    _native.set_attention_rounding(request.param)
+    try:
+        yield request.param
+    finally:
+        _native.set_attention_rounding("reference")
+
+
 def _decode_hip(wl: workloads.PagedWorkload, kc, vc, q, dtype, host_plan=False):
     """The kernel's output.  host_plan: pass a host copy of the lengths (exact
     launch plan, work items in the kernel arguments)."""
@@ -187,7 +199,7 @@ def test_rope_kv_append_bit_exact(dtype, q_heads, kv_heads, head_dim):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_decode_small_matches_oracle(dtype):
+def test_decode_small_matches_oracle(dtype, rounding):
     _log(f"decode_small dtype={dtype}")
     wl = workloads.decode_small()
     kc, vc = wl.pool(dtype)
@@ -206,7 +218,7 @@ def test_decode_small_matches_oracle(dtype):
 
 
 @pytest.mark.parametrize("host_plan", [False, True])
-def test_decode_ragged_lognormal_bf16(host_plan):
+def test_decode_ragged_lognormal_bf16(host_plan, rounding):
     """16 sequences, lognormal lengths up to 29600 (split-K with merge);
     launches planned from bounds and from host lengths."""
     _log(f"decode_ragged bf16 host_plan={host_plan}")
@@ -226,7 +238,7 @@ def test_decode_ragged_lognormal_bf16(host_plan):
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("host_plan", [False, True])
-def test_decode_shapes(q_heads, kv_heads, head_dim, block_size, dtype, host_plan):
+def test_decode_shapes(q_heads, kv_heads, head_dim, block_size, dtype, host_plan, rounding):
     _log(f"decode shapes hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} host_plan={host_plan}")
     wl = workloads.ragged([0, 4, 70, 300, 1000], [1] * 5, seed=7, pool_factor=1.5, q_heads=q_heads,
                           kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
@@ -394,7 +406,7 @@ def _append_decode_pair(wl, dtype, host_plan, layer=0, table_edit=None, rope=Fal
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("host_plan", [False, True])
-def test_decode_append_matches_append_then_decode(q_heads, kv_heads, head_dim, block_size, dtype, host_plan):
+def test_decode_append_matches_append_then_decode(q_heads, kv_heads, head_dim, block_size, dtype, host_plan, rounding):
     """The new token lands on every row of a 16-key tile (contexts 0, 4, 15,
     16, 70, 300, 1000) and in single- and multi-split sequences."""
     _log(f"decode_append hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} host_plan={host_plan}")
@@ -426,7 +438,7 @@ def test_decode_append_ragged_lognormal_bf16(host_plan):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("host_plan", [False, True])
 def test_decode_rope_append_matches_rope_append_then_decode(q_heads, kv_heads, head_dim, block_size, dtype,
-                                                           host_plan):
+                                                           host_plan, rounding):
     """Fused RoPE + append + decode == nie_rope_kv_append then nie_paged_decode,
     caches and outputs bit for bit, q left unrotated."""
     _log(f"decode_rope_append hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype} "
@@ -437,7 +449,7 @@ def test_decode_rope_append_matches_rope_append_then_decode(q_heads, kv_heads, h
 
 
 @pytest.mark.parametrize("rope", [False, True])
-def test_decode_append_ignores_stale_slot_content(rope):
+def test_decode_append_ignores_stale_slot_content(rope, rounding):
     """NaN in the new token's slot and in every later slot of its block (what
     an unwritten pool may hold): the fused call's reads of those slots are
     replaced by the new row, so the output is finite and bit-identical to the
@@ -491,7 +503,7 @@ def _prefill_case(wl, dtype, host_plan=True):
 
 @pytest.mark.parametrize("host_plan", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_varlen_prefill_mixed_batch(dtype, host_plan):
+def test_varlen_prefill_mixed_batch(dtype, host_plan, rounding):
     _log(f"varlen mixed {dtype} host_plan={host_plan}")
     wl = workloads.mixed_prefill()
     got, want = _prefill_case(wl, dtype, host_plan)
@@ -501,7 +513,7 @@ def test_varlen_prefill_mixed_batch(dtype, host_plan):
 
 
 @pytest.mark.parametrize("which", ["prefill_prompts", "prefill_long_context"])
-def test_varlen_prefill_long_workloads(which):
+def test_varlen_prefill_long_workloads(which, rounding):
     """The long-prefill workloads the bench times: 4 fresh 2048-token prompts
     (64 query tiles per request, causal) and 4 chunks of 512 tokens on
     8192-token contexts, bf16, launches planned from host lengths."""
@@ -552,7 +564,7 @@ def test_varlen_prefill_merge_batches(dtype, host_plan, context, query):
     [(4, 4, 64, 16), (4, 2, 64, 2), (8, 1, 64, 4), (16, 1, 64, 16), (32, 2, 128, 32), (8, 4, 128, 5)],
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_varlen_prefill_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
+def test_varlen_prefill_shapes(q_heads, kv_heads, head_dim, block_size, dtype, rounding):
     _log(f"varlen shapes hq={q_heads} hkv={kv_heads} d={head_dim} bs={block_size} {dtype}")
     wl = workloads.ragged([0, 3, 50, 0, 17], [19, 5, 1, 40, 2], seed=13, pool_factor=1.5, q_heads=q_heads,
                           kv_heads=kv_heads, head_dim=head_dim, block_size=block_size)
@@ -568,7 +580,7 @@ def test_varlen_prefill_shapes(q_heads, kv_heads, head_dim, block_size, dtype):
 )
 @pytest.mark.parametrize("host_plan", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_varlen_prefill_split_keys(q_heads, kv_heads, head_dim, block_size, dtype, host_plan):
+def test_varlen_prefill_split_keys(q_heads, kv_heads, head_dim, block_size, dtype, host_plan, rounding):
     """Contexts long enough that query tiles are split over several workgroups
     (at least 8 key tiles per split) and merged, next to short requests and
     decode rows; launches planned from host lengths and from bounds."""
