@@ -282,6 +282,51 @@ int nie_set_attention_rounding(int mode);
 int nie_attention_rounding(void);
 
 /*
+ * The one-launch reference-rounding decode.  With the reference rounding, a
+ * bf16 decode call whose head_dim is 64, whose block_size is a power of two
+ * of at least 16, whose GQA group has at most 4 query heads and whose work
+ * items can all be resident on the GPU at once runs as one kernel (each
+ * split keeps its scores on chip; the splits exchange only their (max, sum)
+ * pairs, through the workspace's control region) plus the sum of the split
+ * partials, instead of the two passes over the keys.  Its outputs are
+ * bit-identical to the two passes'.  nie_set_decode_fused(0) turns it off
+ * for calls issued after it in the whole process (1, the default, on);
+ * NIE_EINVAL for other values.
+ * No counterpart in the reference (an execution strategy of its decode
+ * attention, layers/paged_attention.py:88-116).
+ */
+int nie_set_decode_fused(int on);
+int nie_decode_fused(void);
+
+/*
+ * Polls a split of the one-launch decode makes, waiting for the other
+ * splits of its sequence, before it forms their (max, sum) pairs itself
+ * from K (the same numbers, at the cost of reading their keys); default
+ * 32768.  0 makes every wait give up at once, which tests use to run that
+ * path.  NIE_EINVAL for negative values.
+ * No counterpart in the reference.
+ */
+int nie_set_decode_fused_spin(int polls);
+
+/*
+ * Bytes at the start of every decode and prefill workspace that hold the
+ * control region (counters of the one-launch decode).  They must be zero
+ * before a workspace is first used; every call leaves its counters zero, so
+ * a workspace needs clearing only once, when it is allocated.  The
+ * workspace queries include these bytes.
+ * No counterpart in the reference.
+ */
+int64_t nie_workspace_control_bytes(void);
+
+/* Which kernels the calling thread's last nie_paged_decode* call ran. */
+#define NIE_DECODE_PATH_NONE 0     /* no call yet, or it failed before launching */
+#define NIE_DECODE_PATH_ONE_PASS 1 /* fp32, or bf16 with NIE_ROUND_FAST */
+#define NIE_DECODE_PATH_PASSES 2   /* reference rounding: scores pass, P.V pass, sum */
+#define NIE_DECODE_PATH_FUSED 3    /* reference rounding: the one-launch decode, sum */
+#define NIE_DECODE_PATH_GENERIC 4  /* shapes outside the MFMA kernels */
+int nie_decode_last_path(void);
+
+/*
  * Workspace bytes needed by nie_paged_decode for a call with these
  * arguments (same meaning as there; host values), whose sequence lengths
  * have maximum max_seq_len and sum total_seq_len, and the same optional

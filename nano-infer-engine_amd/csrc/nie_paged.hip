@@ -897,6 +897,29 @@ __global__ __launch_bounds__(kWave) void argmax_merge_kernel(const ArgmaxPartial
 // ---------------------------------------------------------------------------
 constexpr int kDecodeWaves = 8;  // KV heads handled by one workgroup (one per wave)
 
+// Control region at the start of every decode and prefill workspace: one
+// counter per (sequence, KV head) of a call, for the one-launch
+// decode's splits to find each other (decode_fused_kernel), each on a
+// 128-byte line of its own (the pollers of different counters do not meet
+// on one line), and a count of the waits that gave up.  It must be zero
+// before a workspace's first call; every call leaves the counters zero
+// again.
+constexpr int64_t kCtlBytes = 256 * 1024;
+constexpr int kCtlSlotBytes = 128;
+constexpr int kCtlPairs = (int)(kCtlBytes / kCtlSlotBytes) - 1;
+
+struct DecodeCtlSlot {
+  uint32_t count;  // splits of the pair that have published their (max, sum) pairs
+  uint32_t done;   // splits of the pair that have published their output shares
+  uint32_t pad[kCtlSlotBytes / 4 - 2];
+};
+
+struct DecodeCtl {
+  DecodeCtlSlot pair[kCtlPairs];
+  DecodeCtlSlot gave_up;  // .count: waits that gave up (only grows; a diagnostic count)
+};
+static_assert(sizeof(DecodeCtl) == kCtlBytes, "control words fill their region");
+
 struct DecodeArgs {
   const void* q;
   int64_t q_sb, q_sh;
@@ -935,6 +958,11 @@ struct DecodeArgs {
   // captured launch replays with the plan its step's host lengths call for,
   // written there before each replay; count 0 there: locate on the device.
   const struct DecodeItems* __restrict__ dev_items = nullptr;
+  // One-launch decode: the workspace's control region, and the polls a
+  // split's wait for the others makes before it forms their statistics
+  // itself
+  DecodeCtl* ctl = nullptr;
+  int32_t spin_limit = 0;
 };
 
 // Work items of a decode call planned from host copies of the lengths,
@@ -1676,7 +1704,28 @@ __device__ __forceinline__ void rope_vec(v4u& lo, v4u& hi, const v4u& c, const v
 // The sum of the nsplit split partials of one row (the two-pass rounding's
 // partials are shares of the normalised output, so they merge by plain
 // addition), in the same fixed order as merge_row, rounded once.
-template <typename T, int D>
+// Agent-scope (coherent across the XCDs' L2s) stores and loads of four
+// floats, as two 64-bit halves: how one workgroup hands another its split
+// shares inside a launch.
+__device__ __forceinline__ void store_agent4(float* p, float x, float y, float z, float w) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p + 2),
+                     (uint64_t)__float_as_uint(z) | ((uint64_t)__float_as_uint(w) << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float4 load_agent4(const float* p) {
+  const uint64_t lo = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                     __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32)));
+}
+
+// kAgent: the partials were stored by other workgroups of the running
+// launch (store_agent4), so they are read with agent-scope loads.
+template <typename T, int D, bool kAgent = false>
 __device__ __forceinline__ void sum_row(const float* po, int64_t po_stride, int nsplit, T* out) {
   constexpr int kLanesPerSplit = D / 4;
   constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
@@ -1693,8 +1742,12 @@ __device__ __forceinline__ void sum_row(const float* po, int64_t po_stride, int 
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
       const int sp = p * kSplitsPerPass + sub;
-      v[p] = sp < count ? *reinterpret_cast<const float4*>(po + (s0 + sp) * po_stride)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (kAgent) {
+        v[p] = sp < count ? load_agent4(po + (s0 + sp) * po_stride) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        v[p] = sp < count ? *reinterpret_cast<const float4*>(po + (s0 + sp) * po_stride)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
@@ -1712,6 +1765,68 @@ __device__ __forceinline__ void sum_row(const float* po, int64_t po_stride, int 
     acc.w += __shfl_xor(acc.w, off);
   }
   if (sub == 0) store4<T>(out + 4 * chunk, acc.x, acc.y, acc.z, acc.w);
+}
+
+// sum_row over up to kRows rows at once (row n's split s at po + n *
+// row_stride + s * po_stride, its output at out + n * out_stride): every
+// row's loads of a batch are issued before any is added, and each row is
+// summed in sum_row's order (the same bits).
+template <typename T, int D, bool kAgent, int kRows>
+__device__ __forceinline__ void sum_rows(const float* po, int64_t row_stride, int64_t po_stride, int nsplit, int rows,
+                                         T* out, int64_t out_stride) {
+  constexpr int kLanesPerSplit = D / 4;
+  constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
+  constexpr int kPasses = 8;
+  constexpr int kBatch = kPasses * kSplitsPerPass;
+  const int lane = lane_id();
+  const int sub = lane / kLanesPerSplit;
+  const int chunk = lane % kLanesPerSplit;
+  po += 4 * chunk;
+  float4 acc[kRows];
+#pragma unroll
+  for (int n = 0; n < kRows; ++n) acc[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+    const int count = min(kBatch, nsplit - s0);
+    float4 v[kRows][kPasses];
+#pragma unroll
+    for (int n = 0; n < kRows; ++n) {
+#pragma unroll
+      for (int p = 0; p < kPasses; ++p) {
+        const int sp = p * kSplitsPerPass + sub;
+        const float* src = po + n * row_stride + (s0 + sp) * po_stride;
+        if (n < rows && sp < count) {
+          if constexpr (kAgent) {
+            v[n][p] = load_agent4(src);
+          } else {
+            v[n][p] = *reinterpret_cast<const float4*>(src);
+          }
+        } else {
+          v[n][p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < kRows; ++n) {
+#pragma unroll
+      for (int p = 0; p < kPasses; ++p) {
+        acc[n].x += v[n][p].x;
+        acc[n].y += v[n][p].y;
+        acc[n].z += v[n][p].z;
+        acc[n].w += v[n][p].w;
+      }
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < kRows; ++n) {
+#pragma unroll
+    for (int off = kLanesPerSplit; off < kWave; off <<= 1) {
+      acc[n].x += __shfl_xor(acc[n].x, off);
+      acc[n].y += __shfl_xor(acc[n].y, off);
+      acc[n].z += __shfl_xor(acc[n].z, off);
+      acc[n].w += __shfl_xor(acc[n].w, off);
+    }
+    if (sub == 0 && n < rows) store4<T>(out + n * out_stride + 4 * chunk, acc[n].x, acc[n].y, acc[n].z, acc[n].w);
+  }
 }
 
 template <typename T, int D>
@@ -2624,6 +2739,524 @@ __global__ __launch_bounds__(kHeads* kWave) void decode_pass_kernel(DecodeArgs a
     for (int c = 0; c < D / 16; ++c) {
       *reinterpret_cast<float4*>(dst + 16 * c) = make_float4(o[c][0], o[c][1], o[c][2], o[c][3]);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One-launch decode with the reference's rounding point, for bf16, head_dim
+// 64, block sizes that keep a 16-key tile inside one block and GQA groups of
+// at most four query heads.  decode_pass_kernel's two launches hand the
+// scores over through HBM; here every wave keeps its own scores on chip and
+// only the splits' (max, sum) pairs and output shares cross workgroups:
+//   - a wave owns one KV head of one work item and loads that head's K and V
+//     rows straight into VGPRs (load_slice's operand layout) by buffer
+//     loads, kFusedDepth two-tile steps ahead;
+//   - the K phase forms the scores and the split's (max, sum) exactly as the
+//     scores pass does, keeping the scores in the wave's LDS region (at most
+//     kDecodeMaxTilesPerSplit tiles x 4 query rows x 16 keys, bf16);
+//   - the wave publishes its pairs with agent-scope stores, which write
+//     through to memory, waits for them, and counts itself in the (sequence,
+//     KV head) counter of the workspace's control region; then it issues its
+//     first V loads and waits (one lane polling) until every split of its
+//     head has counted itself, reads their pairs with agent-scope loads and
+//     combines them as the P.V pass does;
+//   - the V phase stages each step's V rows in a 4 KiB LDS region of the
+//     wave, from which the transposing reads form the V^T operands, and
+//     accumulates bf16(e^(s - m) / l) . V as the P.V pass does;
+//   - each split stores its share of the output rows (agent scope) and
+//     counts it; the wave that counts the last share sums the shares in
+//     decode_merge_kernel<kSum>'s order and clears the pair's counters.
+// The waves of a workgroup meet once per kFusedDepth steps of each phase and
+// otherwise run apart.  Only agent-scope atomic accesses carry data between
+// workgroups, so no L2 writeback or invalidate is needed.  The waits rely on
+// every workgroup of the call being resident at once (the launcher takes
+// this path only when the grid fits the CUs' room for the kernel) for speed,
+// not for correctness: a wait that gives up after spin_limit polls forms
+// every split's (max, sum) itself from K, with the same steps and arithmetic
+// as the splits, so it combines the same numbers.  Outputs and cache writes
+// are bit-identical to the two launches' and the sum's.
+// ---------------------------------------------------------------------------
+constexpr int kFusedDim = 64;
+constexpr int kFusedMaxGroup = 4;
+// Two-tile steps of K (or V) loads in flight per wave: 16 KiB per wave,
+// 128 KiB per CU.  Six steps measured slower (16 x 29600 tokens: 176-181 us
+// against 172-176 us a call).
+constexpr int kFusedDepth = 4;
+constexpr int kFusedScoreBytes = (int)kDecodeMaxTilesPerSplit * kFusedMaxGroup * kTileKeys * 2;  // 16 KiB
+constexpr int kFusedStageBytes = kPassStepTiles * kTileKeys * kFusedDim * 2;                       // 4 KiB
+constexpr int kFusedWaveLds = kFusedScoreBytes + kFusedStageBytes;
+constexpr int kFusedSpinLimit = 1 << 15;
+// Cache policy of the K/V loads.  Each load instruction reads 64 of a row's
+// 128 bytes (the next reads the rest), so the lines are worth keeping
+// between the two: the streaming (nt) policy measured 3-8% slower.
+constexpr int kFusedCachePolicy = kCacheDefault;
+// The fourth word of a raw buffer resource on gfx9 (32-bit data format).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// This lane's two 16-byte vectors of one 16-key tile of a head (vector j =
+// bytes [64j + 16 * (lane / 16), +16) of row lane % 16, at lane_off within
+// the tile), by buffer loads whose range ends after the tile's `rows`
+// valid keys: rows past them read as zero without a memory access, and a
+// tile with no valid key reads nothing.  The loads are the compiler's (it
+// counts them), so a loop can keep several tiles in flight.
+__device__ __forceinline__ void load_tile_slice(v4u (&v)[2], const unsigned char* tile, int rows, int row_bytes,
+                                                int lane_off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(tile), (short)0, rows * row_bytes, kBufferRsrcWord3);
+  v[0] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, 0, kFusedCachePolicy);
+  v[1] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off + 64, 0, kFusedCachePolicy);
+}
+
+// Polls (one lane) until *word reaches `target`; false after `limit` polls.
+// The sleep between polls (about 500 clocks) keeps thousands of waiting
+// waves from crowding the lines they poll.
+__device__ __forceinline__ bool wait_count(uint32_t* word, uint32_t target, int limit) {
+  for (int n = 0; n < limit; ++n) {
+    if (__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
+    __builtin_amdgcn_s_sleep(8);
+  }
+  return false;
+}
+
+template <int kHeads>
+__global__ __launch_bounds__(kHeads* kWave) void decode_fused_kernel(DecodeArgs a, DecodeItems items) {
+  using T = bf16_t;
+  constexpr int D = kFusedDim;
+  using F = Frag<T, D>;
+  using VT = GroupTile<T, D, 1>;  // one head's rows of a V tile
+  static_assert(F::kVec == 2 && VT::kBytes * kPassStepTiles == kFusedStageBytes, "head_dim 64 layout");
+  constexpr int kEltPerChunk = 16 / (int)sizeof(T);
+  constexpr int kDepth = kFusedDepth;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kHeads][kFusedWaveLds];
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int g = lane >> 4;
+  const int row = lane & 15;
+
+  DecodeWork w;
+  if (!decode_work(a, items, w)) return;
+  // the work item in SGPRs: the loops' bounds and the buffer ranges below
+  // must be known uniform, or the compiler serialises the loads over lanes
+  const int64_t b = uniform64(w.b);
+  const int64_t nsplit = uniform64(w.nsplit);
+  const int64_t item = uniform64(w.first_item + w.split);
+  w.first_item = uniform64(w.first_item);
+  w.split = uniform64(w.split);
+  const int seq_len = __builtin_amdgcn_readfirstlane(w.seq_len);
+  const int tps = __builtin_amdgcn_readfirstlane((int)w.tps);
+  const int h = (int)blockIdx.y * kHeads + wave;
+  const int group = a.group;
+  const int32_t* table = a.tables + b * a.table_stride;
+  const int tlen = (int)a.table_stride;
+  const int key_begin = (int)w.split * tps * kTileKeys;
+  const int key_end = min(key_begin + tps * kTileKeys, seq_len);
+  const bool row_valid = row < group;
+  const int qh = h * group + row;
+  const bool has_new = a.k_new != nullptr;
+  const int last_key = seq_len - 1;  // the appended key, with an append
+  const int row_bytes = a.geom.row_elems32 * (int)sizeof(T);
+  const int lane_off = row * row_bytes + (h * D + kEltPerChunk * g) * (int)sizeof(T);
+  const unsigned char* const kbytes = reinterpret_cast<const unsigned char*>(a.k_cache);
+  const unsigned char* const vbytes = reinterpret_cast<const unsigned char*>(a.v_cache);
+  DecodeCtl* const ctl = a.ctl;
+  const int64_t pair = b * a.geom.kv_heads + h;  // (sequence, KV head)
+  // the sequence's (max, sum) slots lie inside the workspace and its pair
+  // has a counter (uniform); otherwise only the append is done
+  const bool ws_ok = a.ws_ml != nullptr && ctl != nullptr && w.first_item + nsplit <= a.ws_items && pair < kCtlPairs;
+
+  // q, and with an append the new K row (both rotated with RoPE) and V row
+  F qf, kn, vn;
+  if (row_valid) {
+    load_slice<T, D>(qf, reinterpret_cast<const T*>(a.q) + b * a.q_sb + qh * a.q_sh);
+  } else {
+    qf.v[0] = qf.v[1] = uint4{0u, 0u, 0u, 0u};
+  }
+  kn.v[0] = kn.v[1] = vn.v[0] = vn.v[1] = uint4{0u, 0u, 0u, 0u};
+  // append: the new rows have a slot in the pool, so they are written there
+  // and their key reads them; otherwise (as kv_append skips such a slot)
+  // nothing is written and the key reads what the cache holds
+  bool append = false;
+  if (has_new) {
+    load_slice<T, D>(kn, reinterpret_cast<const T*>(a.k_new) + b * a.kn_s + h * D);
+    load_slice<T, D>(vn, reinterpret_cast<const T*>(a.v_new) + b * a.vn_s + h * D);
+    if (a.rope_cos != nullptr) {
+      int64_t pos = last_key;
+      pos = pos >= a.rope_rows ? a.rope_rows - 1 : pos;
+      const int d0 = kEltPerChunk * g;  // the lane's dims 8g..8g+7 (and 32 + 8g..)
+      const v4u c = *reinterpret_cast<const v4u*>(reinterpret_cast<const T*>(a.rope_cos) + pos * (D / 2) + d0);
+      const v4u s = *reinterpret_cast<const v4u*>(reinterpret_cast<const T*>(a.rope_sin) + pos * (D / 2) + d0);
+      v4u lo = __builtin_bit_cast(v4u, kn.v[0]), hi = __builtin_bit_cast(v4u, kn.v[1]);
+      rope_vec<T>(lo, hi, c, s);
+      kn.v[0] = __builtin_bit_cast(uint4, lo);
+      kn.v[1] = __builtin_bit_cast(uint4, hi);
+      if (row_valid) {
+        lo = __builtin_bit_cast(v4u, qf.v[0]);
+        hi = __builtin_bit_cast(v4u, qf.v[1]);
+        rope_vec<T>(lo, hi, c, s);
+        qf.v[0] = __builtin_bit_cast(uint4, lo);
+        qf.v[1] = __builtin_bit_cast(uint4, hi);
+      }
+    }
+    int lb, off;
+    if (a.geom.bs_shift >= 0) {
+      lb = last_key >> a.geom.bs_shift;
+      off = last_key & (a.geom.block_size - 1);
+    } else {
+      lb = (int)((uint32_t)last_key / (uint32_t)a.geom.block_size);
+      off = last_key - lb * a.geom.block_size;
+    }
+    const int phys = __builtin_amdgcn_readfirstlane(lb < tlen ? table[lb] : -1);
+    append = phys >= 0 && phys < a.geom.num_blocks;
+    // the split that ends the sequence writes the new rows to their slot
+    // (row 0's lanes the K row, row 1's the V row); the loads below take
+    // the new rows from registers, never from the slot
+    if (append && key_end == seq_len && row < 2) {
+      {
+        T* cache = reinterpret_cast<T*>(const_cast<void*>(row == 0 ? a.k_cache : a.v_cache));
+        uint4* dst = reinterpret_cast<uint4*>(cache + a.geom.layer_offset +
+                                              ((int64_t)phys * a.geom.block_size + off) * a.geom.row_elems + h * D +
+                                              kEltPerChunk * g);
+        uint4 lo, hi;  // (assigned by branches: a conditional over the two rows would select their addresses)
+        if (row == 0) {
+          lo = kn.v[0];
+          hi = kn.v[1];
+        } else {
+          lo = vn.v[0];
+          hi = vn.v[1];
+        }
+        dst[0] = lo;
+        dst[4] = hi;  // 64 bytes further: dims 32 + 8g..
+      }
+    }
+  }
+  if (!ws_ok) return;
+  // the loads above are issued before the K loads (the loop's waits count on it)
+  __builtin_amdgcn_sched_barrier(0);
+
+  unsigned char* const scores = &lds[wave][0];  // tile t, query row n, key k at ((t * group + n) * 16 + k) * 2
+  unsigned char* const vstage = &lds[wave][kFusedScoreBytes];
+
+  // The (max, sum of e^(s - max)) of query row `row` over the keys [kb, ke)
+  // (kb a multiple of 16, at most kDecodeMaxTilesPerSplit tiles, inside the
+  // window of tc), formed as the scores pass forms a split's; with kKeep the
+  // scores go to the wave's LDS region.
+  auto split_stats = [&](auto keep, int kb, int ke, TableCache& tc) -> float2 {
+    constexpr bool kKeep = decltype(keep)::value;
+    const int last = ke - 1;
+    const int ntiles = (ke - kb + kTileKeys - 1) / kTileKeys;
+    const int nsteps = (ntiles + kPassStepTiles - 1) / kPassStepTiles;
+    auto issue = [&](v4u (&dst)[kPassStepTiles][2], int st) {
+#pragma unroll
+      for (int u = 0; u < kPassStepTiles; ++u) {
+        const int key0 = kb + (st * kPassStepTiles + u) * kTileKeys;
+        TileAddr<true, false> ta;
+        ta.init(a.geom, table, tlen, tc, key0);
+        const int rows = key0 <= last ? min(kTileKeys, ke - key0) : 0;
+        load_tile_slice(dst[u], kbytes + ta.base * (int64_t)sizeof(T), rows, row_bytes, lane_off);
+      }
+    };
+    v4u kq[kDepth][kPassStepTiles][2];
+    // in step order (the loop's waits count on it)
+    static_for<0, kDepth>([&](auto j) {
+      issue(kq[j], j);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    float run_m = kNegInf;
+    double run_l = 0.0;
+    // step st, whose loads are in slot j = st % kDepth
+    auto step = [&](auto jc, int st) {
+        constexpr int j = decltype(jc)::value;
+        v4u kt[kPassStepTiles][2];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          kt[u][0] = kq[j][u][0];
+          kt[u][1] = kq[j][u][1];
+        }
+        const int key0 = kb + st * kPassStepTiles * kTileKeys;
+        if (append && key0 <= last_key && last_key - key0 < kPassStepTiles * kTileKeys) {
+          // the appended key's row from registers (its slot may not hold it yet)
+#pragma unroll
+          for (int u = 0; u < kPassStepTiles; ++u) {
+            if (key0 + u * kTileKeys + row == last_key) {
+              kt[u][0] = __builtin_bit_cast(v4u, kn.v[0]);
+              kt[u][1] = __builtin_bit_cast(v4u, kn.v[1]);
+            }
+          }
+        }
+        v4f sc[kPassStepTiles];
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int jj = 0; jj < F::kVec; ++jj) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kt[u][jj]),
+                                                          __builtin_bit_cast(bf16x8_t, qf.v[jj]), acc, 0, 0, 0);
+          }
+          sc[u] = acc;
+        }
+        // the slot's next loads only once the MFMAs have read it, so the
+        // new values can take the old ones' registers (two live copies of a
+        // slot would make the compiler copy in-flight registers, and wait)
+        __builtin_amdgcn_sched_barrier(0);
+        issue(kq[j], st + kDepth);  // steps past the range read nothing
+        __builtin_amdgcn_sched_barrier(0);
+        float tmax = kNegInf;
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + u * kTileKeys + 4 * g + i;
+            sc[u][i] = key <= last ? scaled_score<T>(sc[u][i], a.scale) : kNegInf;
+            tmax = score_max(tmax, sc[u][i]);
+          }
+          if constexpr (kKeep) {
+            const int t = st * kPassStepTiles + u;
+            if (row_valid && t < ntiles) {
+              *reinterpret_cast<uint2*>(scores + (((t * group + row) * kTileKeys + 4 * g) << 1)) =
+                  uint2{pack_bf16x2(sc[u][0], sc[u][1]), pack_bf16x2(sc[u][2], sc[u][3])};
+            }
+          }
+        }
+        const float m_new = score_max(run_m, max_over_groups(tmax));
+        if (m_new != kNegInf) {
+          if (run_m != m_new) run_l *= (double)fast_exp2((run_m - m_new) * kLog2e);
+          const float nref = -m_new * kLog2e;
+          float e[kPassStepTiles];
+#pragma unroll
+          for (int u = 0; u < kPassStepTiles; ++u) {
+            float q4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q4[i] = fast_exp2(fmaf(sc[u][i], kLog2e, nref));
+            e[u] = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+          }
+          run_l += (double)(e[0] + e[1]);
+        }
+        run_m = m_new;
+    };
+    // whole rounds of kDepth steps (the loop's only exit is its condition,
+    // so the compiler counts the loads in flight across its back edge
+    // exactly), then the rest.  In the split's own pass the waves of the
+    // workgroup meet after every round: left alone, the oldest waves take
+    // most of the CU's memory issue and the youngest finish far behind,
+    // with the CU half idle meanwhile (all of them run the same rounds; the
+    // statistics of other splits, which only some waves may form, do not
+    // meet)
+    int s0 = 0;
+    for (; s0 + kDepth <= nsteps; s0 += kDepth) {
+      static_for<0, kDepth>([&](auto j) { step(j, s0 + j); });
+      if constexpr (kKeep) __builtin_amdgcn_s_barrier();
+    }
+    static_for<0, kDepth - 1>([&](auto j) {
+      if (s0 + j < nsteps) step(j, s0 + j);
+    });
+    double tl = run_l + __shfl_xor(run_l, 16);
+    tl = tl + __shfl_xor(tl, 32);
+    return make_float2(run_m, (float)tl);
+  };
+
+  // ---- K phase: this split's scores (kept) and (max, sum) ----
+  TableCache tc;
+  tc.load(table, tlen, key_begin >> a.geom.bs_shift);
+  const float2 own = split_stats(std::true_type{}, key_begin, key_end, tc);
+
+  // publish: the pairs are stored through to memory before the count moves
+  float* const ml = a.ws_ml + (w.first_item * a.q_heads + qh) * 2;  // this row's pair of the sequence's split 0
+  if (nsplit > 1) {
+    if (row_valid && g == 0) {
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(ml + w.split * a.q_heads * 2),
+                         (uint64_t)__float_as_uint(own.x) | ((uint64_t)__float_as_uint(own.y) << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    if (lane == 0) __hip_atomic_fetch_add(&ctl->pair[pair].count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // ---- V phase ----
+  const int ntiles = (key_end - key_begin + kTileKeys - 1) / kTileKeys;
+  const int nsteps = (ntiles + kPassStepTiles - 1) / kPassStepTiles;
+  const int last = key_end - 1;
+  auto issue_v = [&](v4u (&dst)[kPassStepTiles][2], int st) {
+#pragma unroll
+    for (int u = 0; u < kPassStepTiles; ++u) {
+      const int key0 = key_begin + (st * kPassStepTiles + u) * kTileKeys;
+      TileAddr<true, false> ta;
+      ta.init(a.geom, table, tlen, tc, key0);
+      const int rows = key0 <= last ? min(kTileKeys, key_end - key0) : 0;
+      load_tile_slice(dst[u], vbytes + ta.base * (int64_t)sizeof(T), rows, row_bytes, lane_off);
+    }
+  };
+  v4u vq[kDepth][kPassStepTiles][2];
+  static_for<0, kDepth>([&](auto j) {
+    issue_v(vq[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  // the row's (m, l) over every split of the sequence: lane group g takes
+  // splits g, g + 4, ... in order, then the groups combine (as in the P.V
+  // pass)
+  float m = kNegInf, l = 0.f;
+  auto combine = [&](float2 v) {
+    const float mn = score_max(m, v.x);
+    if (mn != kNegInf) l = fmaf(l, exp_ref(m - mn), v.y * exp_ref(v.x - mn));
+    m = mn;
+  };
+  if (nsplit == 1) {
+    if (g == 0) combine(row_valid ? own : make_float2(kNegInf, 0.f));
+  } else {
+    // the wave waits only for its own head's splits (a wave of the
+    // workgroup that is behind holds no other wave back)
+    int ready = 1;
+    if (lane == 0) ready = wait_count(&ctl->pair[pair].count, (uint32_t)nsplit, a.spin_limit) ? 1 : 0;
+    ready = __builtin_amdgcn_readfirstlane(ready);
+    if (ready) {
+      constexpr int kMlBatch = 8;
+      for (int64_t s0 = 0; s0 < nsplit; s0 += 4 * kMlBatch) {
+        float2 v[kMlBatch];
+#pragma unroll
+        for (int j = 0; j < kMlBatch; ++j) {
+          const int64_t sp = s0 + 4 * j + g;
+          if (row_valid && sp < nsplit) {
+            const uint64_t bits = __hip_atomic_load(reinterpret_cast<uint64_t*>(ml + sp * a.q_heads * 2),
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v[j] = make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+          } else {
+            v[j] = make_float2(kNegInf, 0.f);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kMlBatch; ++j) combine(v[j]);
+      }
+    } else {
+      // the other splits did not all arrive within the poll limit: form
+      // every split's pair from K here, combining them in the same order
+      if (lane == 0) __hip_atomic_fetch_add(&ctl->gave_up.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      TableCache tcs;
+      for (int64_t sp = 0; sp < nsplit; ++sp) {
+        const int kb = (int)sp * tps * kTileKeys;
+        const int ke = min(kb + tps * kTileKeys, seq_len);
+        tcs.load(table, tlen, kb >> a.geom.bs_shift);
+        const float2 v = split_stats(std::false_type{}, kb, ke, tcs);
+        if ((int)(sp & 3) == g) combine(row_valid ? v : make_float2(kNegInf, 0.f));
+      }
+      // nothing of the K loads in flight past here (their registers are
+      // free for the V phase without a wait per step)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
+  }
+  const float row_m = max_over_groups(m);
+  const float row_l = sum_over_groups(row_m == kNegInf ? 0.f : l * exp_ref(m - row_m));
+  const float row_r = 1.f / row_l;
+
+  v4f o[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) o[c] = v4f{0.f, 0.f, 0.f, 0.f};
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  typedef __attribute__((address_space(3))) unsigned char lds_u8;
+  lds_u8* const vstage_lds = (lds_u8*)vstage;
+  auto vstep = [&](auto jc, int st) {
+      constexpr int j = decltype(jc)::value;
+      v4u vt[kPassStepTiles][2];
+#pragma unroll
+      for (int u = 0; u < kPassStepTiles; ++u) {
+        vt[u][0] = vq[j][u][0];
+        vt[u][1] = vq[j][u][1];
+      }
+      const int key0 = key_begin + st * kPassStepTiles * kTileKeys;
+      if (append && key0 <= last_key && last_key - key0 < kPassStepTiles * kTileKeys) {
+#pragma unroll
+        for (int u = 0; u < kPassStepTiles; ++u) {
+          if (key0 + u * kTileKeys + row == last_key) {
+            vt[u][0] = __builtin_bit_cast(v4u, vn.v[0]);
+            vt[u][1] = __builtin_bit_cast(v4u, vn.v[1]);
+          }
+        }
+      }
+      // the step's V rows into the wave's stage (chunk 4jj + g of row `row`)
+#pragma unroll
+      for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          *reinterpret_cast<v4u*>(vstage + u * VT::kBytes + VT::chunk_offset(row, 4 * jj + g)) = vt[u][jj];
+        }
+      }
+      // the slot's next loads once its values are staged (as in the K phase)
+      __builtin_amdgcn_sched_barrier(0);
+      issue_v(vq[j], st + kDepth);
+      __builtin_amdgcn_sched_barrier(0);
+      // the lane's scores (keys 4g..4g+3 of both tiles) and the V^T operands
+      uint2 sv[kPassStepTiles];
+#pragma unroll
+      for (int u = 0; u < kPassStepTiles; ++u) {
+        const int t = min(st * kPassStepTiles + u, ntiles - 1);
+        sv[u] = *reinterpret_cast<const uint2*>(scores + (((t * group + row) * kTileKeys + 4 * g) << 1));
+      }
+      v4s vtr[kPassStepTiles][D / 16];
+#pragma unroll
+      for (int u = 0; u < kPassStepTiles; ++u) {
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          vtr[u][c] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4s*)(vstage_lds + u * VT::kBytes + VT::vt_offset(lane, 0, c)));
+        }
+      }
+      v4s pb[kPassStepTiles];
+#pragma unroll
+      for (int u = 0; u < kPassStepTiles; ++u) {
+        const uint32_t sw[2] = {sv[u].x, sv[u].y};
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = bf16_bits_to_f32((sw[i / 2] >> (16 * (i % 2))) & 0xffffu);
+          const int key = key0 + u * kTileKeys + 4 * g + i;
+          p[i] = (row_valid && key <= last) ? div_ref(exp_ref(x - row_m), row_l, row_r) : 0.f;
+        }
+        pb[u] = pack_bf16x4(p[0], p[1], p[2], p[3]);
+      }
+      const bf16x8_t pp = join_bf16x4(pb[0], pb[1]);
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(join_bf16x4(vtr[0][c], vtr[1][c]), pp, o[c], 0, 0, 0);
+      }
+  };
+  // whole rounds of kDepth steps, then the rest (as in the K phase, the
+  // waves meet after every round)
+  int s0 = 0;
+  for (; s0 + kDepth <= nsteps; s0 += kDepth) {
+    static_for<0, kDepth>([&](auto j) { vstep(j, s0 + j); });
+    __builtin_amdgcn_s_barrier();
+  }
+  static_for<0, kDepth - 1>([&](auto j) {
+    if (s0 + j < nsteps) vstep(j, s0 + j);
+  });
+
+  if (nsplit == 1) {
+    if (!row_valid) return;
+    T* dst = reinterpret_cast<T*>(a.out) + b * a.o_sb + qh * a.o_sh + 4 * g;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) store4<T>(dst + 16 * c, o[c][0], o[c][1], o[c][2], o[c][3]);
+    return;
+  }
+  // the split's share of each row, through to memory; the wave that counts
+  // the pair's last share sums them (in decode_merge_kernel<kSum>'s order)
+  // and starts the pair's counters over: every split of the pair has passed
+  // its wait by then (each counts its share after its wait)
+  if (row_valid) {
+    float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) store_agent4(dst + 16 * c, o[c][0], o[c][1], o[c][2], o[c][3]);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  uint32_t before = 0;
+  if (lane == 0) before = __hip_atomic_fetch_add(&ctl->pair[pair].done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  before = __builtin_amdgcn_readfirstlane(before);
+  if (before != (uint32_t)nsplit - 1u) return;
+  sum_rows<T, D, true, kFusedMaxGroup>(a.ws_o + (w.first_item * a.q_heads + h * group) * D, D, (int64_t)a.q_heads * D,
+                                      (int)nsplit, group, reinterpret_cast<T*>(a.out) + b * a.o_sb + h * group * a.o_sh,
+                                      a.o_sh);
+  if (lane == 0) {
+    __hip_atomic_store(&ctl->pair[pair].count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ctl->pair[pair].done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -4782,6 +5415,63 @@ void launch_decode_two_pass(const DecodeArgs& a, const DecodePlan& p, const Deco
   }
 }
 
+// The one-launch decode (decode_fused_kernel), process-wide switch
+// (nie_set_decode_fused), and the polls of its waits (nie_set_decode_fused_spin).
+std::atomic<int> g_decode_fused{1};
+std::atomic<int> g_fused_spin{kFusedSpinLimit};
+// Which path the calling thread's last decode call took (nie_decode_last_path).
+thread_local int g_decode_path = NIE_DECODE_PATH_NONE;
+
+// Resident decode_fused_kernel workgroups per CU (the runtime's occupancy
+// figure, or the LDS bound when it cannot be queried).
+template <int H>
+int fused_resident() {
+  static const int n = [] {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_fused_kernel<H>, H * kWave, 0) != hipSuccess ||
+        blocks < 1) {
+      (void)hipGetLastError();
+      blocks = kDecodeLdsBudget / (H * kFusedWaveLds) > 0 ? kDecodeLdsBudget / (H * kFusedWaveLds) : 1;
+    }
+    return blocks;
+  }();
+  return n;
+}
+
+int fused_resident_h(int heads) {
+  switch (heads) {
+    case 1: return fused_resident<1>();
+    case 2: return fused_resident<2>();
+    case 4: return fused_resident<4>();
+    default: return fused_resident<8>();
+  }
+}
+
+// Whether decode_fused_kernel runs a reference-rounding call: bf16 head_dim
+// 64 on whole-tile blocks, GQA groups of at most kFusedMaxGroup query heads
+// (the wave's score region), a counter per (sequence, KV head) in the
+// control region, and every work item the launch can hold (`live`, times
+// the head groups) resident at once.
+bool fused_fits(const CacheGeom& g, const DecodePlan& p, int64_t head_dim, int64_t q_heads, int64_t batch,
+                int64_t live) {
+  if (g_decode_fused.load(std::memory_order_relaxed) == 0) return false;
+  if (head_dim != kFusedDim || !uniform_tiles(g) || q_heads / g.kv_heads > kFusedMaxGroup) return false;
+  if (batch * g.kv_heads > kCtlPairs) return false;
+  const int64_t groups = g.kv_heads / p.heads;
+  return live * groups <= device_cus() * (int64_t)fused_resident_h(p.heads);
+}
+
+void launch_decode_fused(const DecodeArgs& a, const DecodePlan& p, const DecodeItems& items, hipStream_t stream) {
+  const int64_t n = items.count > 0 ? items.count : p.items;
+  const dim3 grid((unsigned)n, (unsigned)(a.geom.kv_heads / p.heads));
+  switch (p.heads) {
+    case 1: hipLaunchKernelGGL((decode_fused_kernel<1>), grid, dim3(kWave), 0, stream, a, items); break;
+    case 2: hipLaunchKernelGGL((decode_fused_kernel<2>), grid, dim3(2 * kWave), 0, stream, a, items); break;
+    case 4: hipLaunchKernelGGL((decode_fused_kernel<4>), grid, dim3(4 * kWave), 0, stream, a, items); break;
+    default: hipLaunchKernelGGL((decode_fused_kernel<8>), grid, dim3(8 * kWave), 0, stream, a, items); break;
+  }
+}
+
 template <typename T, int D, int NB, bool P2, int M>
 void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc, hipStream_t stream) {
   const dim3 grid((unsigned)(p.items * a.geom.kv_heads));
@@ -5296,7 +5986,7 @@ NIE_API int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64
   if (host_seq_lens != nullptr && !host_lens_ok(host_seq_lens, batch, max_seq_len, total_seq_len)) return 0;
   if (!tuned_attention(head_dim, q_heads, kv_heads)) return 0;  // the generic kernel needs no workspace
   const DecodePlan p = plan_decode(dtype, head_dim, kv_heads, block_size, batch, total_seq_len, host_seq_lens);
-  return decode_workspace_need(p, q_heads, head_dim, batch, total_seq_len, two_pass(dtype));
+  return kCtlBytes + decode_workspace_need(p, q_heads, head_dim, batch, total_seq_len, two_pass(dtype));
 }
 
 NIE_API int nie_set_attention_rounding(int mode) {
@@ -5308,6 +5998,24 @@ NIE_API int nie_set_attention_rounding(int mode) {
 }
 
 NIE_API int nie_attention_rounding(void) { return g_rounding.load(std::memory_order_relaxed); }
+
+NIE_API int nie_set_decode_fused(int on) {
+  if (on != 0 && on != 1) return fail(NIE_EINVAL, "nie_set_decode_fused takes 0 or 1");
+  g_decode_fused.store(on, std::memory_order_relaxed);
+  return NIE_OK;
+}
+
+NIE_API int nie_decode_fused(void) { return g_decode_fused.load(std::memory_order_relaxed); }
+
+NIE_API int nie_set_decode_fused_spin(int polls) {
+  if (polls < 0) return fail(NIE_EINVAL, "nie_set_decode_fused_spin takes a non-negative poll count");
+  g_fused_spin.store(polls, std::memory_order_relaxed);
+  return NIE_OK;
+}
+
+NIE_API int64_t nie_workspace_control_bytes(void) { return kCtlBytes; }
+
+NIE_API int nie_decode_last_path(void) { return g_decode_path; }
 
 namespace {
 
@@ -5330,6 +6038,7 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
                       int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
                       const int32_t* host_seq_lens, const DecodeAppend& append, void* stream,
                       bool static_scratch = false, const void* device_plan = nullptr) {
+  g_decode_path = NIE_DECODE_PATH_NONE;
   int rc = check_dtype(dtype);
   if (rc) return rc;
   rc = check_geometry(num_layers, layer_index, num_blocks, block_size, kv_heads, head_dim);
@@ -5414,6 +6123,7 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
     ga.rope_cos = append.k_new != nullptr ? append.cos_table : nullptr;
     ga.rope_sin = append.k_new != nullptr ? append.sin_table : nullptr;
     ga.rope_rows = append.table_rows;
+    g_decode_path = NIE_DECODE_PATH_GENERIC;
     return generic_attention(dtype, ga, s);
   }
   if (!check_aligned(q, q_stride_b, q_stride_h, es) || !check_aligned(out, out_stride_b, out_stride_h, es) ||
@@ -5446,7 +6156,8 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   // the two-pass rounding always needs the workspace (its score buffer and
   // the (max, sum) pairs of every split, one split included)
   const bool two = two_pass(dtype);
-  const int64_t need = decode_workspace_need(plan, q_heads, head_dim, batch, total_seq_len, two);
+  // the workspace: the control region, then the partials (and scores)
+  const int64_t need = kCtlBytes + decode_workspace_need(plan, q_heads, head_dim, batch, total_seq_len, two);
   if ((may_split || two) && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     if (static_scratch) {
       return fail(NIE_EINVAL,
@@ -5479,12 +6190,14 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   a.o_sb = out_stride_b;
   a.o_sh = out_stride_h;
   const bool have_ws = workspace != nullptr && workspace_bytes >= need;
-  a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
+  unsigned char* const body = have_ws ? reinterpret_cast<unsigned char*>(workspace) + kCtlBytes : nullptr;
+  a.ctl = have_ws ? reinterpret_cast<DecodeCtl*>(workspace) : nullptr;
+  a.spin_limit = g_fused_spin.load(std::memory_order_relaxed);
+  a.ws_o = have_ws ? reinterpret_cast<float*>(body) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + items * q_heads * head_dim : nullptr;
   a.ws_items = have_ws ? items : 0;
   if (two && have_ws) {
-    a.ws_s = reinterpret_cast<uint16_t*>(reinterpret_cast<unsigned char*>(workspace) +
-                                         decode_ws_partials(plan, q_heads, head_dim));
+    a.ws_s = reinterpret_cast<uint16_t*>(body + decode_ws_partials(plan, q_heads, head_dim));
     a.ws_s_keys = decode_score_keys(plan, batch, total_seq_len);
   }
   a.k_new = append.k_new;
@@ -5500,12 +6213,28 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
   fill_decode_items(plan, host_seq_lens, batch, &work);
   hipStream_t s = (hipStream_t)stream;
   if (two) {
-    if (head_dim == 64) launch_decode_two_pass<bf16_t, 64>(a, plan, work, s, may_split);
-    else launch_decode_two_pass<bf16_t, 128>(a, plan, work, s, may_split);
+    // the most work items the launch can hold: the host plan's, or (the
+    // split length chosen on the device) what decode_device_tps allows,
+    // and with a device-resident plan whatever that table may hold
+    int64_t live = work.count > 0 ? work.count
+                   : plan.tps > 0 ? plan.items
+                                  : std::max(plan.slots - 1,
+                                             decode_max_items(batch, total_seq_len, kDecodeMaxTilesPerSplit));
+    if (device_plan != nullptr) live = std::max(live, (int64_t)kMaxDecodeItems);
+    if (have_ws && fused_fits(a.geom, plan, head_dim, q_heads, batch, live)) {
+      g_decode_path = NIE_DECODE_PATH_FUSED;
+      launch_decode_fused(a, plan, work, s);
+    } else {
+      g_decode_path = NIE_DECODE_PATH_PASSES;
+      if (head_dim == 64) launch_decode_two_pass<bf16_t, 64>(a, plan, work, s, may_split);
+      else launch_decode_two_pass<bf16_t, 128>(a, plan, work, s, may_split);
+    }
   } else if (dtype == NIE_DTYPE_BF16) {
+    g_decode_path = NIE_DECODE_PATH_ONE_PASS;
     if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, work, s, may_split);
     else launch_decode<bf16_t, 128>(a, plan, work, s, may_split);
   } else {
+    g_decode_path = NIE_DECODE_PATH_ONE_PASS;
     if (head_dim == 64) launch_decode<float, 64>(a, plan, work, s, may_split);
     else launch_decode<float, 128>(a, plan, work, s, may_split);
   }
@@ -5720,7 +6449,7 @@ NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t tot
   // slots are needed (the query has no dtype: with the reference rounding it
   // sizes for bf16, which an fp32 call can use too)
   if (!p.split && g_rounding.load(std::memory_order_relaxed) != NIE_ROUND_REFERENCE) return 0;
-  return p.items * kv_heads * p.rows * (head_dim + 2) * (int64_t)sizeof(float);
+  return kCtlBytes + p.items * kv_heads * p.rows * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
 NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int64_t q_stride_h,
@@ -5801,7 +6530,9 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   // the reference rounding always needs the workspace: every item's
   // (max, sum) slots, one piece included
   const bool two = two_pass(dtype);
-  const int64_t need = plan.items * kv_heads * plan.rows * (head_dim + 2) * (int64_t)sizeof(float);
+  // the workspace: the control region (which prefill leaves alone), then
+  // the partials
+  const int64_t need = kCtlBytes + plan.items * kv_heads * plan.rows * (head_dim + 2) * (int64_t)sizeof(float);
   if ((may_split || two) && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,
                 (long long)workspace_bytes);
@@ -5828,7 +6559,7 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   a.o_st = out_stride_t;
   a.o_sh = out_stride_h;
   const bool have_ws = (may_split || two) && workspace != nullptr && workspace_bytes >= need;
-  a.ws_o = have_ws ? reinterpret_cast<float*>(workspace) : nullptr;
+  a.ws_o = have_ws ? reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) + kCtlBytes) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + plan.items * kv_heads * plan.rows * head_dim : nullptr;
   a.ws_items = have_ws ? plan.items : 0;
   PrefillMergeJobs jobs;

@@ -62,6 +62,11 @@ EXPORTED_SYMBOLS = (
     "nie_rms_norm_linear_rows",
     "nie_set_attention_rounding",
     "nie_attention_rounding",
+    "nie_set_decode_fused",
+    "nie_decode_fused",
+    "nie_set_decode_fused_spin",
+    "nie_workspace_control_bytes",
+    "nie_decode_last_path",
     "nie_paged_decode_workspace_bytes",
     "nie_paged_decode",
     "nie_paged_decode_append",
@@ -122,6 +127,11 @@ _SIGNATURES = {
     ),
     "nie_set_attention_rounding": (_i32, [_i32]),
     "nie_attention_rounding": (_i32, []),
+    "nie_set_decode_fused": (_i32, [_i32]),
+    "nie_decode_fused": (_i32, []),
+    "nie_set_decode_fused_spin": (_i32, [_i32]),
+    "nie_workspace_control_bytes": (_i64, []),
+    "nie_decode_last_path": (_i32, []),
     "nie_paged_decode_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "nie_paged_decode": (
         _i32,
@@ -222,7 +232,9 @@ _lib_lock = threading.Lock()
 
 # Split-partial workspaces of the decode and prefill calls, one per (device,
 # stream), grown as needed and reused: calls on one stream are ordered, so
-# they can share a buffer; calls on different streams cannot.
+# they can share a buffer; calls on different streams cannot.  Each starts
+# zeroed: its first workspace_control_bytes() bytes are the library's
+# control region, which must be zero before first use (calls leave it zero).
 _decode_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _workspace_lock = threading.Lock()
 
@@ -233,7 +245,7 @@ def _decode_workspace(device: torch.device, stream: int, nbytes: int) -> torch.T
         ws = _decode_workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
             size = max(nbytes, 1 << 20, 0 if ws is None else 2 * ws.numel())
-            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
             _decode_workspaces[key] = ws
     return ws
 
@@ -322,6 +334,39 @@ def attention_rounding() -> str:
     """The rounding mode of ``set_attention_rounding``."""
     code = load_library().nie_attention_rounding()
     return next(name for name, value in ROUNDING_MODES.items() if value == code)
+
+
+#: Paths of a decode call (nie_decode_last_path).
+DECODE_PATHS = {0: "none", 1: "one_pass", 2: "passes", 3: "fused", 4: "generic"}
+
+
+def set_decode_fused(on: bool) -> None:
+    """Whether reference-rounding bf16 decode calls whose shape allows it run
+    as one kernel (each split keeps its scores on chip and the splits exchange
+    only their (max, sum) pairs) instead of the scores and P.V passes; the
+    outputs are bit-identical either way.  On by default; process-wide."""
+    _check(load_library().nie_set_decode_fused(1 if on else 0), "nie_set_decode_fused")
+
+
+def decode_fused() -> bool:
+    return bool(load_library().nie_decode_fused())
+
+
+def set_decode_fused_spin(polls: int) -> None:
+    """Polls a split of the one-launch decode makes while waiting for the
+    other splits of its sequence before it forms their statistics itself (0:
+    give up at once, the path tests use to run that code)."""
+    _check(load_library().nie_set_decode_fused_spin(int(polls)), "nie_set_decode_fused_spin")
+
+
+def workspace_control_bytes() -> int:
+    """Bytes at the start of a decode or prefill workspace that hold the control region."""
+    return int(load_library().nie_workspace_control_bytes())
+
+
+def decode_last_path() -> str:
+    """Which kernels this thread's last decode call ran ("fused", "passes", ...)."""
+    return DECODE_PATHS[load_library().nie_decode_last_path()]
 
 
 def _check(rc: int, what: str) -> None:

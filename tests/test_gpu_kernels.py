@@ -267,10 +267,18 @@ def test_decode_ignores_garbage_past_length():
     assert (got.float() - want.float()).abs().max().item() <= 2e-2
 
 
+def _control_regions_zero() -> bool:
+    """Every cached workspace's control region (the one-launch decode's counters) is zero."""
+    ctl = _native.workspace_control_bytes()
+    # the region's last 128-byte line only counts waits that gave up
+    return all(int(ws[: ctl - 128].count_nonzero().item()) == 0 for ws in _native._decode_workspaces.values())
+
+
 def test_decode_tolerates_stale_workspace():
-    """The decode workspace needs no clearing: a workspace full of garbage
-    (random bytes, all ones, small integers), or one just overwritten by a
-    prefill call's partials, gives correct output."""
+    """Past its control region the decode workspace needs no clearing: a
+    workspace full of garbage there (random bytes, all ones, small
+    integers), or one just overwritten by a prefill call's partials, gives
+    correct output, and every call leaves the control region zero."""
     _log("decode stale workspace")
     wl = workloads.decode_ragged(seed=5)
     kc, vc = wl.pool(torch.bfloat16)
@@ -287,6 +295,8 @@ def test_decode_tolerates_stale_workspace():
         return (out.cpu().float() - want.float()).abs().max().item()
 
     run()  # creates the cached workspace
+    assert _control_regions_zero()
+    ctl = _native.workspace_control_bytes()
     gen = torch.Generator(device=DEV).manual_seed(0)
     fills = {
         "random": lambda w: w.copy_(torch.randint(0, 256, w.shape, generator=gen, device=DEV, dtype=torch.uint8)),
@@ -297,16 +307,19 @@ def test_decode_tolerates_stale_workspace():
     for name, fill in fills.items():
         with torch.inference_mode():  # cached workspaces may have been made under inference mode
             for ws in _native._decode_workspaces.values():
-                fill(ws)
+                fill(ws[ctl:])
         err = run()
         _log(f"  {name}: max_abs_err={err:.3e}")
         assert err <= 2e-2
+        assert _control_regions_zero()
     # a split-key prefill writes its partials over the same workspace
     pwl = workloads.ragged([3000, 40], [64, 1], seed=11)
     _prefill_case(pwl, torch.bfloat16)
+    assert _control_regions_zero()
     err = run()
     _log(f"  after prefill: max_abs_err={err:.3e}")
     assert err <= 2e-2
+    assert _control_regions_zero()
 
 
 def test_decode_workspace_reuse_across_calls():

@@ -368,10 +368,13 @@ def test_attention_rounding_mode_switch():
 
 def test_library_workspace_queries(fast_rounding):
     lib = _native.load_library()
+    # every workspace starts with the 256 KiB control region
+    ctl = _native.workspace_control_bytes()
+    assert ctl == 256 * 1024
     # decode partials: items * q_heads * (head_dim + 2) floats, items bounded by the split count
-    small = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710, None)
+    small = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710, None) - ctl
     assert small > 0 and small % (32 * 66 * 4) == 0
-    big = lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None)
+    big = lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None) - ctl
     assert big >= small
     # at most 128 tiles of 16 keys per split (the block-table window): at least 16 * ceil(1850 / 128) items
     assert big >= 16 * 15 * 32 * 66 * 4
@@ -379,7 +382,7 @@ def test_library_workspace_queries(fast_rounding):
     # device, (tiles + 128 per sequence) * 16 slots; fp32 calls do not round probabilities (no scores)
     _native.set_attention_rounding("reference")
     ref = lib.nie_paged_decode_workspace_bytes(1, 4, 32, 8, 64, 16, 500, 710, None)
-    assert ref == -(-small // 256) * 256 + (-(-710 // 16) + 4 * 128) * 16 * 32 * 2
+    assert ref == ctl + -(-small // 256) * 256 + (-(-710 // 16) + 4 * 128) * 16 * 32 * 2
     assert (lib.nie_paged_decode_workspace_bytes(0, 4, 32, 8, 64, 16, 500, 710, None)
             == lib.nie_paged_decode_workspace_bytes(0, 4, 32, 8, 64, 16, 500, 710, None))
     _native.set_attention_rounding("fast")
@@ -408,14 +411,16 @@ def test_library_decode_plan_from_host_lengths():
         lens = np.asarray(lens, dtype=np.int32)
         return lib.nie_paged_decode_workspace_bytes(1, len(lens), 32, 8, 64, 16, mx, total, lens.ctypes.data)
 
-    # reference rounding: the partials, then a bf16 score per key slot (256 items x 116 tiles x 16) and head
-    assert query([29600] * 16, 29600, 16 * 29600) == 256 * 32 * 66 * 4 + 256 * 116 * 16 * 32 * 2
+    # reference rounding: the control region, the partials, then a bf16 score per key slot (256 items x
+    # 116 tiles x 16) and head
+    ctl = _native.workspace_control_bytes()
+    assert query([29600] * 16, 29600, 16 * 29600) == ctl + 256 * 32 * 66 * 4 + 256 * 116 * 16 * 32 * 2
     _native.set_attention_rounding("fast")
     try:
-        assert query([29600] * 16, 29600, 16 * 29600) == 256 * 32 * 66 * 4
+        assert query([29600] * 16, 29600, 16 * 29600) == ctl + 256 * 32 * 66 * 4
         # the bound-based plan (124-tile splits: 240 items) sizes for an upper bound on its items
         assert (lib.nie_paged_decode_workspace_bytes(1, 16, 32, 8, 64, 16, 29600, 16 * 29600, None)
-                >= 240 * 32 * 66 * 4)
+                >= ctl + 240 * 32 * 66 * 4)
     finally:
         _native.set_attention_rounding("reference")
     assert query([29600] * 16, 29600, 16 * 29600 - 1) == 0  # sum does not match
@@ -437,15 +442,16 @@ def test_library_prefill_plan_from_host_lengths():
 
     # four 128-token chunks on empty contexts: at most 8 key tiles per query tile, never split, so the
     # one-pass rounding needs no workspace; the reference rounding keeps every item's (max, sum) slots
-    # in the same layout (16 items here: 4 query tiles of 32 tokens per chunk)
-    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 16 * 8 * 128 * 66 * 4
+    # in the same layout (16 items here: 4 query tiles of 32 tokens per chunk), after the control region
+    ctl = _native.workspace_control_bytes()
+    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == ctl + 16 * 8 * 128 * 66 * 4
     _native.set_attention_rounding("fast")
     try:
         assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 0
     finally:
         _native.set_attention_rounding("reference")
     # the mixed step's chunks (contexts 0, 384, 1024, 4000): the long context is split
-    mixed = query([0, 128, 256, 384, 512], [0, 384, 1024, 4000], 512, 128, 4128)
+    mixed = query([0, 128, 256, 384, 512], [0, 384, 1024, 4000], 512, 128, 4128) - ctl
     assert mixed > 0 and mixed % (8 * 128 * 66 * 4) == 0
     # lengths that do not match the sizes of the call
     assert query([0, 128, 256, 384, 500], [0, 384, 1024, 4000], 512, 128, 4128) == 0

@@ -60,7 +60,7 @@ def _call(lib, noalloc: bool, dtype, q, k_new, v_new, kc, vc, tables, lens_dev, 
         return lib.nie_paged_decode_append_noalloc(*common, host_ptr, stream)
     ws_bytes = lib.nie_paged_decode_workspace_bytes(code, batch, q_heads, kv_heads, head_dim, block_size, max(lens),
                                                     sum(lens), host_ptr)
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(max(ws_bytes, 16), dtype=torch.uint8, device=DEV)  # the control region starts zeroed
     rc = lib.nie_paged_decode_append(*common, ws.data_ptr(), ws.numel(), host_ptr, stream)
     torch.cuda.synchronize()
     return rc
