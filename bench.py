@@ -40,12 +40,12 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the value leg's call, per rounding mode
 TRAFFIC_PROFILES = {
-    "reference": os.path.join("profiles", "decode_pass_kernel__decode_step_b16_lognormal__hbm_traffic.json"),
+    "reference": os.path.join("profiles", "decode_fused_kernel__decode_step_b16_lognormal__hbm_traffic.json"),
     "fast": os.path.join("profiles", "paged_decode_kernel__decode_step_b16_lognormal__hbm_traffic.json"),
 }
 # the kernels of one nie_paged_decode_append call, per rounding mode
 DECODE_CALL_KERNELS = {
-    "reference": "decode_pass_kernel (scores pass) + decode_pass_kernel (P.V pass) + decode_merge_kernel (sum)",
+    "reference": "decode_fused_kernel (one launch: K phase, (max, sum) exchange between splits, P.V phase, last split sums)",
     "fast": "paged_decode_kernel + decode_merge_kernel",
 }
 
