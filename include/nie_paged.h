@@ -29,9 +29,12 @@
  *    validate tables on the host (the Python layer does).
  *  - Every call is asynchronous on `stream` (a hipStream_t; NULL = default
  *    stream).  The library never allocates or frees device memory: scratch
- *    space is the caller's `workspace`, sized by the *_workspace_bytes query;
- *    it needs no initialisation.  Calls that overlap in time (different
- *    streams) need different workspaces.
+ *    space is the caller's `workspace`, sized by the *_workspace_bytes query.
+ *    A decode or prefill workspace starts with a control region
+ *    (nie_workspace_control_bytes()) that must be zero before the
+ *    workspace's first call and that every call leaves zero; past it the
+ *    workspace needs no initialisation.  Calls that overlap in time
+ *    (different streams) need different workspaces.
  *  - Return value: NIE_OK, or a negative NIE_E* code; nie_last_error() then
  *    holds a message for the calling thread.
  */
@@ -285,13 +288,14 @@ int nie_attention_rounding(void);
  * The one-launch reference-rounding decode.  With the reference rounding, a
  * bf16 decode call whose head_dim is 64, whose block_size is a power of two
  * of at least 16, whose GQA group has at most 4 query heads and whose work
- * items can all be resident on the GPU at once runs as one kernel (each
- * split keeps its scores on chip; the splits exchange only their (max, sum)
- * pairs, through the workspace's control region) plus the sum of the split
- * partials, instead of the two passes over the keys.  Its outputs are
- * bit-identical to the two passes'.  nie_set_decode_fused(0) turns it off
- * for calls issued after it in the whole process (1, the default, on);
- * NIE_EINVAL for other values.
+ * items can all be resident on the GPU at once runs as one kernel instead of
+ * the two pass launches and the sum of their split partials: each split
+ * keeps its scores on chip, the splits exchange only their (max, sum) pairs
+ * and output shares, through counters in the workspace's control region,
+ * and the split that finishes last sums the shares.  nie_set_decode_fused(0)
+ * turns it off for calls issued after it in the whole process (1, the
+ * default, on); the pass launches then run the same plan, so both give the
+ * same bits.  NIE_EINVAL for other values.
  * No counterpart in the reference (an execution strategy of its decode
  * attention, layers/paged_attention.py:88-116).
  */
@@ -332,9 +336,11 @@ int nie_decode_last_path(void);
  * have maximum max_seq_len and sum total_seq_len, and the same optional
  * host copy of the lengths as the call.  The split of the work depends on
  * all of them, so query with the values of the call.
- * Layout: fp32 split partials (O rows, then (max, sum) pairs); with the
- * reference rounding (bf16) also the bf16 scores of every key of the call.
- * The pointer must be 16-byte aligned.  Returns 0 for invalid arguments.
+ * Layout: the control region (nie_workspace_control_bytes(); zero before
+ * the workspace's first call, left zero by every call), then fp32 split
+ * partials (O rows, then (max, sum) pairs); with the reference rounding
+ * (bf16) also the bf16 scores of every key of the call.  The pointer must
+ * be 16-byte aligned.  Returns 0 for invalid arguments.
  */
 int64_t nie_paged_decode_workspace_bytes(int dtype, int64_t batch, int64_t q_heads,
                                          int64_t kv_heads, int64_t head_dim,
@@ -513,7 +519,9 @@ int nie_paged_decode_append_noalloc(int dtype,
  * sequences, total and maximum query length, maximum context+query length,
  * and the same optional host copies of cu_seqlens_q / context_lens as the
  * call, which change the launch plan).  Returns 0 when no workspace is
- * needed or the arguments are invalid.
+ * needed or the arguments are invalid.  A workspace starts with the
+ * control region (nie_workspace_control_bytes(), which prefill leaves
+ * alone), so one buffer can serve decode and prefill calls in turn.
  */
 int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t total_query_tokens,
                                            int64_t max_query_len, int64_t max_seq_len,
