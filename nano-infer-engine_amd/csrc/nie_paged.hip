@@ -4328,12 +4328,16 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
           const float m_new = score_max(run_m[nb], max_over_groups(lm));
           if (m_new != kNegInf) {
             if (run_m[nb] != m_new) run_l[nb] *= (double)fast_exp2((run_m[nb] - m_new) * score_f * kLog2e);
+            // e^(s - m) as 2^(s c - m c), one fma per score (as the decode
+            // kernels form their sums)
+            const float ec = score_f * kLog2e;
+            const float nref = -m_new * ec;
             float e[kSub];
 #pragma unroll
             for (int t = 0; t < kSub; ++t) {
               float q4[4];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) q4[i] = fast_exp2((p[nb][t][i] - m_new) * score_f * kLog2e);
+              for (int i = 0; i < 4; ++i) q4[i] = fast_exp2(fmaf(p[nb][t][i], ec, nref));
               e[t] = (q4[0] + q4[1]) + (q4[2] + q4[3]);
             }
             run_l[nb] += (double)((e[0] + e[1]) + (e[2] + e[3]));
