@@ -295,7 +295,15 @@ int nie_attention_rounding(void);
  * and the split that finishes last sums the shares.  nie_set_decode_fused(0)
  * turns it off for calls issued after it in the whole process (1, the
  * default, on); the pass launches then run the same plan, so both give the
- * same bits.  NIE_EINVAL for other values.
+ * same bits.  The switch also covers the one-pass rounding (fp32, and bf16
+ * with NIE_ROUND_FAST): there, when a call splits its sequences' keys, the
+ * split of a (sequence, KV head) that finishes last merges the split
+ * partials inside the decode kernel (a counter per pair in the control
+ * region, up to 2047 pairs) instead of a separate merge launch, in the
+ * merge launch's order (the same bits), in calls of at most a quarter of
+ * the CUs' workgroups (larger calls keep the merge launch, which costs them
+ * less); 2 does so in calls of every size (as 1 otherwise).  NIE_EINVAL for
+ * other values.
  * No counterpart in the reference (an execution strategy of its decode
  * attention, layers/paged_attention.py:88-116).
  */
@@ -324,10 +332,11 @@ int64_t nie_workspace_control_bytes(void);
 
 /* Which kernels the calling thread's last nie_paged_decode* call ran. */
 #define NIE_DECODE_PATH_NONE 0     /* no call yet, or it failed before launching */
-#define NIE_DECODE_PATH_ONE_PASS 1 /* fp32, or bf16 with NIE_ROUND_FAST */
+#define NIE_DECODE_PATH_ONE_PASS 1 /* fp32, or bf16 with NIE_ROUND_FAST (merge launch when split) */
 #define NIE_DECODE_PATH_PASSES 2   /* reference rounding: scores pass, P.V pass, sum */
 #define NIE_DECODE_PATH_FUSED 3    /* reference rounding: the one-launch decode, sum */
 #define NIE_DECODE_PATH_GENERIC 4  /* shapes outside the MFMA kernels */
+#define NIE_DECODE_PATH_ONE_PASS_MERGED 5 /* one pass, split, merged by the last split: one launch */
 int nie_decode_last_path(void);
 
 /*

@@ -963,6 +963,9 @@ struct DecodeArgs {
   // itself
   DecodeCtl* ctl = nullptr;
   int32_t spin_limit = 0;
+  // One-pass rounding: the split that finishes last merges the partials of
+  // its (sequence, KV head), counted on ctl's counters (no merge launch)
+  int32_t merge_last = 0;
 };
 
 // Work items of a decode call planned from host copies of the lengths,
@@ -1892,6 +1895,97 @@ __device__ __forceinline__ void merge_row(const float* po, int64_t po_stride, co
   }
 }
 
+// merge_row over up to kRows rows at once (row n's split s at po + n *
+// row_stride + s * po_stride and ml + n * ml_row_stride + s * ml_stride,
+// its output at out + n * out_stride), reading partials that other
+// workgroups of the running launch stored with agent-scope stores: every
+// row's loads of a batch are issued before any is used, and each row is
+// merged in merge_row's order (the same bits).
+template <typename T, int D, int kRows>
+__device__ __forceinline__ void merge_rows_agent(const float* po, int64_t row_stride, int64_t po_stride, const float* ml,
+                                                 int64_t ml_row_stride, int64_t ml_stride, int nsplit, int rows,
+                                                 T* out, int64_t out_stride) {
+  constexpr int kLanesPerSplit = D / 4;
+  constexpr int kSplitsPerPass = kWave / kLanesPerSplit;
+  constexpr int kPasses = 8;
+  constexpr int kBatch = kPasses * kSplitsPerPass;
+  static_assert(kBatch <= kWave, "one (max, sum) pair per lane");
+  const int lane = lane_id();
+  const int sub = lane / kLanesPerSplit;
+  const int chunk = lane % kLanesPerSplit;
+  po += 4 * chunk;
+  float run_max[kRows], denom[kRows];
+  float4 acc[kRows];
+#pragma unroll
+  for (int n = 0; n < kRows; ++n) {
+    run_max[n] = kNegInf;
+    denom[n] = 0.f;
+    acc[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+    const int count = min(kBatch, nsplit - s0);
+    float4 v[kRows][kPasses];
+    float2 mls[kRows];
+#pragma unroll
+    for (int n = 0; n < kRows; ++n) {
+#pragma unroll
+      for (int p = 0; p < kPasses; ++p) {
+        const int sp = p * kSplitsPerPass + sub;
+        v[n][p] = (n < rows && sp < count) ? load_agent4(po + n * row_stride + (s0 + sp) * po_stride)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      if (n < rows && lane < count) {
+        const uint64_t bits = __hip_atomic_load(
+            reinterpret_cast<const uint64_t*>(ml + n * ml_row_stride + (s0 + lane) * ml_stride), __ATOMIC_RELAXED,
+            __HIP_MEMORY_SCOPE_AGENT);
+        mls[n] = make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+      } else {
+        mls[n] = make_float2(kNegInf, 0.f);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < kRows; ++n) {
+      float bmax = mls[n].x;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off));
+      const float new_max = fmaxf(run_max[n], bmax);
+      const float keep = run_max[n] == kNegInf ? 0.f : exp2f((run_max[n] - new_max) * kLog2e);
+      const float w = mls[n].x == kNegInf ? 0.f : exp2f((mls[n].x - new_max) * kLog2e);
+      float dsum = w * mls[n].y;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
+      denom[n] = denom[n] * keep + dsum;
+      acc[n].x *= keep;
+      acc[n].y *= keep;
+      acc[n].z *= keep;
+      acc[n].w *= keep;
+#pragma unroll
+      for (int p = 0; p < kPasses; ++p) {
+        const float ws = __shfl(w, p * kSplitsPerPass + sub);
+        acc[n].x += ws * v[n][p].x;
+        acc[n].y += ws * v[n][p].y;
+        acc[n].z += ws * v[n][p].z;
+        acc[n].w += ws * v[n][p].w;
+      }
+      run_max[n] = new_max;
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < kRows; ++n) {
+#pragma unroll
+    for (int off = kLanesPerSplit; off < kWave; off <<= 1) {
+      acc[n].x += __shfl_xor(acc[n].x, off);
+      acc[n].y += __shfl_xor(acc[n].y, off);
+      acc[n].z += __shfl_xor(acc[n].z, off);
+      acc[n].w += __shfl_xor(acc[n].w, off);
+    }
+    if (sub == 0 && n < rows) {
+      const float inv = 1.f / denom[n];
+      store4<T>(out + n * out_stride + 4 * chunk, acc[n].x * inv, acc[n].y * inv, acc[n].z * inv, acc[n].w * inv);
+    }
+  }
+}
+
 // Heads per decode workgroup: as many as fill a 1 KiB row slice, capped by
 // the largest power of two dividing kv_heads (so every wave has a head).
 template <typename T, int D>
@@ -2224,9 +2318,44 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
     return;
   }
   // Split-K: store this split's partial (unnormalised O, running max, sum)
-  // for the merge kernel.  The bound keeps inconsistent length hints from
-  // writing outside the workspace.
+  // for the merge.  The bound keeps inconsistent length hints from writing
+  // outside the workspace.
   const int64_t item = first_item + split;
+  if (a.merge_last) {
+    // Through to memory (agent scope), then counted on the (sequence, KV
+    // head) counter; the wave that counts the last split merges every
+    // split's partial of its query heads, in decode_merge_kernel's order,
+    // and starts the counter over.  The bound holds for all splits of a
+    // sequence or for none, so either every split counts or none does.
+    if (a.ws_o == nullptr || first_item + nsplit > a.ws_items) return;
+    if (row_valid) {
+      float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) store_agent4(dst + 16 * c, st.o[c][0], st.o[c][1], st.o[c][2], st.o[c][3]);
+      if (g == 0) {
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(a.ws_ml + (item * a.q_heads + qh) * 2),
+                           (uint64_t)__float_as_uint(st.m) | ((uint64_t)__float_as_uint(lsum) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    const int64_t pair = b * a.geom.kv_heads + h;
+    uint32_t before = 0;
+    if (lane == 0) {
+      before = __hip_atomic_fetch_add(&a.ctl->pair[pair].done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    before = __builtin_amdgcn_readfirstlane(before);
+    if (before != (uint32_t)nsplit - 1u) return;
+    const int qh0 = h * a.group;
+    for (int r0 = 0; r0 < a.group; r0 += 2) {
+      merge_rows_agent<T, D, 2>(a.ws_o + (first_item * a.q_heads + qh0 + r0) * D, D, (int64_t)a.q_heads * D,
+                                a.ws_ml + (first_item * a.q_heads + qh0 + r0) * 2, 2, (int64_t)a.q_heads * 2,
+                                (int)nsplit, min(2, a.group - r0),
+                                reinterpret_cast<T*>(a.out) + b * a.o_sb + (qh0 + r0) * a.o_sh, a.o_sh);
+    }
+    if (lane == 0) __hip_atomic_store(&a.ctl->pair[pair].done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   if (!row_valid || a.ws_o == nullptr || item >= a.ws_items) return;
   float* dst = a.ws_o + (item * a.q_heads + qh) * D + 4 * g;
 #pragma unroll
@@ -6004,7 +6133,7 @@ NIE_API int nie_set_attention_rounding(int mode) {
 NIE_API int nie_attention_rounding(void) { return g_rounding.load(std::memory_order_relaxed); }
 
 NIE_API int nie_set_decode_fused(int on) {
-  if (on != 0 && on != 1) return fail(NIE_EINVAL, "nie_set_decode_fused takes 0 or 1");
+  if (on < 0 || on > 2) return fail(NIE_EINVAL, "nie_set_decode_fused takes 0, 1 or 2");
   g_decode_fused.store(on, std::memory_order_relaxed);
   return NIE_OK;
 }
@@ -6233,14 +6362,29 @@ int paged_decode_call(int dtype, const void* q, int64_t q_stride_b, int64_t q_st
       if (head_dim == 64) launch_decode_two_pass<bf16_t, 64>(a, plan, work, s, may_split);
       else launch_decode_two_pass<bf16_t, 128>(a, plan, work, s, may_split);
     }
-  } else if (dtype == NIE_DTYPE_BF16) {
-    g_decode_path = NIE_DECODE_PATH_ONE_PASS;
-    if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, work, s, may_split);
-    else launch_decode<bf16_t, 128>(a, plan, work, s, may_split);
   } else {
-    g_decode_path = NIE_DECODE_PATH_ONE_PASS;
-    if (head_dim == 64) launch_decode<float, 64>(a, plan, work, s, may_split);
-    else launch_decode<float, 128>(a, plan, work, s, may_split);
+    // The split that finishes last merges its sequence's partials (a counter
+    // per (sequence, KV head) in the control region), or a merge launch does.
+    // The merge at the end of a split costs three dependent memory round
+    // trips (the partial's write-through, the count, the other partials):
+    // cheaper than a merge launch only while the memory system is quiet,
+    // i.e. for calls of at most a quarter of the CUs' workgroups (the
+    // 4-sequence decode: 16.5 -> 14.5 us per call; the 16-sequence step
+    // and 16 x 29600 were 3 us slower with it).
+    // (Switch value 2 merges by the last split in calls of every size.)
+    const int fused = g_decode_fused.load(std::memory_order_relaxed);
+    const int64_t wgs = (work.count > 0 ? work.count : items) * (kv_heads / plan.heads);
+    a.merge_last = may_split && have_ws && fused != 0 && batch * kv_heads <= kCtlPairs &&
+                   (fused == 2 || wgs <= device_cus() / 4);
+    const bool merge = may_split && !a.merge_last;
+    g_decode_path = a.merge_last ? NIE_DECODE_PATH_ONE_PASS_MERGED : NIE_DECODE_PATH_ONE_PASS;
+    if (dtype == NIE_DTYPE_BF16) {
+      if (head_dim == 64) launch_decode<bf16_t, 64>(a, plan, work, s, merge);
+      else launch_decode<bf16_t, 128>(a, plan, work, s, merge);
+    } else {
+      if (head_dim == 64) launch_decode<float, 64>(a, plan, work, s, merge);
+      else launch_decode<float, 128>(a, plan, work, s, merge);
+    }
   }
   return launched("paged_decode");
 }

@@ -337,19 +337,26 @@ def attention_rounding() -> str:
 
 
 #: Paths of a decode call (nie_decode_last_path).
-DECODE_PATHS = {0: "none", 1: "one_pass", 2: "passes", 3: "fused", 4: "generic"}
+DECODE_PATHS = {0: "none", 1: "one_pass", 2: "passes", 3: "fused", 4: "generic", 5: "one_pass_merged"}
 
 
-def set_decode_fused(on: bool) -> None:
+def set_decode_fused(on: bool | int) -> None:
     """Whether reference-rounding bf16 decode calls whose shape allows it run
     as one kernel (each split keeps its scores on chip and the splits exchange
-    only their (max, sum) pairs) instead of the scores and P.V passes; the
-    outputs are bit-identical either way.  On by default; process-wide."""
-    _check(load_library().nie_set_decode_fused(1 if on else 0), "nie_set_decode_fused")
+    only their (max, sum) pairs) instead of the scores and P.V passes, and
+    whether small one-pass decode calls that split their keys merge the
+    splits inside the decode kernel (the last split of each (sequence, KV
+    head) merges) instead of a merge launch; the outputs are bit-identical
+    either way.  On by default; process-wide.  2: as on, and the one-pass
+    merge by the last split in calls of every size."""
+    value = int(on) if not isinstance(on, bool) else (1 if on else 0)
+    _check(load_library().nie_set_decode_fused(value), "nie_set_decode_fused")
 
 
-def decode_fused() -> bool:
-    return bool(load_library().nie_decode_fused())
+def decode_fused() -> int:
+    """The switch's value: 0 off, 1 on (the default), 2 on with every
+    one-pass call merged by its last split."""
+    return int(load_library().nie_decode_fused())
 
 
 def set_decode_fused_spin(polls: int) -> None:

@@ -93,6 +93,8 @@ def _workload(base: str):
     if base == "many_short":  # 100 rows, most of them one split
         rng = np.random.default_rng(26)
         return workloads.ragged([int(x) for x in rng.integers(0, 300, 100)], [1] * 100, seed=26, pool_factor=1.3)
+    if base == "few_long":  # one sequence of 39 splits at the smallest split length, in a small call
+        return workloads.ragged([2490, 20, 100], [1] * 3, seed=28, pool_factor=1.3)
     if base == "gqa16":
         return workloads.ragged([1500, 40, 777], [1] * 3, seed=22, pool_factor=1.5, q_heads=16, kv_heads=1)
     if base == "d128":
@@ -215,6 +217,103 @@ def test_fused_decode_back_to_back_calls():
             single.append(call(p, host))
             torch.cuda.synchronize()
             assert _native.decode_last_path() == "fused"
+        outs = [call(prepared[i % len(prepared)], host) for i in range(24)]
+        torch.cuda.synchronize()
+        for i, got in enumerate(outs):
+            assert _same_bits(got, single[i % len(prepared)]), i
+        assert _control_regions_zero()
+
+
+# --- the one-pass rounding: split partials merged by the last split -------
+
+# small calls take the merge by the last split by default; the others only
+# with the switch at 2 (forced), which these tests use to run the merge over
+# many splits (several batches of 32 at head_dim 64)
+MERGED_SMALL = ["small_host"]
+MERGED_FORCED = ["small", "few_long", "few_long_host", "lognormal", "lognormal_host", "long_host", "many_short", "group2", "gqa16", "d128", "bs8", "bs32"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("case", MERGED_SMALL + MERGED_FORCED)
+@pytest.mark.parametrize("append", ["none", "rope"])
+def test_one_pass_merge_by_last_split_matches_merge_launch(case, append, dtype):
+    """One-pass decode (fp32, and bf16 with the one-pass rounding): the
+    merge of split partials by the split that finishes last, inside the
+    decode kernel, equals the merge launch bit for bit (outputs and cache
+    writes), within the oracle's bar, control regions zero."""
+    _log(f"one-pass merged by the last split: {case} {append} {dtype}")
+    _native.set_attention_rounding("fast")
+    if case in MERGED_FORCED:
+        _native.set_decode_fused(2)
+    host_plan = case.endswith("_host")
+    wl = _workload(case[: -len("_host")] if host_plan else case)
+    kc, vc = wl.pool(dtype)
+    q, k_new, v_new = wl.new_tokens(dtype)
+    tables = torch.from_numpy(wl.table_array()).to(DEV)
+    lens = torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)
+    host = list(wl.seq_lens) if host_plan else None
+    rope_tables = None
+    if append == "rope":
+        from nano_infer_engine.layers.rope import RopeScale
+
+        rope_tables = RopeScale(wl.head_dim).tables(DEV, dtype, max(wl.seq_lens))
+    dq = q.to(DEV)
+
+    def run():
+        k, v = kc.to(DEV), vc.to(DEV)
+        kw = {}
+        if append != "none":
+            kw = dict(new_kv=(k_new.to(DEV), v_new.to(DEV)), rope_tables=rope_tables)
+        out = _native.paged_decode(dq, k, v, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens),
+                                   wl.head_dim**-0.5, seq_lens_host=host, **kw)
+        return out, k, v
+
+    fused = run()
+    torch.cuda.synchronize()
+    p1 = _native.decode_last_path()
+    _native.set_decode_fused(False)
+    passes = run()
+    torch.cuda.synchronize()
+    p2 = _native.decode_last_path()
+    (o1, k1, v1), (o2, k2, v2) = fused, passes
+    _log(f"  paths: {p1} / {p2}")
+    assert p1 == "one_pass_merged" and p2 == "one_pass"
+    assert _same_bits(o1, o2), "merge by the last split differs from the merge launch"
+    assert _same_bits(k1, k2) and _same_bits(v1, v2)
+    assert _control_regions_zero()
+    if append == "none":
+        err = (o1.cpu().float() - _decode_oracle(wl, kc, vc, q).float()).abs().max().item()
+        _log(f"  max_abs_err={err:.3e}")
+        assert err <= (2e-2 if dtype == torch.bfloat16 else 1e-4)
+
+
+def test_one_pass_merge_by_last_split_back_to_back():
+    """Many one-pass calls on one stream with no host synchronisation, long
+    and short batches alternating (the merge by the last split forced on
+    all of them): each equals its single-call result bit for bit, and the
+    counters end zero."""
+    _log("one-pass merged back to back")
+    _native.set_attention_rounding("fast")
+    _native.set_decode_fused(2)
+    cases = [workloads.decode_ragged(seed=s) for s in (2, 4)] + [workloads.decode_small()]
+    prepared = []
+    for wl in cases:
+        kc, vc = wl.pool(torch.bfloat16)
+        q, _, _ = wl.new_tokens(torch.bfloat16)
+        prepared.append((wl, kc.to(DEV), vc.to(DEV), q.to(DEV), torch.from_numpy(wl.table_array()).to(DEV),
+                         torch.tensor(wl.seq_lens, dtype=torch.int32, device=DEV)))
+
+    def call(p, host):
+        wl, dk, dv, dq, tables, lens = p
+        return _native.paged_decode(dq, dk, dv, 0, tables, lens, max(wl.seq_lens), sum(wl.seq_lens),
+                                    wl.head_dim**-0.5, seq_lens_host=list(wl.seq_lens) if host else None)
+
+    for host in (True, False):
+        single = []
+        for p in prepared:
+            single.append(call(p, host))
+            torch.cuda.synchronize()
+            assert _native.decode_last_path() == "one_pass_merged"
         outs = [call(prepared[i % len(prepared)], host) for i in range(24)]
         torch.cuda.synchronize()
         for i, got in enumerate(outs):
