@@ -357,6 +357,51 @@ struct TableCache {
   }
 };
 
+// kWindows consecutive windows of kTableWindow block-table entries, loaded
+// together (lane i of register r holds entry base + 64r + i), for a wave
+// whose lookups only move forward: the front window serves the lookups, and
+// when one passes it the queued windows move up a place (register moves, no
+// load).  A prefill piece of up to kWindows x kTableWindow blocks so keeps
+// its table in registers with no load inside its DMA loop, whose waits count
+// the loop's outstanding K/V loads exactly.  (The moves sit behind uniform
+// branches in that loop, which cost the short pieces of a causal prompt
+// about 6%, so pieces that fit one window run the kWindows = 1 kernel,
+// which has neither.)
+template <int kWindows>
+struct TableWindows {
+  int base;                    // first logical block of the front window (wave-uniform)
+  int entries[2 * kWindows];   // clamped to the row's last entry past its end
+
+  // Only the registers that blocks [first, first + count) reach are loaded
+  // (count wave-uniform; the others are never looked up).
+  __device__ __forceinline__ void load(const int32_t* table, int table_len, int first, int count) {
+    base = __builtin_amdgcn_readfirstlane(first);
+    count = __builtin_amdgcn_readfirstlane(count);
+#pragma unroll
+    for (int r = 0; r < 2 * kWindows; ++r) {
+      if (r < 2 || r * kWave < count) entries[r] = table[min(base + r * kWave + lane_id(), table_len - 1)];
+    }
+  }
+  // Physical block of logical block `lb` (wave-uniform; lb never below an
+  // earlier lookup's, and below the first block + kWindows x kTableWindow).
+  __device__ __forceinline__ int lookup_forward(int lb) {
+    lb = __builtin_amdgcn_readfirstlane(lb);
+#pragma unroll
+    for (int w = 1; w < kWindows; ++w) {
+      if (lb - base >= kTableWindow) {  // uniform, once per window
+#pragma unroll
+        for (int r = 0; r + 2 < 2 * kWindows; ++r) entries[r] = entries[r + 2];
+        base += kTableWindow;
+      }
+    }
+    int idx = lb - base;
+    idx = idx < 0 ? 0 : (idx >= kTableWindow ? kTableWindow - 1 : idx);
+    const int lo = __builtin_amdgcn_readlane(entries[0], idx & (kWave - 1));
+    const int hi = __builtin_amdgcn_readlane(entries[1], idx & (kWave - 1));
+    return idx < kWave ? lo : hi;
+  }
+};
+
 // Addressing of the 16 keys of one tile (tiles start at multiples of 16).
 // kUniform: block_size is a power of two >= 16, so the whole tile lies in one
 // physical block: one wave-uniform lookup (through a TableCache) serves all
@@ -3784,6 +3829,10 @@ __global__ __launch_bounds__(256) void rope_kv_append_generic_kernel(RopeAppendA
 // Varlen prefill
 // ---------------------------------------------------------------------------
 constexpr int kPrefillWaves = 4;
+// Block-table windows (kTableWindow entries each, two VGPRs per window) a
+// prefill wave holds: a piece covers up to 640 key tiles (10240 keys at
+// block size 16), so a chunk on an 8192-token context is one piece.
+constexpr int kPrefillTableWindows = 5;
 constexpr int kPrefillLdsBudget = 128 * 1024;
 
 // Query rows per wave: kRowBlocks MFMA row blocks of 16 rows, each block
@@ -4134,7 +4183,9 @@ constexpr int kPrefillOnline = 0;
 constexpr int kPrefillStats = 1;
 constexpr int kPrefillExact = 2;
 
-template <typename T, int D, bool kUniform, int kRowBlocks, bool kPow2Scale, int kMode>
+// kWindows: block-table windows a wave holds (see TableWindows): 1, or
+// kPrefillTableWindows for plans with pieces longer than one window.
+template <typename T, int D, bool kUniform, int kRowBlocks, bool kPow2Scale, int kMode, int kWindows>
 __global__ __launch_bounds__(kPrefillWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
 void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   using F = Frag<T, D>;
@@ -4239,8 +4290,11 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
 
   // the block-table window first: the first K/V fetch waits for it, the Q
   // rows only the first scores
-  TableCache tc;
-  if constexpr (kUniform) tc.load(table, tlen, (tile_begin * kTileKeys) >> a.geom.bs_shift);
+  TableWindows<kWindows> tc;
+  if constexpr (kUniform) {
+    const int first_block = (tile_begin * kTileKeys) >> a.geom.bs_shift;
+    tc.load(table, tlen, first_block, (last >> a.geom.bs_shift) - first_block + 1);
+  }
 
   // Rows: block nb of this wave = tokens t0 + (wave*kRowBlocks + nb)*(16/G) + row/G, head row%G.
   const int tpb = 16 / a.group;  // tokens per row block
@@ -4292,7 +4346,7 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
       // the tile lies in one block: one wave-uniform table lookup, then the
       // lane's row (clamped to the item's last key) and chunk
       const int lb = min(tkey0 >> a.geom.bs_shift, tlen - 1);
-      int phys = tc.template lookup<false>(table, tlen, lb);
+      int phys = tc.lookup_forward(lb);
       phys = phys < 0 ? 0 : (phys >= a.geom.num_blocks ? a.geom.num_blocks - 1 : phys);
       const int64_t tile = a.geom.layer_offset +
                            ((int64_t)phys * a.geom.block_size + (tkey0 & (a.geom.block_size - 1))) *
@@ -5021,8 +5075,9 @@ __global__ __launch_bounds__(kPrefillMergeWaves* kWave) void prefill_merge_kerne
 // bound on the total work gives about kPrefillTargetItems workgroups.
 constexpr int64_t kPrefillTargetItems = 2048;
 constexpr int64_t kPrefillMinTilesPerSplit = 8;
-constexpr int64_t kPrefillMaxTilesPerSplit = kTableWindow;  // a piece's blocks fit the block-table window
-static_assert(kPrefillMaxTilesPerSplit <= kTableWindow, "a piece's lookups stay in its block-table window");
+// A piece of L >= 2 tiles spans at most L blocks of 16 keys or more, so its
+// lookups stay in the kernel's block-table windows.
+constexpr int64_t kPrefillMaxTilesPerSplit = kTableWindow * kPrefillTableWindows;
 
 // A query tile of a host-planned prefill call (tiles in request order) and
 // its pieces' workspace slots [first, first + pieces).
@@ -5049,6 +5104,7 @@ struct PrefillPlan {
   int64_t rows = 0;    // rows per item
   bool split = false;  // some query tile is split over several items
   int64_t max_split = 0;  // items of the most-split query tile (a bound without host metadata)
+  bool long_pieces = false;  // some piece spans more than one block-table window (kTableWindow tiles)
   // host metadata: the query tiles and the items in dispatch order
   std::vector<PrefillTile> tiles;
   std::vector<PrefillPiece> order;
@@ -5116,7 +5172,7 @@ bool plan_balanced(PrefillPlan& p, int64_t kv_heads) {
       const int64_t size = steps / n[i] + (j < steps % n[i] ? 1 : 0);
       const int64_t begin = done * kPrefillStepTiles;
       const int64_t len = std::min(size * kPrefillStepTiles, t.ktiles - begin);
-      if (begin > 0xffff || len > 255) return false;
+      if (begin > 0xffff || len > kPrefillMaxTilesPerSplit) return false;
       pieces.push_back(PrefillPiece{(int32_t)i, (int32_t)j, (int32_t)begin, (int32_t)len});
       done += size;
     }
@@ -5133,6 +5189,7 @@ bool plan_balanced(PrefillPlan& p, int64_t kv_heads) {
   p.order.insert(p.order.end(), by_size.begin() + big, by_size.end());
   p.items = (int64_t)pieces.size();
   p.split = splits > 0;
+  for (const PrefillPiece& q : pieces) p.long_pieces |= q.len > kTableWindow;
   return true;
 }
 
@@ -5184,6 +5241,7 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
       }
     }
     p.items = first;
+    for (const PrefillPiece& q : p.order) p.long_pieces |= q.len > kTableWindow;
     return p;
   }
   const int64_t qtiles = total_tokens / tpt + num_seqs;  // >= sum_r ceil(len_r / tpt)
@@ -5194,6 +5252,7 @@ PrefillPlan plan_prefill(int64_t group, int64_t kv_heads, int64_t num_seqs, int6
   p.qtiles = qtiles;
   p.split = ktiles > p.tps;
   p.max_split = cdiv(ktiles, p.tps);
+  p.long_pieces = std::min(p.tps, ktiles) > kTableWindow;
   return p;
 }
 
@@ -5608,12 +5667,14 @@ void launch_decode_fused(const DecodeArgs& a, const DecodePlan& p, const DecodeI
 template <typename T, int D, int NB, bool P2, int M>
 void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc, hipStream_t stream) {
   const dim3 grid((unsigned)(p.items * a.geom.kv_heads));
-  if (uniform_tiles(a.geom)) {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2, M>), grid, dim3(kPrefillWaves * kWave), 0, stream,
+  const dim3 block(kPrefillWaves * kWave);
+  if (uniform_tiles(a.geom) && p.long_pieces) {
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2, M, kPrefillTableWindows>), grid, block, 0, stream,
                        a, sc);
+  } else if (uniform_tiles(a.geom)) {
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2, M, 1>), grid, block, 0, stream, a, sc);
   } else {
-    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2, M>), grid, dim3(kPrefillWaves * kWave), 0, stream,
-                       a, sc);
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D, false, NB, P2, M, 1>), grid, block, 0, stream, a, sc);
   }
 }
 
