@@ -2048,8 +2048,11 @@ constexpr int decode_stages() {
 }
 
 // One workgroup = one (sequence, key split, head group); wave w handles KV
-// head group*kHeads + w and its GQA query heads.
-template <typename T, int D, bool kUniform, int kHeads>
+// head group*kHeads + w and its GQA query heads.  kMergeLast: the build for
+// calls whose splits merge inside the kernel (DecodeArgs::merge_last); its
+// merge needs more VGPRs than the loop, so the other calls run a build
+// without it.
+template <typename T, int D, bool kUniform, int kHeads, bool kMergeLast = false>
 __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs a, DecodeItems items) {
   using F = Frag<T, D>;
   using GT = GroupTile<T, D, kHeads>;
@@ -2366,7 +2369,7 @@ __global__ __launch_bounds__(kHeads* kWave) void paged_decode_kernel(DecodeArgs 
   // for the merge.  The bound keeps inconsistent length hints from writing
   // outside the workspace.
   const int64_t item = first_item + split;
-  if (a.merge_last) {
+  if constexpr (kMergeLast) {
     // Through to memory (agent scope), then counted on the (sequence, KV
     // head) counter; the wave that counts the last split merges every
     // split's partial of its query heads, in decode_merge_kernel's order,
@@ -5449,7 +5452,11 @@ template <typename T, int D, bool U, int H, int P>
 void launch_decode_h(const DecodeArgs& a, const DecodeItems& items, int64_t grid_items, hipStream_t stream) {
   const dim3 grid((unsigned)grid_items, (unsigned)(a.geom.kv_heads / H));
   if constexpr (P == 0) {
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a, items);
+    if (a.merge_last) {
+      hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H, true>), grid, dim3(H * kWave), 0, stream, a, items);
+    } else {
+      hipLaunchKernelGGL((paged_decode_kernel<T, D, U, H>), grid, dim3(H * kWave), 0, stream, a, items);
+    }
   } else {
     hipLaunchKernelGGL((decode_pass_kernel<T, D, U, H, P>), grid, dim3(H * kWave), 0, stream, a, items);
   }
