@@ -4197,7 +4197,9 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   constexpr bool kFetchV = kMode != kPrefillStats;
   constexpr int kSub = kPrefillStepTiles;
   constexpr int kStages = prefill_stages<T, D>();
-  constexpr int kStageBytes = prefill_stage_bytes<T, D>();
+  // the stats pass stages K only: half the LDS, so more of its workgroups
+  // fit a CU
+  constexpr int kStageBytes = kFetchV ? prefill_stage_bytes<T, D>() : prefill_stage_bytes<T, D>() / 2;
   // DMA ops of one step: per tile, K ops then V ops (the stats pass: K only)
   constexpr int kStepOps = kSub * (kFetchV ? 2 : 1) * GT::kOps;
   static_assert(kStepOps % kPrefillWaves == 0, "step DMA ops must spread evenly over the waves");
