@@ -1034,7 +1034,7 @@ struct DecodeItems {
 // kDecodeMaxTilesPerSplit]) whose items fit `slots` workgroups in one round.
 // With `tiles` = sum over the sequences of ceil(len / 16), a call then has
 // at most tiles / tps + batch <= slots - 1 items unless the upper clamp binds.
-constexpr int64_t kDecodeMinTilesPerSplit = 4;
+constexpr int64_t kDecodeMinTilesPerSplit = 2;
 constexpr int64_t kDecodeMaxTilesPerSplit = 2 * kWave;  // the per-split block-table window
 
 __host__ __device__ inline int64_t decode_device_tps(int64_t tiles, int64_t batch, int64_t slots) {

@@ -755,7 +755,7 @@ def test_library_decode_plan_table():
     lens = [17, 64, 129, 500, 3000]
     count, tps, items, seq_len, first = plan(lens)
     splits = [-(-(-(-n // 16)) // tps) for n in lens]
-    assert tps >= 4 and count == sum(splits) and seq_len == lens
+    assert tps >= 2 and count == sum(splits) and seq_len == lens
     assert first == [sum(splits[:b]) for b in range(len(lens))]
     assert items == [(b, s) for b in range(len(lens)) for s in range(splits[b])]
     assert _native.decode_plan_fits(torch.bfloat16, 32, 8, 64, 16, lens)
