@@ -3908,8 +3908,12 @@ struct SplitWalk {
   }
 };
 
-// Items of query tiles [0, count) of a request.
+// Items of query tiles [0, count) of a request.  When the request's last
+// query tile (which sees the most keys) fits one piece, every tile is one
+// item and no walk is needed (a 2048-token prompt has 64 query tiles, and
+// the walk over them cost each workgroup about a third of its VALU work).
 __device__ __forceinline__ int prefill_items_upto(int q_len, int ctx, int tpt, int S, int count) {
+  if ((ctx + q_len + kTileKeys - 1) / kTileKeys <= S) return count;
   SplitWalk w;
   w.start(q_len, ctx, tpt, S);
   int n = 0;
@@ -4250,16 +4254,22 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     // launch (indices past the call's items exit here, first)
     const PrefillItem pit = prefill_locate(a, (int64_t)(a.grid_items - 1 - wg_item));
     if (pit.r < 0) return;  // uniform over the workgroup
-    // (query tile, split) of this item; the loop is wave-uniform
-    int qt = 0, split = (int)pit.local;
-    SplitWalk w;
-    w.start(pit.q_len, pit.ctx, tpt, S);
-    while (split >= w.nsplit && w.nsplit > 0) {  // nsplit >= 1 for a request with query tokens
-      split -= w.nsplit;
-      ++qt;
-      w.next();
+    // (query tile, split) of this item; the loop is wave-uniform (none when
+    // every query tile of the request is one piece)
+    int qt = 0, split = (int)pit.local, nsplit = 1;
+    if ((pit.ctx + pit.q_len + kTileKeys - 1) / kTileKeys <= S) {
+      qt = split;
+      split = 0;
+    } else {
+      SplitWalk w;
+      w.start(pit.q_len, pit.ctx, tpt, S);
+      while (split >= w.nsplit && w.nsplit > 0) {  // nsplit >= 1 for a request with query tokens
+        split -= w.nsplit;
+        ++qt;
+        w.next();
+      }
+      nsplit = w.nsplit;
     }
-    const int nsplit = w.nsplit;
     r = pit.r;
     q_begin = pit.q_begin;
     q_len = pit.q_len;
