@@ -383,16 +383,14 @@ struct TableWindows {
     }
   }
   // Physical block of logical block `lb` (wave-uniform; lb never below an
-  // earlier lookup's, and below the first block + kWindows x kTableWindow).
+  // earlier lookup's, at most kTableWindow past it, and below the first
+  // block + kWindows x kTableWindow).
   __device__ __forceinline__ int lookup_forward(int lb) {
     lb = __builtin_amdgcn_readfirstlane(lb);
+    if (kWindows > 1 && lb - base >= kTableWindow) {  // uniform, once per window
 #pragma unroll
-    for (int w = 1; w < kWindows; ++w) {
-      if (lb - base >= kTableWindow) {  // uniform, once per window
-#pragma unroll
-        for (int r = 0; r + 2 < 2 * kWindows; ++r) entries[r] = entries[r + 2];
-        base += kTableWindow;
-      }
+      for (int r = 0; r + 2 < 2 * kWindows; ++r) entries[r] = entries[r + 2];
+      base += kTableWindow;
     }
     int idx = lb - base;
     idx = idx < 0 ? 0 : (idx >= kTableWindow ? kTableWindow - 1 : idx);
