@@ -3865,6 +3865,12 @@ struct PrefillArgs {
   int64_t ws_items;  // item slots in the workspace
   int32_t grid_items;   // prefill launch: items per KV head (1-D grid of grid_items * kv_heads)
   int32_t merge_tiles;  // merge launch: query tiles per KV head
+  // The reference rounding's stats pass cuts each piece's keys into
+  // stats_parts parts (1 or 2, workgroups of their own), each with its
+  // (max, sum) slot: slot (first item of the tile + piece) * stats_parts +
+  // part, of ws_ml_slots; the exact pass combines a tile's parts in order.
+  int32_t stats_parts = 1;
+  int64_t ws_ml_slots = 0;
 };
 
 // Key tiles visible to query tile qt of request r (its last row's position + 1).
@@ -4218,9 +4224,14 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   const int S = a.tiles_per_split;
   // (item, KV head) of this workgroup, head-major over the XCDs; 32-bit
   // and scalar, so the schedule below is read with scalar loads
-  const uint32_t logical = xcd_logical32(blockIdx.x, (uint32_t)a.grid_items * (uint32_t)a.geom.kv_heads);
-  const int h = __builtin_amdgcn_readfirstlane((int)(logical / (uint32_t)a.grid_items));
-  const int wg_item = __builtin_amdgcn_readfirstlane((int)(logical - (uint32_t)h * (uint32_t)a.grid_items));
+  // (the stats pass: parts of items, consecutive)
+  const int parts = kMode == kPrefillStats ? __builtin_amdgcn_readfirstlane(a.stats_parts) : 1;
+  const uint32_t grid_parts = (uint32_t)a.grid_items * (uint32_t)parts;
+  const uint32_t logical = xcd_logical32(blockIdx.x, grid_parts * (uint32_t)a.geom.kv_heads);
+  const int h = __builtin_amdgcn_readfirstlane((int)(logical / grid_parts));
+  const int wg_part = __builtin_amdgcn_readfirstlane((int)(logical - (uint32_t)h * grid_parts));
+  const int wg_item = parts == 1 ? wg_part : wg_part >> 1;
+  const int part = wg_part - wg_item * parts;
 
   // This workgroup's item: request r, query tile from token t0, key tiles
   // [tile_begin, tile_cap), and the workspace slot of its partial (-1: the
@@ -4293,6 +4304,19 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
   tile_cap = __builtin_amdgcn_readfirstlane(tile_cap);
   const int t_end = min(t0 + tpt, q_len);
   const int key_end = ctx + t_end;
+  if constexpr (kMode == kPrefillStats) {
+    if (parts == 2) {
+      // the first part takes the first half of the piece's steps (rounded
+      // up), the second the rest (none for a one-step piece)
+      const int steps = (min(tile_cap, (key_end + kTileKeys - 1) / kTileKeys) - tile_begin + kSub - 1) / kSub;
+      const int first_steps = (steps + 1) / 2;
+      if (part == 0) {
+        tile_cap = tile_begin + first_steps * kSub;
+      } else {
+        tile_begin += first_steps * kSub;
+      }
+    }
+  }
   const int tile_end = min(tile_cap, (key_end + kTileKeys - 1) / kTileKeys);
   const int last = min(tile_end * kTileKeys, key_end) - 1;  // last key this item reads
   const int last_key0 = (last / kTileKeys) * kTileKeys;     // first key of the tile holding it
@@ -4437,15 +4461,18 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     for (int nb = 0; nb < kRowBlocks; ++nb) {
       const int64_t rowidx = (wave * kRowBlocks + nb) * 16 + row;
       float m = kNegInf, l = 0.f;
-      if (a.ws_ml != nullptr && tile_first + npieces <= a.ws_items) {
-        for (int64_t p0 = 0; p0 < npieces; p0 += 4 * kB) {
+      // the stats pass's parts of the tile's pieces, in order
+      const int64_t sparts = a.stats_parts;
+      const int64_t nst = npieces * sparts, st0 = tile_first * sparts;
+      if (a.ws_ml != nullptr && st0 + nst <= a.ws_ml_slots) {
+        for (int64_t p0 = 0; p0 < nst; p0 += 4 * kB) {
           float2 v[kB];
 #pragma unroll
           for (int jb = 0; jb < kB; ++jb) {
             const int64_t pc = p0 + 4 * jb + g;
-            v[jb] = pc < npieces ? *reinterpret_cast<const float2*>(
-                                       a.ws_ml + (((tile_first + pc) * a.geom.kv_heads + h) * kRows + rowidx) * 2)
-                                 : make_float2(kNegInf, 0.f);
+            v[jb] = pc < nst ? *reinterpret_cast<const float2*>(
+                                   a.ws_ml + (((st0 + pc) * a.geom.kv_heads + h) * kRows + rowidx) * 2)
+                             : make_float2(kNegInf, 0.f);
           }
 #pragma unroll
           for (int jb = 0; jb < kB; ++jb) {
@@ -4546,13 +4573,13 @@ void varlen_prefill_kernel(PrefillArgs a, PrefillSchedule sc) {
     // in scaled units; a + b == b + a, so every lane of a row forms the
     // same sum)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    const int64_t stats_slot = tile_first + piece;
+    const int64_t stats_slot = (tile_first + piece) * parts + part;
 #pragma unroll
     for (int nb = 0; nb < kRowBlocks; ++nb) {
       double tl = run_l[nb] + __shfl_xor(run_l[nb], 16);
       tl = tl + __shfl_xor(tl, 32);
       const int64_t rowidx = (wave * kRowBlocks + nb) * 16 + row;
-      if (g == 0 && a.ws_ml != nullptr && stats_slot < a.ws_items) {
+      if (g == 0 && a.ws_ml != nullptr && stats_slot < a.ws_ml_slots) {
         const float m = run_m[nb] == kNegInf ? kNegInf : run_m[nb] * score_f;
         *reinterpret_cast<float2*>(a.ws_ml + ((stats_slot * a.geom.kv_heads + h) * kRows + rowidx) * 2) =
             make_float2(m, (float)tl);
@@ -5683,7 +5710,7 @@ void launch_decode_fused(const DecodeArgs& a, const DecodePlan& p, const DecodeI
 
 template <typename T, int D, int NB, bool P2, int M>
 void launch_prefill_kernel(const PrefillArgs& a, const PrefillPlan& p, const PrefillSchedule& sc, hipStream_t stream) {
-  const dim3 grid((unsigned)(p.items * a.geom.kv_heads));
+  const dim3 grid((unsigned)(p.items * a.geom.kv_heads * (M == kPrefillStats ? a.stats_parts : 1)));
   const dim3 block(kPrefillWaves * kWave);
   if (uniform_tiles(a.geom) && p.long_pieces) {
     hipLaunchKernelGGL((varlen_prefill_kernel<T, D, true, NB, P2, M, kPrefillTableWindows>), grid, block, 0, stream,
@@ -6675,7 +6702,7 @@ NIE_API int64_t nie_varlen_prefill_workspace_bytes(int64_t num_seqs, int64_t tot
   // slots are needed (the query has no dtype: with the reference rounding it
   // sizes for bf16, which an fp32 call can use too)
   if (!p.split && g_rounding.load(std::memory_order_relaxed) != NIE_ROUND_REFERENCE) return 0;
-  return kCtlBytes + p.items * kv_heads * p.rows * (head_dim + 2) * (int64_t)sizeof(float);
+  return kCtlBytes + p.items * kv_heads * p.rows * (head_dim + 4) * (int64_t)sizeof(float);
 }
 
 NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int64_t q_stride_h,
@@ -6758,7 +6785,9 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   const bool two = two_pass(dtype);
   // the workspace: the control region (which prefill leaves alone), then
   // the partials
-  const int64_t need = kCtlBytes + plan.items * kv_heads * plan.rows * (head_dim + 2) * (int64_t)sizeof(float);
+  // the control region, the partials, then two (max, sum) slots per item
+  // and row (the stats pass's parts)
+  const int64_t need = kCtlBytes + plan.items * kv_heads * plan.rows * (head_dim + 4) * (int64_t)sizeof(float);
   if ((may_split || two) && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace % 16))) {
     return fail(NIE_EINVAL, "workspace too small: need %lld bytes, got %lld", (long long)need,
                 (long long)workspace_bytes);
@@ -6788,6 +6817,10 @@ NIE_API int nie_varlen_prefill(int dtype, const void* q, int64_t q_stride_t, int
   a.ws_o = have_ws ? reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) + kCtlBytes) : nullptr;
   a.ws_ml = have_ws ? a.ws_o + plan.items * kv_heads * plan.rows * head_dim : nullptr;
   a.ws_items = have_ws ? plan.items : 0;
+  a.ws_ml_slots = have_ws ? 2 * plan.items : 0;
+  // parts of two in the stats pass when its workgroups would otherwise
+  // leave room on the CUs (it holds four per CU, the other passes two)
+  a.stats_parts = two && plan.items * kv_heads <= 2 * device_cus() ? 2 : 1;
   PrefillMergeJobs jobs;
   jobs.count = 0;
   if (may_split) fill_merge_jobs(plan, num_seqs, host ? host_cu_seqlens : nullptr, host ? host_context_lens : nullptr, &jobs);

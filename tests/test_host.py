@@ -430,8 +430,9 @@ def test_library_decode_plan_from_host_lengths():
 def test_library_prefill_plan_from_host_lengths():
     """With host copies of the lengths the prefill plan uses the exact work:
     split partials exist only when some query tile's keys are split, are a
-    whole number of (items x kv_heads x 128 rows x (64 + 2) floats), and
-    lengths that do not fit the call's sizes are rejected."""
+    whole number of (items x kv_heads x 128 rows x (64 + 4) floats: the
+    partial O rows and two (max, sum) slots per row), and lengths that do
+    not fit the call's sizes are rejected."""
     lib = _native.load_library()
 
     def query(cu, ctx, total, max_q, max_s):
@@ -444,7 +445,7 @@ def test_library_prefill_plan_from_host_lengths():
     # one-pass rounding needs no workspace; the reference rounding keeps every item's (max, sum) slots
     # in the same layout (16 items here: 4 query tiles of 32 tokens per chunk), after the control region
     ctl = _native.workspace_control_bytes()
-    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == ctl + 16 * 8 * 128 * 66 * 4
+    assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == ctl + 16 * 8 * 128 * 68 * 4
     _native.set_attention_rounding("fast")
     try:
         assert query([0, 128, 256, 384, 512], [0, 0, 0, 0], 512, 128, 128) == 0
@@ -452,7 +453,7 @@ def test_library_prefill_plan_from_host_lengths():
         _native.set_attention_rounding("reference")
     # the mixed step's chunks (contexts 0, 384, 1024, 4000): the long context is split
     mixed = query([0, 128, 256, 384, 512], [0, 384, 1024, 4000], 512, 128, 4128) - ctl
-    assert mixed > 0 and mixed % (8 * 128 * 66 * 4) == 0
+    assert mixed > 0 and mixed % (8 * 128 * 68 * 4) == 0
     # lengths that do not match the sizes of the call
     assert query([0, 128, 256, 384, 500], [0, 384, 1024, 4000], 512, 128, 4128) == 0
     assert query([0, 128, 256, 384, 512], [0, 384, 1024, 4001], 512, 128, 4128) == 0
