@@ -363,10 +363,10 @@ struct TableCache {
 // when one passes it the queued windows move up a place (register moves, no
 // load).  A prefill piece of up to kWindows x kTableWindow blocks so keeps
 // its table in registers with no load inside its DMA loop, whose waits count
-// the loop's outstanding K/V loads exactly.  (The moves sit behind uniform
-// branches in that loop, which cost the short pieces of a causal prompt
-// about 6%, so pieces that fit one window run the kWindows = 1 kernel,
-// which has neither.)
+// the loop's outstanding K/V loads exactly.  (The moves sit behind a
+// uniform branch in that loop, which cost the short pieces of a causal
+// prompt about 6% when every lookup checked every window, so pieces that
+// fit one window run the kWindows = 1 kernel, which has neither.)
 template <int kWindows>
 struct TableWindows {
   int base;                    // first logical block of the front window (wave-uniform)
@@ -383,8 +383,9 @@ struct TableWindows {
     }
   }
   // Physical block of logical block `lb` (wave-uniform; lb never below an
-  // earlier lookup's, at most kTableWindow past it, and below the first
-  // block + kWindows x kTableWindow).
+  // earlier lookup's, less than two windows past the front window's first
+  // block (a prefill wave's lookups advance a few blocks per step), and
+  // below the first block + kWindows x kTableWindow).
   __device__ __forceinline__ int lookup_forward(int lb) {
     lb = __builtin_amdgcn_readfirstlane(lb);
     if (kWindows > 1 && lb - base >= kTableWindow) {  // uniform, once per window
