@@ -1,10 +1,13 @@
 """The allocation-free decode step (nie_paged_decode_append_noalloc) against
 nie_paged_decode_append with a caller workspace, both called through the C ABI.
 
-The caches and outputs must be bit-identical.  Two calls in a row share the
+The caches and outputs must be bit-identical.  Calls in a row share the
 library's static scratch: the second, smaller call reads partials written
-over the first call's stale ones.  A call whose partials would not fit the
-scratch is rejected with NIE_EINVAL before anything is launched.
+over the first call's stale ones, and the third (4 short sequences, small
+enough that with the one-pass rounding of fp32 its splits merge inside the
+decode kernel) counts on the scratch's control region, which every call
+leaves zero.  A call whose partials would not fit the scratch is rejected
+with NIE_EINVAL before anything is launched.
 """
 
 from __future__ import annotations
@@ -97,7 +100,8 @@ def test_noalloc_matches_workspace_entry_point_twice(dtype, host_plan):
     # stale partials
     first = workloads.decode_ragged()
     second = workloads.ragged([40, 700, 1500, 3000, 5], [1] * 5, seed=21, pool_factor=1.5)
-    for name, wl in (("lognormal x16", first), ("ragged x5", second)):
+    third = workloads.decode_small()
+    for name, wl in (("lognormal x16", first), ("ragged x5", second), ("small x4", third)):
         _log(f"noalloc {name} {dtype} host_plan={host_plan}")
         (ka, va, oa), (kb, vb, ob) = _pair(lib, wl, dtype, host_plan)
         assert _same_bits(ka, kb) and _same_bits(va, vb), f"{name}: cache differs"
